@@ -1,0 +1,82 @@
+"""Build the gfx950 fitter library and CLI in-tree.
+
+    python -m cusr_amd.build [--jobs N]
+
+Outputs (next to the ctypes loader, like the reference's make targets,
+cusr/kernel/Makefile:77-81):
+    cusr_amd/kernel/libcusr_co_ad.so   C ABI of include/cusr_co.h
+    cusr_amd/kernel/batch_lm_ad        CLI with the reference's arguments/blobs
+Objects go to cusr_amd/_build/. Every call recompiles.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+REPO = ROOT.parent
+CSRC = ROOT / "csrc"
+BUILD = ROOT / "_build"
+KDIR = ROOT / "kernel"
+LIB = KDIR / "libcusr_co_ad.so"
+CLI = KDIR / "batch_lm_ad"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# -ffp-contract=off: fused multiply-adds only where fma() is written, so the
+# device arithmetic order is the one the CPU oracle reproduces.
+# -packed-fp32-ops off: no v_pk_*_f32 generated from float code.
+DEVICE_FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-ffp-contract=off",
+                "-fno-fast-math", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                f"-I{REPO / 'include'}", "-Wall", "-Wno-unused-function"]
+
+FIT_VARIANTS = [("double", 0, "launch_fit_f64_fwd"), ("double", 1, "launch_fit_f64_rev"),
+                ("float", 0, "launch_fit_f32_fwd"), ("float", 1, "launch_fit_f32_rev")]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in (r.stderr or "").splitlines()
+                    if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(map(str, cmd))}\n{err}")
+    return err
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    compiles = []
+    for rtype, ad, name in FIT_VARIANTS:
+        obj = BUILD / f"fit_{name}.o"
+        compiles.append([HIPCC, *DEVICE_FLAGS, "-x", "hip", f"-DCUSR_FIT_R={rtype}",
+                         f"-DCUSR_FIT_AD={ad}", f"-DCUSR_FIT_LAUNCH={name}", "-c",
+                         str(CSRC / "fit_kernels.hip"), "-o", str(obj)])
+    compiles.append([HIPCC, *DEVICE_FLAGS, "-x", "hip", "-c", str(CSRC / "co_lib.hip"),
+                     "-o", str(BUILD / "co_lib.o")])
+    compiles.append([HIPCC, *DEVICE_FLAGS, "-x", "hip", "-c", str(CSRC / "program.cpp"),
+                     "-o", str(BUILD / "program.o")])
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        for err in ex.map(_run, compiles):
+            if verbose and err.strip():
+                print(err, file=sys.stderr)
+    objs = [str(c[c.index("-o") + 1]) for c in compiles]
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs])
+    os.replace(tmp, LIB)
+    _run(["g++", "-O2", "-std=c++17", f"-I{REPO / 'include'}", "-o", str(CLI),
+          str(CSRC / "batch_lm_main.cpp"), f"-L{KDIR}", "-lcusr_co_ad",
+          "-Wl,-rpath,$ORIGIN"])
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("-v", "--verbose", action="store_true")
+    a = ap.parse_args()
+    print(build(a.jobs, a.verbose))

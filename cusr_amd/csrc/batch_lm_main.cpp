@@ -1,0 +1,181 @@
+// batch_lm_main.cpp -- command-line front end with the reference CLI contract
+// (cusr/kernel/batch_lm_ad.cu:196-551):
+//
+//   batch_lm_ad <pop.bin> [out_dir] [--max-iter N] [--quiet] [--rev] [--mixed]
+//
+// writes out_dir/{status.bin, c_final.bin, loss_init.bin, loss_final.bin}
+// (int32 / float32 blobs, batch_lm_ad.cu:526-536) and prints the completion
+// line the reference benchmark parses (cusr/benchmark/backends.py:745):
+//   [batch-lm] 总耗时 <seconds> 秒 (<trees/s> trees/s, M_prob=<M>)
+// Exit status: 0 ok, 1 load or device failure, 2 beyond device bounds.
+// --rev / --mixed select reverse AD / mixed precision (extensions).
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/cusr_co.h"
+
+namespace {
+
+struct Pop {
+    PopHeader h;
+    std::vector<int32_t> nt, ci;
+    std::vector<float> nv, c_init, xs, ym;
+    std::vector<TreeMeta> metas;
+};
+
+bool read_exact(FILE *f, void *dst, size_t bytes, const char *what) {
+    if (bytes == 0) return true;
+    if (fread(dst, 1, bytes, f) != bytes) {
+        fprintf(stderr, "load_pop_bin: short read on %s\n", what);
+        return false;
+    }
+    return true;
+}
+
+bool load_pop(const char *path, Pop &p) {
+    FILE *f = fopen(path, "rb");
+    if (!f) {
+        fprintf(stderr, "load_pop_bin: cannot open %s\n", path);
+        return false;
+    }
+    bool ok = read_exact(f, &p.h, sizeof(p.h), "header");
+    if (ok && p.h.magic != POP_MAGIC) {
+        fprintf(stderr, "load_pop_bin: bad magic 0x%08x\n", (unsigned)p.h.magic);
+        ok = false;
+    }
+    if (ok && p.h.version != POP_VERSION) {
+        fprintf(stderr, "load_pop_bin: version %d != %d\n", p.h.version, POP_VERSION);
+        ok = false;
+    }
+    if (ok && (p.h.M_prob < 0 || p.h.total_nodes < 0 || p.h.total_c < 0 || p.h.N < 0 ||
+               p.h.n_vars < 0)) {
+        fprintf(stderr, "load_pop_bin: negative size in header\n");
+        ok = false;
+    }
+    if (ok) {
+        const size_t T = p.h.total_nodes, M = p.h.M_prob, C = p.h.total_c;
+        const size_t N = p.h.N, D = p.h.n_vars;
+        p.nt.resize(T); p.nv.resize(T); p.ci.resize(T); p.metas.resize(M);
+        p.c_init.resize(C); p.xs.resize(N * D); p.ym.resize(M * N);
+        ok = read_exact(f, p.nt.data(), 4 * T, "nt") && read_exact(f, p.nv.data(), 4 * T, "nv") &&
+             read_exact(f, p.ci.data(), 4 * T, "ci") &&
+             read_exact(f, p.metas.data(), 16 * M, "metas") &&
+             read_exact(f, p.c_init.data(), 4 * C, "c_init") &&
+             read_exact(f, p.xs.data(), 4 * N * D, "xs") &&
+             read_exact(f, p.ym.data(), 4 * M * N, "ym");
+    }
+    fclose(f);
+    return ok;
+}
+
+bool write_blob(const std::string &path, const void *buf, size_t bytes) {
+    FILE *f = fopen(path.c_str(), "wb");
+    if (!f) {
+        fprintf(stderr, "cannot write %s\n", path.c_str());
+        return false;
+    }
+    bool ok = fwrite(buf, 1, bytes, f) == bytes;
+    fclose(f);
+    return ok;
+}
+
+double seconds() {
+    timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return t.tv_sec + t.tv_nsec * 1e-9;
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    if (argc < 2) {
+        fprintf(stderr, "usage: %s <pop.bin> [out_dir] [--max-iter N] [--quiet] [--rev] [--mixed]\n",
+                argv[0]);
+        return 1;
+    }
+    const double t0 = seconds();
+    const char *pop_path = argv[1];
+    std::string out_dir;
+    int max_iter = 50, quiet = 0, rev = 0, mixed = 0;
+    for (int i = 2; i < argc; i++) {
+        if (!strcmp(argv[i], "--max-iter") && i + 1 < argc) max_iter = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--quiet")) quiet = 1;
+        else if (!strcmp(argv[i], "--rev")) rev = 1;
+        else if (!strcmp(argv[i], "--mixed")) mixed = 1;
+        else if (argv[i][0] != '-') out_dir = argv[i];
+    }
+    if (out_dir.empty()) {
+        const char *slash = strrchr(pop_path, '/');
+        out_dir = slash ? std::string(pop_path, slash - pop_path) : std::string(".");
+    }
+    Pop p;
+    if (!load_pop(pop_path, p)) {
+        fprintf(stderr, "load failed.\n");
+        return 1;
+    }
+    const PopHeader &h = p.h;
+    if (!quiet)
+        printf("[batch-lm] loaded %s: M_prob=%d total_nodes=%d total_c=%d N=%d n_vars=%d "
+               "K_max=%d max_stack=%d\n",
+               pop_path, h.M_prob, h.total_nodes, h.total_c, h.N, h.n_vars, h.K_max,
+               h.max_stack);
+    const int rc0 = co_decode(&h, p.nt.data(), p.nv.data(), p.ci.data(), p.metas.data(), nullptr,
+                              nullptr, nullptr, nullptr);
+    if (rc0 == CO_ERR_BOUNDS) {
+        fprintf(stderr, "[batch-lm] population beyond device bounds (K<=%d, stack<=%d, "
+                        "n_vars<=%d, nodes<=%d)\n", CO_MAX_K, CO_MAX_STACK, CO_MAX_VARS,
+                CO_MAX_NODES);
+        return 2;
+    }
+    if (rc0 != CO_OK) {
+        fprintf(stderr, "[batch-lm] invalid population (code %d)\n", rc0);
+        return 1;
+    }
+    void *handle = nullptr;
+    if (co_init(0, &handle) != CO_OK) {
+        fprintf(stderr, "[batch-lm] device init failed\n");
+        return 1;
+    }
+    const size_t M = h.M_prob, C = h.total_c;
+    std::vector<double> c0(p.c_init.begin(), p.c_init.end());
+    std::vector<double> xs(p.xs.begin(), p.xs.end()), ym(p.ym.begin(), p.ym.end());
+    std::vector<double> cf(C > 0 ? C : 1), li(M > 0 ? M : 1), lf(M > 0 ? M : 1);
+    std::vector<int32_t> status(M > 0 ? M : 1), iters(M > 0 ? M : 1);
+    CoOptions opt;
+    co_options_default(&opt);
+    opt.max_iter = max_iter;
+    opt.ad_mode = rev ? CO_AD_REVERSE : CO_AD_FORWARD;
+    opt.precision = mixed ? CO_PREC_MIXED : CO_PREC_FP64;
+    int rc = co_optimize_ex(handle, &opt, &h, p.nt.data(), p.nv.data(), p.ci.data(),
+                            p.metas.data(), c0.data(), xs.data(), ym.data(), cf.data(),
+                            status.data(), li.data(), lf.data(), iters.data());
+    co_teardown(handle);
+    if (rc != CO_OK) {
+        fprintf(stderr, "[batch-lm] fit failed (code %d)\n", rc);
+        return rc == CO_ERR_BOUNDS ? 2 : 1;
+    }
+    std::vector<float> cf32(C > 0 ? C : 1), li32(M > 0 ? M : 1), lf32(M > 0 ? M : 1);
+    for (size_t j = 0; j < C; j++) cf32[j] = (float)cf[j];
+    for (size_t m = 0; m < M; m++) { li32[m] = (float)li[m]; lf32[m] = (float)lf[m]; }
+    bool ok = write_blob(out_dir + "/status.bin", status.data(), 4 * M) &&
+              write_blob(out_dir + "/c_final.bin", cf32.data(), 4 * C) &&
+              write_blob(out_dir + "/loss_final.bin", lf32.data(), 4 * M) &&
+              write_blob(out_dir + "/loss_init.bin", li32.data(), 4 * M);
+    if (!ok) return 1;
+    const double el = seconds() - t0;
+    if (!quiet) {
+        int cnt[5] = {0, 0, 0, 0, 0};
+        for (size_t m = 0; m < M; m++)
+            if (status[m] >= 0 && status[m] < 5) cnt[status[m]]++;
+        printf("[batch-lm] 完成: converged=%d (%.1f%%)  maxiter=%d  fail_nan=%d  "
+               "fail_cholesky=%d  k0_skip=%d  (M_prob=%d)\n",
+               cnt[0], M ? 100.0 * cnt[0] / M : 0.0, cnt[1], cnt[2], cnt[4], cnt[3], h.M_prob);
+        printf("[batch-lm] 总耗时 %.3f 秒 (%.0f trees/s, M_prob=%d)\n", el, M / el, h.M_prob);
+    }
+    return 0;
+}

@@ -1,0 +1,413 @@
+// co_lib.hip -- C ABI of the MI355X batched LM fitter (include/cusr_co.h).
+//
+// Mirrors the reference in-process library (cusr/kernel/co_lib.cu:113-568):
+// a persistent per-device context whose device buffers grow by byte capacity
+// and never shrink (co_lib.cu:16-24,113-153), every call re-seeded from its own
+// inputs (co_lib.cu:284-305), outputs written to caller buffers sized by the
+// current header, errors returned as codes and never exit(). Unlike the
+// reference, the whole LM loop is one kernel launch; the host only plans,
+// uploads, launches once and reads the results back.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include <new>
+#include <vector>
+
+#include "lm_device.h"
+#include "program.h"
+
+namespace cusr {
+
+// ------------------------------------------------------ layout kernels
+
+// xs row-major [N][D] (f32 or f64) -> X column-major [D][N] f64
+template <typename T>
+__global__ void transpose_x_kernel(const T *xs, double *X, int N, int D) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)N * D) return;
+    const size_t i = t / D, v = t % D;
+    X[v * N + i] = (double)xs[t];
+}
+
+__global__ void widen_kernel(const float *src, double *dst, size_t n) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < n) dst[t] = (double)src[t];
+}
+
+}  // namespace cusr
+
+using namespace cusr;
+
+namespace {
+
+double now_ms() {
+    timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return t.tv_sec * 1e3 + t.tv_nsec / 1e6;
+}
+
+double g_setup_ms = -1.0, g_loop_ms = -1.0;
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+constexpr int kStreams = 4;
+
+// one launcher per (precision, AD mode), each built from fit_kernels.hip in
+// its own translation unit so the four variants compile in parallel
+typedef hipError_t (*FitLauncher)(int K, unsigned grid, size_t lds, hipStream_t s,
+                                  const FitArgs &fa);
+
+struct Ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    hipStream_t lanes[kStreams] = {};
+    hipEvent_t ev_start = nullptr;
+    hipEvent_t ev_done[kStreams] = {};
+    DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
+    std::vector<uint64_t> h_prog;
+    std::vector<ExprDesc> h_desc;
+    std::vector<double> h_c, h_li, h_lf;
+};
+
+#define CO_HIP(call)                                                                    \
+    do {                                                                                \
+        hipError_t e_ = (call);                                                         \
+        if (e_ != hipSuccess) {                                                         \
+            fprintf(stderr, "[cusr_co] HIP error %s at %s:%d\n", hipGetErrorString(e_), \
+                    __FILE__, __LINE__);                                                \
+            return CO_ERR_CUDA;                                                         \
+        }                                                                               \
+    } while (0)
+
+int grow(DevBuf &b, size_t bytes) {
+    if (bytes == 0) bytes = 256;
+    if (bytes <= b.cap) return CO_OK;
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    hipError_t e = hipMalloc(&b.p, bytes);
+    if (e != hipSuccess) {
+        fprintf(stderr, "[cusr_co] hipMalloc(%zu) failed: %s\n", bytes, hipGetErrorString(e));
+        b.p = nullptr;
+        return (e == hipErrorOutOfMemory) ? CO_ERR_OOM : CO_ERR_CUDA;
+    }
+    b.cap = bytes;
+    return CO_OK;
+}
+
+#define CO_GROW(buf, bytes)                   \
+    do {                                      \
+        int r_ = grow((buf), (bytes));        \
+        if (r_ != CO_OK) return r_;           \
+    } while (0)
+
+template <typename T>
+T *ptr(DevBuf &b) { return (T *)b.p; }
+
+unsigned blocks_for(size_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
+
+// Shared body of co_optimize / co_optimize_ex. Inputs c/xs/ym are either fp32
+// (in32) or fp64 host arrays; outputs are fp64 host arrays (sized by header).
+int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t *nt,
+               const float *nv, const int32_t *ci, const TreeMeta *metas, const void *c,
+               const void *xs, const void *ym, bool in32, double *c_out, int32_t *status_out,
+               double *li_out, double *lf_out, int32_t *iters_out) {
+    const double t0 = now_ms();
+    CO_HIP(hipSetDevice(ctx->device));
+    if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
+    if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
+    if (opt.max_iter < 0) return CO_ERR_NULLARG;
+    const int M = h->M_prob;
+    ctx->h_prog.resize(h->total_nodes > 0 ? h->total_nodes : 1);
+    ctx->h_desc.resize(M > 0 ? M : 1);
+    Plan plan;
+    int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
+                               ctx->h_desc.data(), nullptr, &plan);
+    if (rc != CO_OK) return rc;
+    if (M == 0) {
+        g_setup_ms = now_ms() - t0;
+        g_loop_ms = 0.0;
+        return CO_OK;
+    }
+    const int N = h->N, D = h->n_vars, C = h->total_c;
+    const size_t nX = (size_t)N * D, nY = (size_t)M * N;
+    const size_t esz = in32 ? 4 : 8;
+    CO_GROW(ctx->prog, sizeof(uint64_t) * h->total_nodes);
+    CO_GROW(ctx->desc, sizeof(ExprDesc) * M);
+    CO_GROW(ctx->X, sizeof(double) * nX);
+    CO_GROW(ctx->Y, sizeof(double) * nY);
+    CO_GROW(ctx->C0, sizeof(double) * C);
+    CO_GROW(ctx->C, sizeof(double) * C);
+    CO_GROW(ctx->status, sizeof(int32_t) * M);
+    CO_GROW(ctx->li, sizeof(double) * M);
+    CO_GROW(ctx->lf, sizeof(double) * M);
+    CO_GROW(ctx->iters, sizeof(int32_t) * M);
+    size_t stage = esz * nX;
+    if (in32 && esz * nY > stage) stage = esz * nY;
+    if (in32 && esz * C > stage) stage = esz * C;
+    CO_GROW(ctx->stage, stage);
+    hipStream_t s = ctx->stream;
+
+    CO_HIP(hipMemcpyAsync(ctx->prog.p, ctx->h_prog.data(), sizeof(uint64_t) * h->total_nodes,
+                          hipMemcpyHostToDevice, s));
+    CO_HIP(hipMemcpyAsync(ctx->desc.p, ctx->h_desc.data(), sizeof(ExprDesc) * M,
+                          hipMemcpyHostToDevice, s));
+    // xs: row-major host array -> column-major fp64 on the device
+    if (nX) {
+        CO_HIP(hipMemcpyAsync(ctx->stage.p, xs, esz * nX, hipMemcpyHostToDevice, s));
+        if (in32)
+            transpose_x_kernel<float><<<blocks_for(nX, 256), 256, 0, s>>>(
+                ptr<float>(ctx->stage), ptr<double>(ctx->X), N, D);
+        else
+            transpose_x_kernel<double><<<blocks_for(nX, 256), 256, 0, s>>>(
+                ptr<double>(ctx->stage), ptr<double>(ctx->X), N, D);
+        CO_HIP(hipGetLastError());
+    }
+    if (in32) {
+        if (nY) {
+            CO_HIP(hipMemcpyAsync(ctx->stage.p, ym, 4 * nY, hipMemcpyHostToDevice, s));
+            widen_kernel<<<blocks_for(nY, 256), 256, 0, s>>>(ptr<float>(ctx->stage),
+                                                            ptr<double>(ctx->Y), nY);
+            CO_HIP(hipGetLastError());
+        }
+        if (C) {
+            CO_HIP(hipMemcpyAsync(ctx->stage.p, c, 4 * (size_t)C, hipMemcpyHostToDevice, s));
+            widen_kernel<<<blocks_for(C, 256), 256, 0, s>>>(ptr<float>(ctx->stage),
+                                                           ptr<double>(ctx->C0), C);
+            CO_HIP(hipGetLastError());
+        }
+    } else {
+        if (nY) CO_HIP(hipMemcpyAsync(ctx->Y.p, ym, 8 * nY, hipMemcpyHostToDevice, s));
+        if (C) CO_HIP(hipMemcpyAsync(ctx->C0.p, c, 8 * (size_t)C, hipMemcpyHostToDevice, s));
+    }
+    CO_HIP(hipStreamSynchronize(s));
+    const double t1 = now_ms();
+
+    FitArgs fa;
+    fa.prog = ptr<uint64_t>(ctx->prog);
+    fa.desc = ptr<ExprDesc>(ctx->desc);
+    fa.X = ptr<double>(ctx->X);
+    fa.Y = ptr<double>(ctx->Y);
+    fa.C0 = ptr<double>(ctx->C0);
+    fa.C = ptr<double>(ctx->C);
+    fa.status = ptr<int32_t>(ctx->status);
+    fa.loss_init = ptr<double>(ctx->li);
+    fa.loss_final = ptr<double>(ctx->lf);
+    fa.iters = ptr<int32_t>(ctx->iters);
+    fa.N = N;
+    fa.D = D;
+    fa.max_iter = opt.max_iter;
+    fa.guard = opt.fp64_guard ? 1 : 0;
+    fa.lambda0 = opt.lambda0;
+    fa.xtol = opt.xtol;
+    fa.tape_slots = plan.max_tape;
+    const bool rev = opt.ad_mode == CO_AD_REVERSE;
+    const bool mixed = opt.precision == CO_PREC_MIXED;
+    const size_t tape_bytes = rev ? (size_t)plan.max_tape * kLanes * (mixed ? 4 : 8) : 0;
+    // descriptors are in launch order, largest K first; one launch per K bin,
+    // bins spread over the context's streams so their tails overlap
+    const FitLauncher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
+                                     : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
+    int pos = 0, nb = 0;
+    CO_HIP(hipEventRecord(ctx->ev_start, s));
+    for (int k = CO_MAX_K; k >= 0; --k) {
+        int cnt = 0;
+        while (pos + cnt < M && ctx->h_desc[pos + cnt].K == k) ++cnt;
+        if (cnt == 0) continue;
+        hipStream_t ks = ctx->lanes[nb % kStreams];
+        if (nb < kStreams) CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
+        FitArgs fk = fa;
+        fk.desc = fa.desc + pos;
+        CO_HIP(launch(k, (unsigned)cnt, tape_bytes, ks, fk));
+        pos += cnt;
+        ++nb;
+    }
+    for (int i = 0; i < kStreams && i < nb; ++i) {
+        CO_HIP(hipEventRecord(ctx->ev_done[i], ctx->lanes[i]));
+        CO_HIP(hipStreamWaitEvent(s, ctx->ev_done[i], 0));
+    }
+
+    if (C) CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, hipMemcpyDeviceToHost, s));
+    CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M, hipMemcpyDeviceToHost, s));
+    if (li_out) CO_HIP(hipMemcpyAsync(li_out, ctx->li.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
+    if (lf_out) CO_HIP(hipMemcpyAsync(lf_out, ctx->lf.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
+    if (iters_out)
+        CO_HIP(hipMemcpyAsync(iters_out, ctx->iters.p, 4 * (size_t)M, hipMemcpyDeviceToHost, s));
+    CO_HIP(hipStreamSynchronize(s));
+    g_setup_ms = t1 - t0;
+    g_loop_ms = now_ms() - t1;
+    return CO_OK;
+}
+
+}  // namespace
+
+extern "C" void co_options_default(CoOptions *o) {
+    if (!o) return;
+    memset(o, 0, sizeof(*o));
+    o->struct_size = (int32_t)sizeof(CoOptions);
+    o->ad_mode = CO_AD_FORWARD;
+    o->precision = CO_PREC_FP64;
+    o->max_iter = 50;
+    o->lambda0 = 1e-3;
+    o->xtol = 1e-6;
+    o->fp64_guard = 1;
+}
+
+extern "C" int co_init(int device_id, void **handle_out) {
+    if (!handle_out) return CO_ERR_NULLARG;
+    *handle_out = nullptr;
+    CO_HIP(hipSetDevice(device_id));
+    CO_HIP(hipFree(nullptr));  // create the device context now, once
+    Ctx *ctx = new (std::nothrow) Ctx();
+    if (!ctx) return CO_ERR_OOM;
+    ctx->device = device_id;
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    for (int i = 0; i < kStreams && e == hipSuccess; ++i)
+        e = hipStreamCreateWithFlags(&ctx->lanes[i], hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming);
+    for (int i = 0; i < kStreams && e == hipSuccess; ++i)
+        e = hipEventCreateWithFlags(&ctx->ev_done[i], hipEventDisableTiming);
+    if (e != hipSuccess) {
+        fprintf(stderr, "[cusr_co] stream/event create: %s\n", hipGetErrorString(e));
+        co_teardown(ctx);
+        return CO_ERR_CUDA;
+    }
+    *handle_out = ctx;
+    return CO_OK;
+}
+
+extern "C" int co_optimize(void *handle, const PopHeader *h, const int32_t *nt, const float *nv,
+                           const int32_t *ci, const TreeMeta *metas, const float *c_init,
+                           const float *xs, const float *ym, int max_iter, float *c_final_out,
+                           int32_t *status_out, float *loss_init_out, float *loss_final_out) {
+    if (!handle || !h || !nt || !nv || !ci || !metas || !c_init || !xs || !ym || !c_final_out ||
+        !status_out)
+        return CO_ERR_NULLARG;
+    Ctx *ctx = (Ctx *)handle;
+    CoOptions opt;
+    co_options_default(&opt);
+    opt.max_iter = max_iter;
+    const int M = h->M_prob > 0 ? h->M_prob : 0;
+    const int C = h->total_c > 0 ? h->total_c : 0;
+    ctx->h_c.resize(C > 0 ? C : 1);
+    ctx->h_li.resize(M > 0 ? M : 1);
+    ctx->h_lf.resize(M > 0 ? M : 1);
+    int rc = fit_common(ctx, opt, h, nt, nv, ci, metas, c_init, xs, ym, true, ctx->h_c.data(),
+                        status_out, ctx->h_li.data(), ctx->h_lf.data(), nullptr);
+    if (rc != CO_OK) return rc;
+    for (int j = 0; j < C; j++) c_final_out[j] = (float)ctx->h_c[j];
+    for (int m = 0; m < M; m++) {
+        if (loss_init_out) loss_init_out[m] = (float)ctx->h_li[m];
+        if (loss_final_out) loss_final_out[m] = (float)ctx->h_lf[m];
+    }
+    return CO_OK;
+}
+
+extern "C" int co_optimize_ex(void *handle, const CoOptions *opt, const PopHeader *h,
+                              const int32_t *nt, const float *nv, const int32_t *ci,
+                              const TreeMeta *metas, const double *c, const double *xs,
+                              const double *ym, double *c_final_out, int32_t *status_out,
+                              double *loss_init_out, double *loss_final_out,
+                              int32_t *iters_out) {
+    if (!handle || !opt || !h || !nt || !nv || !ci || !metas || !c || !xs || !ym ||
+        !c_final_out || !status_out)
+        return CO_ERR_NULLARG;
+    if (opt->struct_size != (int32_t)sizeof(CoOptions)) return CO_ERR_NULLARG;
+    return fit_common((Ctx *)handle, *opt, h, nt, nv, ci, metas, c, xs, ym, false, c_final_out,
+                      status_out, loss_init_out, loss_final_out, iters_out);
+}
+
+extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, const float *nv,
+                          const int32_t *ci, const TreeMeta *metas, const double *c,
+                          const double *xs, int precision, double *y_out) {
+    if (!handle || !h || !nt || !nv || !ci || !metas || !c || !xs || !y_out)
+        return CO_ERR_NULLARG;
+    if (precision != CO_PREC_FP64 && precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
+    Ctx *ctx = (Ctx *)handle;
+    CO_HIP(hipSetDevice(ctx->device));
+    const int M = h->M_prob;
+    ctx->h_prog.resize(h->total_nodes > 0 ? h->total_nodes : 1);
+    ctx->h_desc.resize(M > 0 ? M : 1);
+    int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
+                               ctx->h_desc.data(), nullptr, nullptr);
+    if (rc != CO_OK || M == 0) return rc;
+    const int N = h->N, D = h->n_vars, C = h->total_c;
+    const size_t nX = (size_t)N * D, nY = (size_t)M * N;
+    CO_GROW(ctx->prog, sizeof(uint64_t) * h->total_nodes);
+    CO_GROW(ctx->desc, sizeof(ExprDesc) * M);
+    CO_GROW(ctx->X, sizeof(double) * nX);
+    CO_GROW(ctx->Y, sizeof(double) * nY);
+    CO_GROW(ctx->C0, sizeof(double) * C);
+    CO_GROW(ctx->stage, sizeof(double) * nX);
+    hipStream_t s = ctx->stream;
+    CO_HIP(hipMemcpyAsync(ctx->prog.p, ctx->h_prog.data(), sizeof(uint64_t) * h->total_nodes,
+                          hipMemcpyHostToDevice, s));
+    CO_HIP(hipMemcpyAsync(ctx->desc.p, ctx->h_desc.data(), sizeof(ExprDesc) * M,
+                          hipMemcpyHostToDevice, s));
+    if (C) CO_HIP(hipMemcpyAsync(ctx->C0.p, c, 8 * (size_t)C, hipMemcpyHostToDevice, s));
+    if (nX) {
+        CO_HIP(hipMemcpyAsync(ctx->stage.p, xs, 8 * nX, hipMemcpyHostToDevice, s));
+        transpose_x_kernel<double><<<blocks_for(nX, 256), 256, 0, s>>>(
+            ptr<double>(ctx->stage), ptr<double>(ctx->X), N, D);
+        CO_HIP(hipGetLastError());
+    }
+    EvalArgs ea;
+    ea.prog = ptr<uint64_t>(ctx->prog);
+    ea.desc = ptr<ExprDesc>(ctx->desc);
+    ea.X = ptr<double>(ctx->X);
+    ea.C = ptr<double>(ctx->C0);
+    ea.Yout = ptr<double>(ctx->Y);
+    ea.N = N;
+    ea.D = D;
+    if (precision == CO_PREC_FP64)
+        eval_kernel<double><<<M, kLanes, 0, s>>>(ea);
+    else
+        eval_kernel<float><<<M, kLanes, 0, s>>>(ea);
+    CO_HIP(hipGetLastError());
+    if (nY) CO_HIP(hipMemcpyAsync(y_out, ctx->Y.p, 8 * nY, hipMemcpyDeviceToHost, s));
+    CO_HIP(hipStreamSynchronize(s));
+    return CO_OK;
+}
+
+extern "C" int co_decode(const PopHeader *h, const int32_t *nt, const float *nv,
+                         const int32_t *ci, const TreeMeta *metas, uint64_t *program_out,
+                         int32_t *order_out, int32_t *bin_start_out, int32_t *stack_out) {
+    if (!h) return CO_ERR_NULLARG;
+    std::vector<uint64_t> tmp;
+    uint64_t *prog = program_out;
+    if (!prog) {
+        tmp.resize(h->total_nodes > 0 ? h->total_nodes : 1);
+        prog = tmp.data();
+    }
+    return decode_population(h, nt, nv, ci, metas, prog, order_out, bin_start_out, nullptr,
+                             stack_out, nullptr);
+}
+
+extern "C" int co_last_split(double *setup_ms_out, double *loop_ms_out) {
+    if (setup_ms_out) *setup_ms_out = g_setup_ms;
+    if (loop_ms_out) *loop_ms_out = g_loop_ms;
+    return 0;
+}
+
+extern "C" void co_teardown(void *handle) {
+    if (!handle) return;
+    Ctx *ctx = (Ctx *)handle;
+    (void)hipSetDevice(ctx->device);
+    DevBuf *bufs[] = {&ctx->prog, &ctx->desc, &ctx->X, &ctx->Y, &ctx->C0, &ctx->C,
+                      &ctx->status, &ctx->li, &ctx->lf, &ctx->iters, &ctx->stage};
+    for (DevBuf *b : bufs)
+        if (b->p) (void)hipFree(b->p);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    for (int i = 0; i < kStreams; ++i) {
+        if (ctx->lanes[i]) (void)hipStreamDestroy(ctx->lanes[i]);
+        if (ctx->ev_done[i]) (void)hipEventDestroy(ctx->ev_done[i]);
+    }
+    if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
+    delete ctx;
+}

@@ -1,0 +1,28 @@
+// fit_kernels.hip -- instantiates the fit kernels of one (precision, AD mode)
+// variant for K = 0..CO_MAX_K. Built four times with
+//   -DCUSR_FIT_R=double|float -DCUSR_FIT_AD=0|1 -DCUSR_FIT_LAUNCH=<name>.
+#include "lm_device.h"
+
+#if !defined(CUSR_FIT_R) || !defined(CUSR_FIT_AD) || !defined(CUSR_FIT_LAUNCH)
+#error "fit_kernels.hip needs CUSR_FIT_R, CUSR_FIT_AD and CUSR_FIT_LAUNCH"
+#endif
+
+namespace cusr {
+
+hipError_t CUSR_FIT_LAUNCH(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa) {
+    switch (K) {
+#define CUSR_CASE(k)                                                                   \
+    case k:                                                                            \
+        lm_fit_kernel<k, CUSR_FIT_R, CUSR_FIT_AD><<<grid, kLanes, lds, s>>>(fa);       \
+        break;
+        CUSR_CASE(0) CUSR_CASE(1) CUSR_CASE(2) CUSR_CASE(3) CUSR_CASE(4) CUSR_CASE(5)
+        CUSR_CASE(6) CUSR_CASE(7) CUSR_CASE(8) CUSR_CASE(9) CUSR_CASE(10) CUSR_CASE(11)
+        CUSR_CASE(12) CUSR_CASE(13) CUSR_CASE(14) CUSR_CASE(15) CUSR_CASE(16)
+#undef CUSR_CASE
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace cusr

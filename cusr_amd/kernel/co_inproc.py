@@ -1,0 +1,350 @@
+"""ctypes loader of the MI355X fitter library, API of cusr/kernel/co_inproc.py.
+
+`InProcessCO(device_id, lib_path, variant).optimize(pop, max_iter)` and the
+process-wide `get_inproc_co(device_id, variant)` keep the reference's names,
+arguments, return dicts and `COError` codes (co_inproc.py:51-57,101-295): a pop
+dict (popio keys M, total_nodes, ..., nt, nv, ci, metas, c_init, xs, ym) goes
+in; {'c_final', 'status', 'loss_init', 'loss_final'} (fp32) comes out.
+
+Extensions with no reference counterpart:
+  optimize_ex(pop, ...)  fp64 constants/data/outputs, AD mode and precision
+  evaluate(pop, c)       y[m, i] = f_m(x_i; c_m) on the device
+  decode(pop)            host-only checks, device programs and K bins
+
+There is no CPU path: when the library is not built these raise.
+"""
+from __future__ import annotations
+
+import atexit
+import ctypes
+import threading
+from pathlib import Path
+
+import numpy as np
+
+POP_MAGIC = 0x4D4C344D
+POP_VERSION = 1
+
+CO_OK = 0
+CO_ERR_BOUNDS = 2
+CO_ERR_CUDA = -1
+CO_ERR_SUM_C = -2
+CO_ERR_SUM_NODES = -3
+CO_ERR_NULLARG = -4
+CO_ERR_OOM = -5
+CO_ERR_PROGRAM = -6
+
+CO_MAX_K = 16
+CO_MAX_STACK = 16
+CO_MAX_VARS = 8
+CO_MAX_NODES = 255
+
+CO_AD_FORWARD, CO_AD_REVERSE = 0, 1
+CO_PREC_FP64, CO_PREC_MIXED = 0, 1
+
+_ERR_MSG = {
+    CO_ERR_BOUNDS: (f"beyond device bounds (K<={CO_MAX_K}, max_stack<={CO_MAX_STACK}, "
+                    f"n_vars<={CO_MAX_VARS}, n_nodes<={CO_MAX_NODES})"),
+    CO_ERR_CUDA: "HIP error inside the library",
+    CO_ERR_SUM_C: "sum(metas.K) != header.total_c (pop inconsistent)",
+    CO_ERR_SUM_NODES: "sum(metas.n_nodes) != header.total_nodes (pop inconsistent)",
+    CO_ERR_NULLARG: "null pointer / bad argument",
+    CO_ERR_OOM: "out of memory growing a device buffer",
+    CO_ERR_PROGRAM: "malformed expression (unknown op, bad node, rank or variable index)",
+}
+
+
+class COError(RuntimeError):
+    """A non-OK return code of the library (co_inproc.py:51-57)."""
+
+    def __init__(self, code: int, where: str):
+        self.code = code
+        super().__init__(f"{where}: {_ERR_MSG.get(code, f'unknown code {code}')} (code={code})")
+
+
+class PopHeader(ctypes.Structure):
+    """pop_format.h PopHeader: 16 x int32 = 64 B."""
+    _fields_ = [("magic", ctypes.c_int32), ("version", ctypes.c_int32),
+                ("M_prob", ctypes.c_int32), ("total_nodes", ctypes.c_int32),
+                ("total_c", ctypes.c_int32), ("N", ctypes.c_int32),
+                ("n_vars", ctypes.c_int32), ("K_max", ctypes.c_int32),
+                ("max_stack", ctypes.c_int32), ("reserved", ctypes.c_int32 * 7)]
+
+
+class TreeMeta(ctypes.Structure):
+    """pop_format.h TreeMeta: 4 x int32 = 16 B."""
+    _fields_ = [("node_offset", ctypes.c_int32), ("n_nodes", ctypes.c_int32),
+                ("c_offset", ctypes.c_int32), ("K", ctypes.c_int32)]
+
+
+class CoOptions(ctypes.Structure):
+    """cusr_co.h CoOptions."""
+    _fields_ = [("struct_size", ctypes.c_int32), ("ad_mode", ctypes.c_int32),
+                ("precision", ctypes.c_int32), ("max_iter", ctypes.c_int32),
+                ("lambda0", ctypes.c_double), ("xtol", ctypes.c_double),
+                ("fp64_guard", ctypes.c_int32), ("reserved", ctypes.c_int32 * 7)]
+
+
+assert ctypes.sizeof(PopHeader) == 64
+assert ctypes.sizeof(TreeMeta) == 16
+assert ctypes.sizeof(CoOptions) == 64
+
+_VP = ctypes.c_void_p
+_HERE = Path(__file__).resolve().parent
+
+# every extern "C" symbol of include/cusr_co.h
+EXPORTED = ("co_init", "co_optimize", "co_last_split", "co_teardown", "co_options_default",
+            "co_optimize_ex", "co_eval_ex", "co_decode")
+
+
+def lib_path(variant: str = "ad") -> Path:
+    """libcusr_co_<variant>.so next to this module (cusr_amd/build.py output)."""
+    return _HERE / f"libcusr_co_{variant}.so"
+
+
+def _arr(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a, a.ctypes.data_as(_VP)
+
+
+def _header(pop: dict) -> PopHeader:
+    """Full 64-B header from a pop dict (co_inproc.py:148-163)."""
+    h = PopHeader()
+    h.magic, h.version = POP_MAGIC, POP_VERSION
+    h.M_prob = int(pop["M"])
+    h.total_nodes = int(pop["total_nodes"])
+    h.total_c = int(pop["total_c"])
+    h.N = int(pop["N"])
+    h.n_vars = int(pop["n_vars"])
+    h.K_max = int(pop["K_max"])
+    h.max_stack = int(pop["max_stack"])
+    return h
+
+
+def _metas(pop: dict):
+    M = int(pop["M"])
+    m = np.ascontiguousarray(pop["metas"], dtype=np.int32).reshape(M, 4)
+    return m, m.ctypes.data_as(_VP)
+
+
+def _bind(lib) -> None:
+    i32, dbl = ctypes.c_int32, ctypes.c_double
+    lib.co_init.argtypes = [ctypes.c_int, ctypes.POINTER(_VP)]
+    lib.co_init.restype = ctypes.c_int
+    lib.co_optimize.argtypes = [_VP, ctypes.POINTER(PopHeader)] + [_VP] * 7 + [ctypes.c_int] + [_VP] * 4
+    lib.co_optimize.restype = ctypes.c_int
+    lib.co_optimize_ex.argtypes = [_VP, ctypes.POINTER(CoOptions), ctypes.POINTER(PopHeader)] + [_VP] * 12
+    lib.co_optimize_ex.restype = ctypes.c_int
+    lib.co_eval_ex.argtypes = [_VP, ctypes.POINTER(PopHeader)] + [_VP] * 6 + [ctypes.c_int, _VP]
+    lib.co_eval_ex.restype = ctypes.c_int
+    lib.co_decode.argtypes = [ctypes.POINTER(PopHeader)] + [_VP] * 8
+    lib.co_decode.restype = ctypes.c_int
+    lib.co_last_split.argtypes = [ctypes.POINTER(dbl), ctypes.POINTER(dbl)]
+    lib.co_last_split.restype = ctypes.c_int
+    lib.co_teardown.argtypes = [_VP]
+    lib.co_teardown.restype = None
+    lib.co_options_default.argtypes = [ctypes.POINTER(CoOptions)]
+    lib.co_options_default.restype = None
+    del i32
+
+
+_LIBS: dict[str, ctypes.CDLL] = {}
+
+
+def load_library(variant: str = "ad", path: str | Path | None = None) -> ctypes.CDLL:
+    """dlopen the built library (no device call). Raises if it is not built."""
+    p = Path(path) if path is not None else lib_path(variant)
+    key = str(p.resolve()) if p.exists() else str(p)
+    if key not in _LIBS:
+        if not p.exists():
+            raise FileNotFoundError(f"{p} is not built: run `python -m cusr_amd.build`")
+        lib = ctypes.CDLL(str(p.resolve()))
+        _bind(lib)
+        _LIBS[key] = lib
+    return _LIBS[key]
+
+
+def decode(pop: dict, variant: str = "ad"):
+    """Host-only decode: (rc, program uint64[T], order int32[M], bin_start int32[K+2],
+    stack int32[M]). Needs no GPU."""
+    lib = load_library(variant)
+    h = _header(pop)
+    T, M = int(pop["total_nodes"]), int(pop["M"])
+    nt, pnt = _arr(pop["nt"], np.int32)
+    nv, pnv = _arr(pop["nv"], np.float32)
+    ci, pci = _arr(pop["ci"], np.int32)
+    me, pme = _metas(pop)
+    prog = np.zeros(max(T, 1), np.uint64)
+    order = np.zeros(max(M, 1), np.int32)
+    bins = np.zeros(CO_MAX_K + 2, np.int32)
+    stack = np.zeros(max(M, 1), np.int32)
+    rc = lib.co_decode(ctypes.byref(h), pnt, pnv, pci, pme, prog.ctypes.data_as(_VP),
+                       order.ctypes.data_as(_VP), bins.ctypes.data_as(_VP),
+                       stack.ctypes.data_as(_VP))
+    return rc, prog[:T], order[:M], bins, stack[:M]
+
+
+def default_options(**kw) -> CoOptions:
+    o = CoOptions()
+    o.struct_size = ctypes.sizeof(CoOptions)
+    o.ad_mode, o.precision, o.max_iter = CO_AD_FORWARD, CO_PREC_FP64, 50
+    o.lambda0, o.xtol, o.fp64_guard = 1e-3, 1e-6, 1
+    for k, v in kw.items():
+        setattr(o, k, v)
+    return o
+
+
+class InProcessCO:
+    """One persistent device context over the library (co_inproc.py:101-246)."""
+
+    def __init__(self, device_id: int = 0, lib_path: str | Path | None = None,
+                 variant: str = "ad"):
+        self.variant = variant
+        self.device_id = int(device_id)
+        self._lib = load_library(variant, lib_path)
+        self._handle = _VP()
+        self._torn = False
+        rc = self._lib.co_init(self.device_id, ctypes.byref(self._handle))
+        if rc != CO_OK:
+            raise COError(rc, "co_init")
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.teardown()
+        return False
+
+    def _check(self):
+        if self._torn:
+            raise RuntimeError("InProcessCO used after teardown()")
+
+    def _build_header(self, pop: dict) -> PopHeader:
+        return _header(pop)
+
+    def optimize(self, pop: dict, max_iter: int = 50) -> dict:
+        """Reference-compatible fit: fp32 in, fp32 out (co_inproc.py:165-215)."""
+        self._check()
+        M, C = int(pop["M"]), int(pop["total_c"])
+        h = _header(pop)
+        nt, pnt = _arr(pop["nt"], np.int32)
+        nv, pnv = _arr(pop["nv"], np.float32)
+        ci, pci = _arr(pop["ci"], np.int32)
+        me, pme = _metas(pop)
+        c0, pc0 = _arr(pop["c_init"], np.float32)
+        xs, pxs = _arr(pop["xs"], np.float32)
+        ym, pym = _arr(pop["ym"], np.float32)
+        c_final = np.zeros(max(C, 1), np.float32)
+        status = np.zeros(max(M, 1), np.int32)
+        loss_init = np.zeros(max(M, 1), np.float32)
+        loss_final = np.zeros(max(M, 1), np.float32)
+        rc = self._lib.co_optimize(self._handle, ctypes.byref(h), pnt, pnv, pci, pme, pc0, pxs,
+                                   pym, int(max_iter), c_final.ctypes.data_as(_VP),
+                                   status.ctypes.data_as(_VP), loss_init.ctypes.data_as(_VP),
+                                   loss_final.ctypes.data_as(_VP))
+        if rc != CO_OK:
+            raise COError(rc, "co_optimize")
+        return {"c_final": c_final[:C], "status": status[:M],
+                "loss_init": loss_init[:M], "loss_final": loss_final[:M]}
+
+    def optimize_ex(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
+                    precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
+                    fp64_guard: bool = True, c_init=None, xs=None, ym=None) -> dict:
+        """fp64 fit; c_init/xs/ym override the pop's (fp32) arrays when given."""
+        self._check()
+        M, C = int(pop["M"]), int(pop["total_c"])
+        h = _header(pop)
+        o = default_options(ad_mode=int(ad_mode), precision=int(precision),
+                            max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
+                            fp64_guard=1 if fp64_guard else 0)
+        nt, pnt = _arr(pop["nt"], np.int32)
+        nv, pnv = _arr(pop["nv"], np.float32)
+        ci, pci = _arr(pop["ci"], np.int32)
+        me, pme = _metas(pop)
+        c0, pc0 = _arr(pop["c_init"] if c_init is None else c_init, np.float64)
+        x, px = _arr(pop["xs"] if xs is None else xs, np.float64)
+        y, py = _arr(pop["ym"] if ym is None else ym, np.float64)
+        out = {"c_final": np.zeros(max(C, 1)), "status": np.zeros(max(M, 1), np.int32),
+               "loss_init": np.zeros(max(M, 1)), "loss_final": np.zeros(max(M, 1)),
+               "iters": np.zeros(max(M, 1), np.int32)}
+        rc = self._lib.co_optimize_ex(
+            self._handle, ctypes.byref(o), ctypes.byref(h), pnt, pnv, pci, pme, pc0, px, py,
+            *(out[k].ctypes.data_as(_VP) for k in
+              ("c_final", "status", "loss_init", "loss_final", "iters")))
+        if rc != CO_OK:
+            raise COError(rc, "co_optimize_ex")
+        out["c_final"] = out["c_final"][:C]
+        for k in ("status", "loss_init", "loss_final", "iters"):
+            out[k] = out[k][:M]
+        return out
+
+    def evaluate(self, pop: dict, c=None, xs=None, precision: int = CO_PREC_FP64) -> np.ndarray:
+        """y[m, i] of every expression at constants c (default c_init)."""
+        self._check()
+        M, N = int(pop["M"]), int(pop["N"])
+        h = _header(pop)
+        nt, pnt = _arr(pop["nt"], np.int32)
+        nv, pnv = _arr(pop["nv"], np.float32)
+        ci, pci = _arr(pop["ci"], np.int32)
+        me, pme = _metas(pop)
+        cc, pcc = _arr(pop["c_init"] if c is None else c, np.float64)
+        if cc.size == 0:
+            cc, pcc = _arr(np.zeros(1), np.float64)
+        x, px = _arr(pop["xs"] if xs is None else xs, np.float64)
+        y = np.zeros((max(M, 1), max(N, 1)))
+        rc = self._lib.co_eval_ex(self._handle, ctypes.byref(h), pnt, pnv, pci, pme, pcc, px,
+                                  int(precision), y.ctypes.data_as(_VP))
+        if rc != CO_OK:
+            raise COError(rc, "co_eval_ex")
+        return y[:M, :N]
+
+    def last_split(self):
+        """(setup_ms, loop_ms) of the last fit on this process."""
+        s, l = ctypes.c_double(-1.0), ctypes.c_double(-1.0)
+        rc = self._lib.co_last_split(ctypes.byref(s), ctypes.byref(l))
+        if rc != 0 or s.value < 0:
+            return (None, None)
+        return (s.value, l.value)
+
+    def teardown(self):
+        if self._torn:
+            return
+        if self._handle:
+            self._lib.co_teardown(self._handle)
+            self._handle = _VP()
+        self._torn = True
+
+    def __del__(self):
+        try:
+            self.teardown()
+        except Exception:  # noqa: BLE001
+            pass
+
+
+_SINGLETONS: dict[tuple[int, str], InProcessCO] = {}
+_LOCK = threading.Lock()
+_ATEXIT = False
+
+
+def _teardown_all() -> None:
+    for co in list(_SINGLETONS.values()):
+        try:
+            co.teardown()
+        except Exception:  # noqa: BLE001
+            pass
+    _SINGLETONS.clear()
+
+
+def get_inproc_co(device_id: int = 0, variant: str = "ad") -> InProcessCO:
+    """Process-wide InProcessCO per (device, variant) (co_inproc.py:271-295)."""
+    global _ATEXIT
+    key = (int(device_id), str(variant))
+    with _LOCK:
+        co = _SINGLETONS.get(key)
+        if co is None or co._torn:
+            co = InProcessCO(device_id=device_id, variant=variant)
+            _SINGLETONS[key] = co
+            if not _ATEXIT:
+                atexit.register(_teardown_all)
+                _ATEXIT = True
+        return co

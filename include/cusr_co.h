@@ -1,0 +1,142 @@
+/* cusr_co.h -- C ABI of the MI355X batched Levenberg-Marquardt constant fitter.
+ *
+ * Drop-in for the reference in-process CO library (cusr/kernel/co_lib.h:45-71):
+ * the four symbols co_init / co_optimize / co_last_split / co_teardown keep
+ * their names, argument meaning, return codes and ownership rules, so the
+ * reference ctypes loader (cusr/kernel/co_inproc.py:101-215) binds this
+ * library unchanged. Everything else below is an extension with no
+ * counterpart in the reference and says so.
+ *
+ * Threading: a handle is not re-entrant; one handle per (device, process)
+ * is the intended use, serialised by the caller (the Python loader holds a
+ * lock). Every call selects the handle's device first.
+ */
+#ifndef CUSR_CO_H
+#define CUSR_CO_H
+
+#include <stdint.h>
+#include "pop_format.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes (cusr/kernel/co_lib.h:27-41, plus CO_ERR_PROGRAM). */
+#define CO_OK 0
+#define CO_ERR_BOUNDS 2      /* K_max, max_stack, n_vars or n_nodes beyond the device limits */
+#define CO_ERR_CUDA (-1)     /* HIP runtime error */
+#define CO_ERR_SUM_C (-2)    /* sum(K) != header.total_c */
+#define CO_ERR_SUM_NODES (-3) /* sum(n_nodes) != header.total_nodes */
+#define CO_ERR_NULLARG (-4)  /* null pointer or bad argument */
+#define CO_ERR_OOM (-5)      /* device allocation failed */
+#define CO_ERR_PROGRAM (-6)  /* malformed expression: unknown op id, bad node type,
+                                stack under/overflow, bad const rank or var index.
+                                Extension: the reference silently evaluates unknown
+                                ops to 0 (cusr/kernel/lm_core.cuh:82,100). */
+
+/* Device limits of this build (the reference's are MAX_K=32, MAX_STACK=64,
+ * cusr/kernel/ad_interp.cuh:34-39). Populations beyond them get CO_ERR_BOUNDS
+ * before anything is copied to the device. */
+#define CO_MAX_K 16
+#define CO_MAX_STACK 16
+#define CO_MAX_VARS 8
+#define CO_MAX_NODES 255
+
+/* Jacobian mode and arithmetic of a fit (extension). */
+#define CO_AD_FORWARD 0
+#define CO_AD_REVERSE 1
+#define CO_PREC_FP64 0   /* fp64 interpreter, Jacobian, reductions and solve */
+#define CO_PREC_MIXED 1  /* fp32 interpreter and Jacobian, fp64 JtJ/Jtr/loss and solve */
+
+/* Options of co_optimize_ex (extension; no counterpart in the reference,
+ * whose knobs are compile-time flags, cusr/kernel/Makefile:9-88).
+ * struct_size must be sizeof(CoOptions); co_options_default fills defaults:
+ * forward AD, fp64, max_iter 50, lambda0 1e-3, xtol 1e-6, guard on
+ * (the reference values, cusr/kernel/batch_lm_ad.cu:301-316). */
+typedef struct CoOptions {
+    int32_t struct_size;
+    int32_t ad_mode;    /* CO_AD_FORWARD / CO_AD_REVERSE */
+    int32_t precision;  /* CO_PREC_FP64 / CO_PREC_MIXED */
+    int32_t max_iter;
+    double lambda0;
+    double xtol;
+    int32_t fp64_guard; /* 1: deliver c_init where the fp64 loss at c_final is
+                           non-finite or worse (cusr/kernel/lm_core.cuh:299-351) */
+    int32_t reserved[7];
+} CoOptions;
+
+/* --- reference ABI (cusr/kernel/co_lib.h:45-71) ------------------------ */
+
+/* Select device_id, create its context once and return an opaque handle. */
+int co_init(int device_id, void **handle_out);
+
+/* Fit one population; fp32 inputs and outputs (cusr/kernel/co_lib.h:55-61).
+ * Inputs are host pointers read during the call. Outputs are caller-allocated
+ * and sized to the current header: c_final_out[total_c], status_out[M_prob],
+ * loss_init_out / loss_final_out [M_prob] (both may be NULL). The fit itself
+ * runs in fp64 with forward AD; outputs are rounded to fp32. */
+int co_optimize(void *handle, const PopHeader *header,
+                const int32_t *nt, const float *nv, const int32_t *ci,
+                const TreeMeta *metas,
+                const float *c_init, const float *xs, const float *ym,
+                int max_iter,
+                float *c_final_out, int32_t *status_out,
+                float *loss_init_out, float *loss_final_out);
+
+/* Wall-clock split of the last co_optimize / co_optimize_ex call on this
+ * process: setup (entry to loop start: checks, plan, uploads) and loop
+ * (device fit until results are back on the host). Returns 0 and fills
+ * both (the reference returns 1 and -1.0 unless built with -DPROFILE,
+ * cusr/kernel/co_lib.cu:531-541; this build always records). */
+int co_last_split(double *setup_ms_out, double *loop_ms_out);
+
+/* Free device and host state of a handle. Safe on NULL. */
+void co_teardown(void *handle);
+
+/* --- extensions (no counterpart in the reference) ------------------------ */
+
+/* Fill *opt with the defaults listed above. */
+void co_options_default(CoOptions *opt);
+
+/* Fit with fp64 constants, data and outputs, for parity runs at fp64
+ * tolerance (the fp32 carrier of co_optimize cannot hold 1e-9 loss parity).
+ * xs is row-major [N][n_vars] like pop.bin; ym is [M_prob][N].
+ * iters_out [M_prob] (may be NULL) receives the LM iterations each
+ * expression ran. loss_* may be NULL. */
+int co_optimize_ex(void *handle, const CoOptions *opt, const PopHeader *header,
+                   const int32_t *nt, const float *nv, const int32_t *ci,
+                   const TreeMeta *metas,
+                   const double *c, const double *xs, const double *ym,
+                   double *c_final_out, int32_t *status_out,
+                   double *loss_init_out, double *loss_final_out,
+                   int32_t *iters_out);
+
+/* Evaluate every expression at every point: y_out[m*N + i] = f_m(x_i; c_m)
+ * (counterpart of eval_kernel_batched, cusr/kernel/lm_core.cuh:108-125).
+ * precision: CO_PREC_FP64 or CO_PREC_MIXED (fp32 interpreter). */
+int co_eval_ex(void *handle, const PopHeader *header,
+               const int32_t *nt, const float *nv, const int32_t *ci,
+               const TreeMeta *metas, const double *c, const double *xs,
+               int precision, double *y_out);
+
+/* Host-only decode of a population, no device needed: runs every check
+ * co_optimize runs before touching the device and returns its code
+ * (0, 2, -2, -3, -4, -6). When it returns 0 and the pointers are non-NULL:
+ *   program_out[total_nodes]  one 64-bit instruction per node, in the order
+ *                             the device executes it (last node first);
+ *   order_out[M_prob]         expressions grouped by K ascending (stable),
+ *                             the launch order of the fit kernel;
+ *   bin_start_out[CO_MAX_K+2] start of each K bin in order_out, with
+ *                             bin_start_out[CO_MAX_K+1] == M_prob;
+ *   stack_out[M_prob]         value-stack depth each expression needs. */
+int co_decode(const PopHeader *header,
+              const int32_t *nt, const float *nv, const int32_t *ci,
+              const TreeMeta *metas,
+              uint64_t *program_out, int32_t *order_out,
+              int32_t *bin_start_out, int32_t *stack_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUSR_CO_H */

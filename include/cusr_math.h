@@ -1,0 +1,463 @@
+/* cusr_math.h -- portable fp64 / fp32 elementary functions.
+ *
+ * One implementation, compiled unchanged as C (host) and as HIP (gfx950
+ * device), so an expression evaluates to the same bits on the CPU and on the
+ * GPU. The fitter needs that: LM accept/reject decisions on near-ties follow
+ * the last bit, and a 1-ulp difference between two math libraries is enough
+ * to send a trajectory to another minimum.
+ *
+ * Only IEEE-exact building blocks are used: +, -, *, /, sqrt, fma (all
+ * correctly rounded on both sides), exponent bit manipulation, and integer
+ * rounding by the 1.5*2^52 (1.5*2^23) shift. Callers must compile with
+ * -ffp-contract=off so no other operation is fused. Methods (all published):
+ *   exp   Cody-Waite reduction x = k ln2 + r, |r| <= ln2/2 (ln2 split into a
+ *         32-bit head and a tail), Taylor series of e^r to r^13 (fp32: r^7),
+ *         scaling by 2^k through the exponent field, two steps near the ends.
+ *   log   x = 2^e m, m in (sqrt(1/2), sqrt(2)], f = m - 1, s = f/(2+f),
+ *         log(1+f) = f - (f^2/2 - s (f^2/2 + R)), R = 2 s^2/3 + 2 s^4/5 + ...
+ *         (the atanh series, rearranged as in Sun's fdlibm e_log.c), to s^23
+ *         (fp32: s^13).
+ *   sin/cos  k = rint(x 2/pi), r = x - k pi/2 with pi/2 split into three
+ *         doubles subtracted by fma (Cody-Waite); Taylor series on
+ *         [-pi/4, pi/4] to r^17 / r^18 (fp32: r^11 / r^12); cos uses the
+ *         compensated 1 - z/2 step of fdlibm k_cos.c; quadrant by k mod 4.
+ *         For |x| >= 2^50 (fp32: 2^21) the argument carries no phase
+ *         information in the format and the functions return sin = 0, cos = 1.
+ *   tan   sin/cos of the same reduction.
+ *   sinh, cosh, tanh  Taylor series for |x| < 1 (sinh), exp otherwise.
+ *   pow   exp(y log|x|) with the sign of x for integral y; its error grows
+ *         with |y log x| (no extra-precision log).
+ * Accuracy against the C library is checked by tests/test_math.py.
+ */
+#ifndef CUSR_MATH_H
+#define CUSR_MATH_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define CM_FN static inline __host__ __device__
+#else
+#define CM_FN static inline
+#endif
+
+#ifdef __cplusplus
+#define CM_FMA ::fma
+#define CM_FMAF ::fmaf
+#define CM_SQRT ::sqrt
+#define CM_SQRTF ::sqrtf
+#else
+#include <math.h>
+#define CM_FMA fma
+#define CM_FMAF fmaf
+#define CM_SQRT sqrt
+#define CM_SQRTF sqrtf
+#endif
+
+/* ------------------------------------------------------------ bit helpers */
+
+CM_FN uint64_t cm_bits(double x) { uint64_t u; __builtin_memcpy(&u, &x, 8); return u; }
+CM_FN double cm_dbl(uint64_t u) { double x; __builtin_memcpy(&x, &u, 8); return x; }
+CM_FN uint32_t cm_bitsf(float x) { uint32_t u; __builtin_memcpy(&u, &x, 4); return u; }
+CM_FN float cm_flt(uint32_t u) { float x; __builtin_memcpy(&x, &u, 4); return x; }
+
+#define CM_NAN cm_dbl(0x7ff8000000000000ULL)
+#define CM_INF cm_dbl(0x7ff0000000000000ULL)
+#define CM_NANF cm_flt(0x7fc00000u)
+#define CM_INFF cm_flt(0x7f800000u)
+
+CM_FN int cm_isnan(double x) { return x != x; }
+CM_FN double cm_fabs(double x) { return cm_dbl(cm_bits(x) & 0x7fffffffffffffffULL); }
+CM_FN float cm_fabsf(float x) { return cm_flt(cm_bitsf(x) & 0x7fffffffu); }
+
+/* nearest integer (ties to even) of |t| < 2^51, as a double */
+CM_FN double cm_rint_small(double t) {
+    const double shift = 6755399441055744.0; /* 1.5 * 2^52 */
+    double v = t + shift;
+    return v - shift;
+}
+CM_FN float cm_rint_smallf(float t) {
+    const float shift = 12582912.0f; /* 1.5 * 2^23 */
+    float v = t + shift;
+    return v - shift;
+}
+
+/* 2^k for a normal exponent k in [-1022, 1023] */
+CM_FN double cm_pow2i(int k) { return cm_dbl((uint64_t)(k + 1023) << 52); }
+CM_FN float cm_pow2if(int k) { return cm_flt((uint32_t)(k + 127) << 23); }
+
+/* ------------------------------------------------------------------- exp */
+
+CM_FN double cm_exp(double x) {
+    if (cm_isnan(x)) return x;
+    if (x > 709.782712893384) return CM_INF;
+    if (x < -745.1332191019412) return 0.0;
+    const double inv_ln2 = 1.4426950408889634;
+    const double ln2_hi = 0.6931471803691238;
+    const double ln2_lo = 1.9082149288430703e-10;
+    double kf = cm_rint_small(x * inv_ln2);
+    double r = CM_FMA(-kf, ln2_hi, x);
+    r = CM_FMA(-kf, ln2_lo, r);
+    double p = 1.6059043836821613e-10;            /* 1/13! */
+    p = CM_FMA(p, r, 2.08767569878681e-09);       /* 1/12! */
+    p = CM_FMA(p, r, 2.505210838544172e-08);
+    p = CM_FMA(p, r, 2.755731922398589e-07);
+    p = CM_FMA(p, r, 2.7557319223985893e-06);
+    p = CM_FMA(p, r, 2.48015873015873e-05);
+    p = CM_FMA(p, r, 0.0001984126984126984);
+    p = CM_FMA(p, r, 0.001388888888888889);
+    p = CM_FMA(p, r, 0.008333333333333333);
+    p = CM_FMA(p, r, 0.041666666666666664);
+    p = CM_FMA(p, r, 0.16666666666666666);
+    p = CM_FMA(p, r, 0.5);
+    p = CM_FMA(p, r, 1.0);
+    p = CM_FMA(p, r, 1.0);
+    int k = (int)kf;
+    if (k >= -1020 && k <= 1022) return p * cm_pow2i(k);
+    if (k > 1022) return (p * cm_pow2i(k - 2)) * 4.0;
+    return (p * cm_pow2i(k + 1000)) * cm_pow2i(-1000);
+}
+
+CM_FN float cm_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283f) return CM_INFF;
+    if (x < -103.97208f) return 0.0f;
+    const float inv_ln2 = 1.4426950216293335f;
+    const float ln2_hi = 0.693145751953125f;
+    const float ln2_lo = 1.4285906217992306e-06f;
+    float kf = cm_rint_smallf(x * inv_ln2);
+    float r = CM_FMAF(-kf, ln2_hi, x);
+    r = CM_FMAF(-kf, ln2_lo, r);
+    float p = 0.00019841270113829523f;            /* 1/7! */
+    p = CM_FMAF(p, r, 0.0013888889225199819f);
+    p = CM_FMAF(p, r, 0.008333333767950535f);
+    p = CM_FMAF(p, r, 0.0416666679084301f);
+    p = CM_FMAF(p, r, 0.1666666716337204f);
+    p = CM_FMAF(p, r, 0.5f);
+    p = CM_FMAF(p, r, 1.0f);
+    p = CM_FMAF(p, r, 1.0f);
+    int k = (int)kf;
+    if (k >= -124 && k <= 126) return p * cm_pow2if(k);
+    if (k > 126) return (p * cm_pow2if(k - 2)) * 4.0f;
+    return (p * cm_pow2if(k + 100)) * cm_pow2if(-100);
+}
+
+/* ------------------------------------------------------------------- log */
+
+CM_FN double cm_log(double x) {
+    if (cm_isnan(x)) return x;
+    if (x < 0.0) return CM_NAN;
+    if (x == 0.0) return -CM_INF;
+    if (x == CM_INF) return x;
+    uint64_t u = cm_bits(x);
+    int e = (int)((u >> 52) & 0x7ff);
+    if (e == 0) { /* subnormal */
+        u = cm_bits(x * 18014398509481984.0); /* 2^54 */
+        e = (int)((u >> 52) & 0x7ff) - 54;
+    }
+    e -= 1023;
+    double m = cm_dbl((u & 0x000fffffffffffffULL) | 0x3ff0000000000000ULL);
+    if (m > 1.4142135623730951) { m = m * 0.5; e += 1; }
+    double f = m - 1.0;
+    double s = f / (2.0 + f);
+    double z = s * s;
+    double R = 0.08695652173913043;               /* 2/23 */
+    R = CM_FMA(R, z, 0.09523809523809523);
+    R = CM_FMA(R, z, 0.10526315789473684);
+    R = CM_FMA(R, z, 0.11764705882352941);
+    R = CM_FMA(R, z, 0.13333333333333333);
+    R = CM_FMA(R, z, 0.15384615384615385);
+    R = CM_FMA(R, z, 0.18181818181818182);
+    R = CM_FMA(R, z, 0.2222222222222222);
+    R = CM_FMA(R, z, 0.2857142857142857);
+    R = CM_FMA(R, z, 0.4);
+    R = CM_FMA(R, z, 0.6666666666666666);
+    R = R * z;
+    double hfsq = 0.5 * (f * f);
+    double dk = (double)e;
+    const double ln2_hi = 0.6931471803691238;
+    const double ln2_lo = 1.9082149288430703e-10;
+    return dk * ln2_hi - ((hfsq - (s * (hfsq + R) + dk * ln2_lo)) - f);
+}
+
+CM_FN float cm_logf(float x) {
+    if (x != x) return x;
+    if (x < 0.0f) return CM_NANF;
+    if (x == 0.0f) return -CM_INFF;
+    if (x == CM_INFF) return x;
+    uint32_t u = cm_bitsf(x);
+    int e = (int)((u >> 23) & 0xff);
+    if (e == 0) {
+        u = cm_bitsf(x * 33554432.0f); /* 2^25 */
+        e = (int)((u >> 23) & 0xff) - 25;
+    }
+    e -= 127;
+    float m = cm_flt((u & 0x007fffffu) | 0x3f800000u);
+    if (m > 1.4142135381698608f) { m = m * 0.5f; e += 1; }
+    float f = m - 1.0f;
+    float s = f / (2.0f + f);
+    float z = s * s;
+    float R = 0.1538461595773697f;                /* 2/13 */
+    R = CM_FMAF(R, z, 0.1818181872367859f);
+    R = CM_FMAF(R, z, 0.2222222238779068f);
+    R = CM_FMAF(R, z, 0.2857142984867096f);
+    R = CM_FMAF(R, z, 0.4000000059604645f);
+    R = CM_FMAF(R, z, 0.6666666865348816f);
+    R = R * z;
+    float hfsq = 0.5f * (f * f);
+    float dk = (float)e;
+    const float ln2_hi = 0.693145751953125f;
+    const float ln2_lo = 1.4285906217992306e-06f;
+    return dk * ln2_hi - ((hfsq - (s * (hfsq + R) + dk * ln2_lo)) - f);
+}
+
+/* --------------------------------------------------------------- sin/cos */
+
+CM_FN double cm_sin_kernel(double r) {
+    double z = r * r;
+    double p = 2.8114572543455206e-15;            /* 1/17! */
+    p = CM_FMA(p, z, -7.647163731819816e-13);
+    p = CM_FMA(p, z, 1.6059043836821613e-10);
+    p = CM_FMA(p, z, -2.505210838544172e-08);
+    p = CM_FMA(p, z, 2.7557319223985893e-06);
+    p = CM_FMA(p, z, -0.0001984126984126984);
+    p = CM_FMA(p, z, 0.008333333333333333);
+    p = CM_FMA(p, z, -0.16666666666666666);
+    return CM_FMA(r * z, p, r);
+}
+
+CM_FN double cm_cos_kernel(double r) {
+    double z = r * r;
+    double p = -1.5619206968586225e-16;           /* -1/18! */
+    p = CM_FMA(p, z, 4.779477332387385e-14);
+    p = CM_FMA(p, z, -1.1470745597729725e-11);
+    p = CM_FMA(p, z, 2.08767569878681e-09);
+    p = CM_FMA(p, z, -2.755731922398589e-07);
+    p = CM_FMA(p, z, 2.48015873015873e-05);
+    p = CM_FMA(p, z, -0.001388888888888889);
+    p = CM_FMA(p, z, 0.041666666666666664);
+    double hz = 0.5 * z;
+    double w = 1.0 - hz;
+    return w + (((1.0 - w) - hz) + z * (z * p));
+}
+
+/* sin and cos of x from one argument reduction */
+CM_FN void cm_sincos(double x, double *s, double *c) {
+    if (cm_isnan(x) || cm_fabs(x) == CM_INF) { *s = CM_NAN; *c = CM_NAN; return; }
+    if (cm_fabs(x) >= 1125899906842624.0) { *s = 0.0; *c = 1.0; return; } /* 2^50 */
+    double kf = cm_rint_small(x * 0.6366197723675814);
+    double r = CM_FMA(-kf, 1.5707963267948966, x);
+    r = CM_FMA(-kf, 6.123233995736766e-17, r);
+    r = CM_FMA(-kf, -1.4973849048591698e-33, r);
+    double q4 = kf - 4.0 * cm_rint_small(kf * 0.25 - 0.375); /* kf mod 4, in 0..3 */
+    int q = (int)q4;
+    double sr = cm_sin_kernel(r), cr = cm_cos_kernel(r);
+    switch (q & 3) {
+    case 0: *s = sr; *c = cr; break;
+    case 1: *s = cr; *c = -sr; break;
+    case 2: *s = -sr; *c = -cr; break;
+    default: *s = -cr; *c = sr; break;
+    }
+}
+
+CM_FN double cm_sin(double x) { double s, c; cm_sincos(x, &s, &c); return s; }
+CM_FN double cm_cos(double x) { double s, c; cm_sincos(x, &s, &c); return c; }
+CM_FN double cm_tan(double x) { double s, c; cm_sincos(x, &s, &c); return s / c; }
+
+CM_FN float cm_sin_kernelf(float r) {
+    float z = r * r;
+    float p = -2.5052107943679403e-08f;           /* -1/11! */
+    p = CM_FMAF(p, z, 2.7557318844628753e-06f);
+    p = CM_FMAF(p, z, -0.00019841270113829523f);
+    p = CM_FMAF(p, z, 0.008333333767950535f);
+    p = CM_FMAF(p, z, -0.1666666716337204f);
+    return CM_FMAF(r * z, p, r);
+}
+
+CM_FN float cm_cos_kernelf(float r) {
+    float z = r * r;
+    float p = 2.0876755879584152e-09f;            /* 1/12! */
+    p = CM_FMAF(p, z, -2.755731998149713e-07f);
+    p = CM_FMAF(p, z, 2.4801587642286904e-05f);
+    p = CM_FMAF(p, z, -0.0013888889225199819f);
+    p = CM_FMAF(p, z, 0.0416666679084301f);
+    float hz = 0.5f * z;
+    float w = 1.0f - hz;
+    return w + (((1.0f - w) - hz) + z * (z * p));
+}
+
+CM_FN void cm_sincosf(float x, float *s, float *c) {
+    if (x != x || cm_fabsf(x) == CM_INFF) { *s = CM_NANF; *c = CM_NANF; return; }
+    if (cm_fabsf(x) >= 2097152.0f) { *s = 0.0f; *c = 1.0f; return; } /* 2^21 */
+    float kf = cm_rint_smallf(x * 0.6366197466850281f);
+    float r = CM_FMAF(-kf, 1.5707963705062866f, x);
+    r = CM_FMAF(-kf, -4.371138828673793e-08f, r);
+    r = CM_FMAF(-kf, -1.7151245100058819e-15f, r);
+    float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
+    int q = (int)q4;
+    float sr = cm_sin_kernelf(r), cr = cm_cos_kernelf(r);
+    switch (q & 3) {
+    case 0: *s = sr; *c = cr; break;
+    case 1: *s = cr; *c = -sr; break;
+    case 2: *s = -sr; *c = -cr; break;
+    default: *s = -cr; *c = sr; break;
+    }
+}
+
+CM_FN float cm_sinf(float x) { float s, c; cm_sincosf(x, &s, &c); return s; }
+CM_FN float cm_cosf(float x) { float s, c; cm_sincosf(x, &s, &c); return c; }
+CM_FN float cm_tanf(float x) { float s, c; cm_sincosf(x, &s, &c); return s / c; }
+
+/* ------------------------------------------------------ hyperbolic, pow */
+
+CM_FN double cm_sinh(double x) {
+    if (cm_isnan(x)) return x;
+    double a = cm_fabs(x);
+    double r;
+    if (a < 1.0) {
+        double z = a * a;
+        double p = 8.22063524662433e-18;          /* 1/19! */
+        p = CM_FMA(p, z, 2.8114572543455206e-15);
+        p = CM_FMA(p, z, 7.647163731819816e-13);
+        p = CM_FMA(p, z, 1.6059043836821613e-10);
+        p = CM_FMA(p, z, 2.505210838544172e-08);
+        p = CM_FMA(p, z, 2.7557319223985893e-06);
+        p = CM_FMA(p, z, 0.0001984126984126984);
+        p = CM_FMA(p, z, 0.008333333333333333);
+        p = CM_FMA(p, z, 0.16666666666666666);
+        r = CM_FMA(a * z, p, a);
+    } else if (a < 709.0) {
+        double e = cm_exp(a);
+        r = 0.5 * (e - 1.0 / e);
+    } else {
+        r = 2.0 * cm_exp(a - 1.3862943611198906); /* e^a / 2 = 2 e^(a - 2 ln 2) */
+    }
+    return x < 0.0 ? -r : r;
+}
+
+CM_FN double cm_cosh(double x) {
+    if (cm_isnan(x)) return x;
+    double a = cm_fabs(x);
+    if (a < 709.0) {
+        double e = cm_exp(a);
+        return 0.5 * (e + 1.0 / e);
+    }
+    return 2.0 * cm_exp(a - 1.3862943611198906);
+}
+
+CM_FN double cm_tanh(double x) {
+    if (cm_isnan(x)) return x;
+    double a = cm_fabs(x);
+    double r;
+    if (a < 0.55) {
+        r = cm_sinh(a) / cm_cosh(a);
+    } else if (a < 22.0) {
+        double e = cm_exp(2.0 * a);
+        r = 1.0 - 2.0 / (e + 1.0);
+    } else {
+        r = 1.0;
+    }
+    return x < 0.0 ? -r : r;
+}
+
+CM_FN float cm_sinhf(float x) {
+    if (x != x) return x;
+    float a = cm_fabsf(x);
+    float r;
+    if (a < 1.0f) {
+        float z = a * a;
+        float p = 2.5052107943679403e-08f;        /* 1/11! */
+        p = CM_FMAF(p, z, 2.7557318844628753e-06f);
+        p = CM_FMAF(p, z, 0.00019841270113829523f);
+        p = CM_FMAF(p, z, 0.008333333767950535f);
+        p = CM_FMAF(p, z, 0.1666666716337204f);
+        r = CM_FMAF(a * z, p, a);
+    } else if (a < 88.0f) {
+        float e = cm_expf(a);
+        r = 0.5f * (e - 1.0f / e);
+    } else {
+        r = 2.0f * cm_expf(a - 1.3862943611198906f);
+    }
+    return x < 0.0f ? -r : r;
+}
+
+CM_FN float cm_coshf(float x) {
+    if (x != x) return x;
+    float a = cm_fabsf(x);
+    if (a < 88.0f) {
+        float e = cm_expf(a);
+        return 0.5f * (e + 1.0f / e);
+    }
+    return 2.0f * cm_expf(a - 1.3862943611198906f);
+}
+
+CM_FN float cm_tanhf(float x) {
+    if (x != x) return x;
+    float a = cm_fabsf(x);
+    float r;
+    if (a < 0.55f) {
+        r = cm_sinhf(a) / cm_coshf(a);
+    } else if (a < 9.0f) {
+        float e = cm_expf(2.0f * a);
+        r = 1.0f - 2.0f / (e + 1.0f);
+    } else {
+        r = 1.0f;
+    }
+    return x < 0.0f ? -r : r;
+}
+
+/* is y an integer, and if so is it odd */
+CM_FN int cm_int_kind(double y) {
+    double a = cm_fabs(y);
+    if (a >= 9007199254740992.0) return 2;     /* 2^53: even integer */
+    double t = cm_rint_small(a);
+    if (t != a) return 0;                      /* not an integer */
+    double h = cm_rint_small(a * 0.5);
+    return (h * 2.0 == a) ? 2 : 1;             /* 2 even, 1 odd */
+}
+
+CM_FN double cm_pow(double x, double y) {
+    if (y == 0.0) return 1.0;
+    if (x == 1.0) return 1.0;
+    if (cm_isnan(x) || cm_isnan(y)) return CM_NAN;
+    int kind = cm_int_kind(y);
+    double ax = cm_fabs(x);
+    double sign = 1.0;
+    if (x < 0.0 || (x == 0.0 && (cm_bits(x) >> 63))) {
+        if (x != 0.0 && kind == 0) return CM_NAN;
+        if (kind == 1) sign = -1.0;
+    }
+    if (ax == 0.0) return (y < 0.0) ? sign * CM_INF : sign * 0.0;
+    if (ax == CM_INF) return (y < 0.0) ? sign * 0.0 : sign * CM_INF;
+    if (y == CM_INF) return (ax < 1.0) ? 0.0 : CM_INF;
+    if (y == -CM_INF) return (ax < 1.0) ? CM_INF : 0.0;
+    return sign * cm_exp(y * cm_log(ax));
+}
+
+CM_FN int cm_int_kindf(float y) {
+    float a = cm_fabsf(y);
+    if (a >= 16777216.0f) return 2;
+    float t = cm_rint_smallf(a);
+    if (t != a) return 0;
+    float h = cm_rint_smallf(a * 0.5f);
+    return (h * 2.0f == a) ? 2 : 1;
+}
+
+CM_FN float cm_powf(float x, float y) {
+    if (y == 0.0f) return 1.0f;
+    if (x == 1.0f) return 1.0f;
+    if (x != x || y != y) return CM_NANF;
+    int kind = cm_int_kindf(y);
+    float ax = cm_fabsf(x);
+    float sign = 1.0f;
+    if (x < 0.0f || (x == 0.0f && (cm_bitsf(x) >> 31))) {
+        if (x != 0.0f && kind == 0) return CM_NANF;
+        if (kind == 1) sign = -1.0f;
+    }
+    if (ax == 0.0f) return (y < 0.0f) ? sign * CM_INFF : sign * 0.0f;
+    if (ax == CM_INFF) return (y < 0.0f) ? sign * 0.0f : sign * CM_INFF;
+    if (y == CM_INFF) return (ax < 1.0f) ? 0.0f : CM_INFF;
+    if (y == -CM_INFF) return (ax < 1.0f) ? CM_INFF : 0.0f;
+    return sign * cm_expf(y * cm_logf(ax));
+}
+
+#endif /* CUSR_MATH_H */

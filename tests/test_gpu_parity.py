@@ -1,0 +1,132 @@
+"""HIP path vs the CPU oracle on the same seeded inputs (called through the C ABI).
+
+Tolerances: final loss relative 1e-9 for fp64 fits and
+1e-4 for mixed-precision fits; statuses agree on >= 99.9% of expressions.
+"""
+import numpy as np
+import pytest
+
+from oracle import lm_oracle
+from tests.helpers import f64, ref_pop, rel_diff, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _fit_both(co, pop, max_iter, ad_mode=0, precision=0):
+    c0, xs, ym = f64(pop)
+    _say(f"case M={pop['M']} N={pop['N']} ad={ad_mode} prec={precision} max_iter={max_iter}")
+    g = co.optimize_ex(pop, max_iter, ad_mode=ad_mode, precision=precision)
+    o = lm_oracle.fit(pop, max_iter=max_iter, ad_mode=ad_mode, precision=precision)
+    return g, o
+
+
+def _report(g, o):
+    st_agree = float(np.mean(g["status"] == o["status"]))
+    d = rel_diff(g["loss_final"], o["loss_final"])
+    return st_agree, d
+
+
+@pytest.mark.parametrize("name,M,N", [("C1", 256, 256), ("C2", 128, 512)])
+def test_eval_matches_oracle(co, name, M, N):
+    pop, c_true = synth(name, M, N)
+    c0, xs, _ = f64(pop)
+    _say(f"eval {name} M={M} N={N}")
+    yg = co.evaluate(pop, c0, xs)
+    yo = lm_oracle.eval_pop(pop, c=c0, xs=xs)
+    # libm and ROCm transcendentals may differ in the last bit; compare each
+    # value against the scale of its row so cancellation does not inflate it
+    scale = np.maximum(np.max(np.abs(yo), axis=1, keepdims=True), 1e-300)
+    d = np.abs(yg - yo) / scale
+    _say(f"eval exact fraction {np.mean(yg == yo):.6f} max scaled diff {d.max():.3e}")
+    assert np.array_equal(np.isfinite(yg), np.isfinite(yo))
+    assert np.nanmax(d) < 1e-13
+
+
+@pytest.mark.parametrize("ad_mode", [0, 1])
+def test_fit_fp64_c1(co, ad_mode):
+    pop, _ = synth("C1", 512, 256)
+    g, o = _fit_both(co, pop, 20, ad_mode=ad_mode)
+    st, d = _report(g, o)
+    _say(f"status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
+    assert np.mean(d <= 1e-9) >= 0.999
+    assert st >= 0.999
+
+
+def test_fit_fp64_c2_small(co):
+    pop, _ = synth("C2", 256, 1024)
+    g, o = _fit_both(co, pop, 50)
+    st, d = _report(g, o)
+    _say(f"status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
+    assert np.mean(d <= 1e-9) >= 0.999
+    assert st >= 0.996
+
+
+def test_fit_mixed_c5_small(co):
+    pop, _ = synth("C5", 256, 512)
+    g, o = _fit_both(co, pop, 10, precision=1)
+    st, d = _report(g, o)
+    _say(f"mixed: status agree {st:.4f}; loss rel max {d.max():.3e}")
+    assert np.mean(d <= 1e-4) >= 0.99
+
+
+def test_reference_fixture_recovers_truth(co):
+    import json
+    from tests.helpers import REF_FIX
+    pop = ref_pop("pop_fixture.bin")
+    truth = json.loads((REF_FIX / "pop_fixture_truth.json").read_text())
+    _say("pop_fixture.bin")
+    r = co.optimize(pop, 50)
+    for fx in truth["fixtures"]:
+        k0, K = fx["c_offset"], fx["K"]
+        got = r["c_final"][k0:k0 + K].astype(np.float64)
+        want = np.asarray(fx["c_true"])
+        assert np.all(np.abs(got - want) / np.abs(want) < 5e-3), (fx["name"], got, want)
+    assert list(r["status"]) == [0, 0, 0]
+
+
+def test_stress_fixture_statuses(co):
+    import json
+    from tests.helpers import REF_FIX
+    pop = ref_pop("pop_fixture_stress.bin")
+    truth = json.loads((REF_FIX / "pop_fixture_stress_truth.json").read_text())
+    _say("pop_fixture_stress.bin")
+    r = co.optimize(pop, 50)
+    assert list(r["status"]) == [f["expect_status"] for f in truth["fixtures"]]
+
+
+def _op_pop(N, seed):
+    """One expression per operator applied to inputs x0 (and x1), K = 0."""
+    from cusr_amd.benchmark import popio
+    rng = np.random.default_rng(seed)
+    unary = [14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 33, 34, 35]
+    binary = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 32]
+    trees = []
+    for f in unary:
+        trees.append(([2, 0], [f, 0], [-1, -1], []))
+    for f in binary:
+        trees.append(([3, 0, 0], [f, 0, 1], [-1, -1, -1], []))
+    # wide magnitudes, both signs, some exact zeros and tiny values
+    mag = 10.0 ** rng.uniform(-12, 3, size=(N, 2))
+    xs = (mag * rng.choice([-1.0, 1.0], size=(N, 2))).astype(np.float32)
+    xs[::17, 1] = 0.0
+    xs[::23, 0] = 0.0
+    pop = popio.build_pop(trees, xs, np.zeros((len(trees), N)))
+    return pop, unary + binary
+
+
+@pytest.mark.parametrize("precision", [0, 1])
+def test_operators_bit_exact(co, precision):
+    """Every operator, device vs oracle, on wide-range inputs: identical bits."""
+    pop, ops = _op_pop(4096, 7)
+    xs = pop["xs"].astype(np.float64)
+    _say(f"operators precision={precision}")
+    yg = co.evaluate(pop, np.zeros(1), xs, precision=precision)
+    yo = lm_oracle.eval_pop(pop, c=np.zeros(1), xs=xs, precision=precision)
+    same = (yg == yo) | (np.isnan(yg) & np.isnan(yo))
+    bad = [(ops[m], int(np.sum(~same[m]))) for m in range(len(ops)) if not same[m].all()]
+    _say(f"mismatching ops (id, count): {bad}")
+    assert not bad
