@@ -69,6 +69,10 @@ struct Ctx {
     hipStream_t lanes[kStreams] = {};
     hipEvent_t ev_start = nullptr;
     hipEvent_t ev_done[kStreams] = {};
+    hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr;  // timing pair around the fit launches
+    Plan plan = {};
+    bool resident = false;
+    double last_kernel_ms = -1.0;
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
     std::vector<uint64_t> h_prog;
     std::vector<ExprDesc> h_desc;
@@ -112,27 +116,21 @@ T *ptr(DevBuf &b) { return (T *)b.p; }
 
 unsigned blocks_for(size_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
 
-// Shared body of co_optimize / co_optimize_ex. Inputs c/xs/ym are either fp32
-// (in32) or fp64 host arrays; outputs are fp64 host arrays (sized by header).
-int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t *nt,
-               const float *nv, const int32_t *ci, const TreeMeta *metas, const void *c,
-               const void *xs, const void *ym, bool in32, double *c_out, int32_t *status_out,
-               double *li_out, double *lf_out, int32_t *iters_out) {
-    const double t0 = now_ms();
+// Check, decode and upload one population into the context (fp32 or fp64
+// host inputs); the population stays resident until the next upload.
+int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const float *nv,
+                      const int32_t *ci, const TreeMeta *metas, const void *c, const void *xs,
+                      const void *ym, bool in32) {
     CO_HIP(hipSetDevice(ctx->device));
-    if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
-    if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
-    if (opt.max_iter < 0) return CO_ERR_NULLARG;
+    ctx->resident = false;
     const int M = h->M_prob;
     ctx->h_prog.resize(h->total_nodes > 0 ? h->total_nodes : 1);
     ctx->h_desc.resize(M > 0 ? M : 1);
-    Plan plan;
     int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
-                               ctx->h_desc.data(), nullptr, &plan);
+                               ctx->h_desc.data(), nullptr, &ctx->plan);
     if (rc != CO_OK) return rc;
     if (M == 0) {
-        g_setup_ms = now_ms() - t0;
-        g_loop_ms = 0.0;
+        ctx->resident = true;
         return CO_OK;
     }
     const int N = h->N, D = h->n_vars, C = h->total_c;
@@ -187,8 +185,25 @@ int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t
         if (C) CO_HIP(hipMemcpyAsync(ctx->C0.p, c, 8 * (size_t)C, hipMemcpyHostToDevice, s));
     }
     CO_HIP(hipStreamSynchronize(s));
-    const double t1 = now_ms();
+    ctx->resident = true;
+    return CO_OK;
+}
 
+// Fit the resident population; copy results to the host pointers that are
+// non-null (c_out and status_out too may be null: results then stay on the
+// device). Returns after the device work and copies are complete.
+int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, double *li_out,
+            double *lf_out, int32_t *iters_out) {
+    if (!ctx->resident) return CO_ERR_NULLARG;
+    if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
+    if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
+    if (opt.max_iter < 0) return CO_ERR_NULLARG;
+    CO_HIP(hipSetDevice(ctx->device));
+    const Plan &plan = ctx->plan;
+    const int M = plan.M, C = plan.total_c;
+    ctx->last_kernel_ms = 0.0;
+    if (M == 0) return CO_OK;
+    hipStream_t s = ctx->stream;
     FitArgs fa;
     fa.prog = ptr<uint64_t>(ctx->prog);
     fa.desc = ptr<ExprDesc>(ctx->desc);
@@ -200,8 +215,8 @@ int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t
     fa.loss_init = ptr<double>(ctx->li);
     fa.loss_final = ptr<double>(ctx->lf);
     fa.iters = ptr<int32_t>(ctx->iters);
-    fa.N = N;
-    fa.D = D;
+    fa.N = plan.N;
+    fa.D = plan.D;
     fa.max_iter = opt.max_iter;
     fa.guard = opt.fp64_guard ? 1 : 0;
     fa.lambda0 = opt.lambda0;
@@ -210,12 +225,13 @@ int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t
     const bool rev = opt.ad_mode == CO_AD_REVERSE;
     const bool mixed = opt.precision == CO_PREC_MIXED;
     const size_t tape_bytes = rev ? (size_t)plan.max_tape * kLanes * (mixed ? 4 : 8) : 0;
-    // descriptors are in launch order, largest K first; one launch per K bin,
-    // bins spread over the context's streams so their tails overlap
     const FitLauncher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
                                      : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
-    int pos = 0, nb = 0;
+    // descriptors are in launch order, largest K first; one launch per K bin,
+    // bins spread over the context's streams so their tails overlap
+    CO_HIP(hipEventRecord(ctx->ev_t0, s));
     CO_HIP(hipEventRecord(ctx->ev_start, s));
+    int pos = 0, nb = 0;
     for (int k = CO_MAX_K; k >= 0; --k) {
         int cnt = 0;
         while (pos + cnt < M && ctx->h_desc[pos + cnt].K == k) ++cnt;
@@ -232,17 +248,37 @@ int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t
         CO_HIP(hipEventRecord(ctx->ev_done[i], ctx->lanes[i]));
         CO_HIP(hipStreamWaitEvent(s, ctx->ev_done[i], 0));
     }
-
-    if (C) CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, hipMemcpyDeviceToHost, s));
-    CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M, hipMemcpyDeviceToHost, s));
+    CO_HIP(hipEventRecord(ctx->ev_t1, s));
+    if (c_out && C) CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, hipMemcpyDeviceToHost, s));
+    if (status_out)
+        CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M, hipMemcpyDeviceToHost, s));
     if (li_out) CO_HIP(hipMemcpyAsync(li_out, ctx->li.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
     if (lf_out) CO_HIP(hipMemcpyAsync(lf_out, ctx->lf.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
     if (iters_out)
         CO_HIP(hipMemcpyAsync(iters_out, ctx->iters.p, 4 * (size_t)M, hipMemcpyDeviceToHost, s));
     CO_HIP(hipStreamSynchronize(s));
+    float ms = 0.0f;
+    CO_HIP(hipEventElapsedTime(&ms, ctx->ev_t0, ctx->ev_t1));
+    ctx->last_kernel_ms = ms;
+    return CO_OK;
+}
+
+// Shared body of co_optimize / co_optimize_ex: upload, fit, read back.
+int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t *nt,
+               const float *nv, const int32_t *ci, const TreeMeta *metas, const void *c,
+               const void *xs, const void *ym, bool in32, double *c_out, int32_t *status_out,
+               double *li_out, double *lf_out, int32_t *iters_out) {
+    const double t0 = now_ms();
+    if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
+    if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
+    if (opt.max_iter < 0) return CO_ERR_NULLARG;
+    int rc = upload_population(ctx, h, nt, nv, ci, metas, c, xs, ym, in32);
+    if (rc != CO_OK) return rc;
+    const double t1 = now_ms();
+    rc = run_fit(ctx, opt, c_out, status_out, li_out, lf_out, iters_out);
     g_setup_ms = t1 - t0;
     g_loop_ms = now_ms() - t1;
-    return CO_OK;
+    return rc;
 }
 
 }  // namespace
@@ -271,6 +307,8 @@ extern "C" int co_init(int device_id, void **handle_out) {
     for (int i = 0; i < kStreams && e == hipSuccess; ++i)
         e = hipStreamCreateWithFlags(&ctx->lanes[i], hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t0);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t1);
     for (int i = 0; i < kStreams && e == hipSuccess; ++i)
         e = hipEventCreateWithFlags(&ctx->ev_done[i], hipEventDisableTiming);
     if (e != hipSuccess) {
@@ -331,6 +369,7 @@ extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, c
     if (precision != CO_PREC_FP64 && precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
     Ctx *ctx = (Ctx *)handle;
     CO_HIP(hipSetDevice(ctx->device));
+    ctx->resident = false;  // the evaluation reuses the population buffers
     const int M = h->M_prob;
     ctx->h_prog.resize(h->total_nodes > 0 ? h->total_nodes : 1);
     ctx->h_desc.resize(M > 0 ? M : 1);
@@ -389,6 +428,31 @@ extern "C" int co_decode(const PopHeader *h, const int32_t *nt, const float *nv,
                              stack_out, nullptr);
 }
 
+extern "C" int co_upload_ex(void *handle, const PopHeader *h, const int32_t *nt,
+                            const float *nv, const int32_t *ci, const TreeMeta *metas,
+                            const double *c, const double *xs, const double *ym) {
+    if (!handle || !h || !nt || !nv || !ci || !metas || !c || !xs || !ym) return CO_ERR_NULLARG;
+    return upload_population((Ctx *)handle, h, nt, nv, ci, metas, c, xs, ym, false);
+}
+
+extern "C" int co_fit_resident(void *handle, const CoOptions *opt, double *c_final_out,
+                               int32_t *status_out, double *loss_init_out,
+                               double *loss_final_out, int32_t *iters_out) {
+    if (!handle || !opt || opt->struct_size != (int32_t)sizeof(CoOptions)) return CO_ERR_NULLARG;
+    const double t0 = now_ms();
+    int rc = run_fit((Ctx *)handle, *opt, c_final_out, status_out, loss_init_out, loss_final_out,
+                     iters_out);
+    g_setup_ms = 0.0;
+    g_loop_ms = now_ms() - t0;
+    return rc;
+}
+
+extern "C" int co_last_kernel_ms(void *handle, double *fit_ms_out) {
+    if (!handle || !fit_ms_out) return CO_ERR_NULLARG;
+    *fit_ms_out = ((Ctx *)handle)->last_kernel_ms;
+    return CO_OK;
+}
+
 extern "C" int co_last_split(double *setup_ms_out, double *loop_ms_out) {
     if (setup_ms_out) *setup_ms_out = g_setup_ms;
     if (loop_ms_out) *loop_ms_out = g_loop_ms;
@@ -409,5 +473,7 @@ extern "C" void co_teardown(void *handle) {
         if (ctx->ev_done[i]) (void)hipEventDestroy(ctx->ev_done[i]);
     }
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
+    if (ctx->ev_t0) (void)hipEventDestroy(ctx->ev_t0);
+    if (ctx->ev_t1) (void)hipEventDestroy(ctx->ev_t1);
     delete ctx;
 }

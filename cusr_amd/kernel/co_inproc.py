@@ -94,7 +94,8 @@ _HERE = Path(__file__).resolve().parent
 
 # every extern "C" symbol of include/cusr_co.h
 EXPORTED = ("co_init", "co_optimize", "co_last_split", "co_teardown", "co_options_default",
-            "co_optimize_ex", "co_eval_ex", "co_decode")
+            "co_optimize_ex", "co_eval_ex", "co_upload_ex", "co_fit_resident",
+            "co_last_kernel_ms", "co_decode")
 
 
 def lib_path(variant: str = "ad") -> Path:
@@ -137,6 +138,12 @@ def _bind(lib) -> None:
     lib.co_optimize_ex.restype = ctypes.c_int
     lib.co_eval_ex.argtypes = [_VP, ctypes.POINTER(PopHeader)] + [_VP] * 6 + [ctypes.c_int, _VP]
     lib.co_eval_ex.restype = ctypes.c_int
+    lib.co_upload_ex.argtypes = [_VP, ctypes.POINTER(PopHeader)] + [_VP] * 7
+    lib.co_upload_ex.restype = ctypes.c_int
+    lib.co_fit_resident.argtypes = [_VP, ctypes.POINTER(CoOptions)] + [_VP] * 5
+    lib.co_fit_resident.restype = ctypes.c_int
+    lib.co_last_kernel_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
+    lib.co_last_kernel_ms.restype = ctypes.c_int
     lib.co_decode.argtypes = [ctypes.POINTER(PopHeader)] + [_VP] * 8
     lib.co_decode.restype = ctypes.c_int
     lib.co_last_split.argtypes = [ctypes.POINTER(dbl), ctypes.POINTER(dbl)]
@@ -204,6 +211,7 @@ class InProcessCO:
         self._lib = load_library(variant, lib_path)
         self._handle = _VP()
         self._torn = False
+        self._resident = (0, 0)
         rc = self._lib.co_init(self.device_id, ctypes.byref(self._handle))
         if rc != CO_OK:
             raise COError(rc, "co_init")
@@ -297,6 +305,60 @@ class InProcessCO:
         if rc != CO_OK:
             raise COError(rc, "co_eval_ex")
         return y[:M, :N]
+
+    def upload(self, pop: dict, *, c_init=None, xs=None, ym=None) -> None:
+        """Make pop resident on the device for fit_resident() (fp64 inputs)."""
+        self._check()
+        h = _header(pop)
+        nt, pnt = _arr(pop["nt"], np.int32)
+        nv, pnv = _arr(pop["nv"], np.float32)
+        ci, pci = _arr(pop["ci"], np.int32)
+        me, pme = _metas(pop)
+        c0, pc0 = _arr(pop["c_init"] if c_init is None else c_init, np.float64)
+        if c0.size == 0:
+            c0, pc0 = _arr(np.zeros(1), np.float64)
+        x, px = _arr(pop["xs"] if xs is None else xs, np.float64)
+        y, py = _arr(pop["ym"] if ym is None else ym, np.float64)
+        rc = self._lib.co_upload_ex(self._handle, ctypes.byref(h), pnt, pnv, pci, pme, pc0, px, py)
+        if rc != CO_OK:
+            raise COError(rc, "co_upload_ex")
+        self._resident = (int(pop["M"]), int(pop["total_c"]))
+
+    def fit_resident(self, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
+                     precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
+                     fp64_guard: bool = True, outputs: bool = True):
+        """Fit the uploaded population again; outputs=False leaves results on the device."""
+        self._check()
+        M, C = self._resident
+        o = default_options(ad_mode=int(ad_mode), precision=int(precision),
+                            max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
+                            fp64_guard=1 if fp64_guard else 0)
+        if not outputs:
+            rc = self._lib.co_fit_resident(self._handle, ctypes.byref(o), None, None, None, None, None)
+            if rc != CO_OK:
+                raise COError(rc, "co_fit_resident")
+            return None
+        out = {"c_final": np.zeros(max(C, 1)), "status": np.zeros(max(M, 1), np.int32),
+               "loss_init": np.zeros(max(M, 1)), "loss_final": np.zeros(max(M, 1)),
+               "iters": np.zeros(max(M, 1), np.int32)}
+        rc = self._lib.co_fit_resident(
+            self._handle, ctypes.byref(o),
+            *(out[k].ctypes.data_as(_VP) for k in
+              ("c_final", "status", "loss_init", "loss_final", "iters")))
+        if rc != CO_OK:
+            raise COError(rc, "co_fit_resident")
+        out["c_final"] = out["c_final"][:C]
+        for k in ("status", "loss_init", "loss_final", "iters"):
+            out[k] = out[k][:M]
+        return out
+
+    def last_kernel_ms(self) -> float:
+        """Device time of the last fit (HIP events on the library's stream)."""
+        v = ctypes.c_double(-1.0)
+        rc = self._lib.co_last_kernel_ms(self._handle, ctypes.byref(v))
+        if rc != CO_OK:
+            raise COError(rc, "co_last_kernel_ms")
+        return v.value
 
     def last_split(self):
         """(setup_ms, loop_ms) of the last fit on this process."""

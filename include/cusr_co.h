@@ -119,13 +119,34 @@ int co_eval_ex(void *handle, const PopHeader *header,
                const TreeMeta *metas, const double *c, const double *xs,
                int precision, double *y_out);
 
+/* Decode and upload a population (fp64 inputs as in co_optimize_ex) into the
+ * handle's device buffers, where it stays resident for co_fit_resident until
+ * the next upload, co_optimize* or co_eval_ex call on the handle. Returns the
+ * codes of co_optimize. */
+int co_upload_ex(void *handle, const PopHeader *header,
+                 const int32_t *nt, const float *nv, const int32_t *ci,
+                 const TreeMeta *metas,
+                 const double *c, const double *xs, const double *ym);
+
+/* Fit the resident population from its uploaded starting constants. Output
+ * pointers (all may be NULL; results then stay on the device) are as in
+ * co_optimize_ex. CO_ERR_NULLARG when nothing is resident. */
+int co_fit_resident(void *handle, const CoOptions *opt,
+                    double *c_final_out, int32_t *status_out,
+                    double *loss_init_out, double *loss_final_out,
+                    int32_t *iters_out);
+
+/* Device time of the last fit on the handle, from HIP events recorded on the
+ * handle's stream before the first and after the last fit kernel. */
+int co_last_kernel_ms(void *handle, double *fit_ms_out);
+
 /* Host-only decode of a population, no device needed: runs every check
  * co_optimize runs before touching the device and returns its code
  * (0, 2, -2, -3, -4, -6). When it returns 0 and the pointers are non-NULL:
  *   program_out[total_nodes]  one 64-bit instruction per node, in the order
  *                             the device executes it (last node first);
- *   order_out[M_prob]         expressions grouped by K ascending (stable),
- *                             the launch order of the fit kernel;
+ *   order_out[M_prob]         expressions grouped by K ascending (stable);
+ *                             the fit launches these bins largest K first;
  *   bin_start_out[CO_MAX_K+2] start of each K bin in order_out, with
  *                             bin_start_out[CO_MAX_K+1] == M_prob;
  *   stack_out[M_prob]         value-stack depth each expression needs. */
