@@ -116,6 +116,21 @@ T *ptr(DevBuf &b) { return (T *)b.p; }
 
 unsigned blocks_for(size_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
 
+// dynamic LDS per workgroup the fit kernels may request
+constexpr size_t kMaxDynLds = 64 * 1024;
+
+size_t fit_lds_bytes(bool mixed, bool rev, int K, int D, int slots, int tape) {
+    const bool small = K <= 8;
+    if (mixed) {
+        if (rev) return fit_lds_bytes_t<float, 1, CO_AD_REVERSE>(D, slots, tape);
+        return small ? fit_lds_bytes_t<float, 1, CO_AD_FORWARD>(D, slots, tape)
+                     : fit_lds_bytes_t<float, 16, CO_AD_FORWARD>(D, slots, tape);
+    }
+    if (rev) return fit_lds_bytes_t<double, 1, CO_AD_REVERSE>(D, slots, tape);
+    return small ? fit_lds_bytes_t<double, 1, CO_AD_FORWARD>(D, slots, tape)
+                 : fit_lds_bytes_t<double, 16, CO_AD_FORWARD>(D, slots, tape);
+}
+
 // Check, decode and upload one population into the context (fp32 or fp64
 // host inputs); the population stays resident until the next upload.
 int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const float *nv,
@@ -127,7 +142,7 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
     ctx->h_prog.resize(h->total_nodes > 0 ? h->total_nodes : 1);
     ctx->h_desc.resize(M > 0 ? M : 1);
     int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
-                               ctx->h_desc.data(), nullptr, &ctx->plan);
+                               ctx->h_desc.data(), nullptr, nullptr, &ctx->plan);
     if (rc != CO_OK) return rc;
     if (M == 0) {
         ctx->resident = true;
@@ -221,10 +236,8 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     fa.guard = opt.fp64_guard ? 1 : 0;
     fa.lambda0 = opt.lambda0;
     fa.xtol = opt.xtol;
-    fa.tape_slots = plan.max_tape;
     const bool rev = opt.ad_mode == CO_AD_REVERSE;
     const bool mixed = opt.precision == CO_PREC_MIXED;
-    const size_t tape_bytes = rev ? (size_t)plan.max_tape * kLanes * (mixed ? 4 : 8) : 0;
     const FitLauncher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
                                      : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
     // descriptors are in launch order, largest K first; one launch per K bin,
@@ -233,14 +246,24 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     CO_HIP(hipEventRecord(ctx->ev_start, s));
     int pos = 0, nb = 0;
     for (int k = CO_MAX_K; k >= 0; --k) {
-        int cnt = 0;
-        while (pos + cnt < M && ctx->h_desc[pos + cnt].K == k) ++cnt;
+        int cnt = 0, slots = 0, tape = 0;
+        while (pos + cnt < M && ctx->h_desc[pos + cnt].K == k) {
+            const ExprDesc &d = ctx->h_desc[pos + cnt];
+            if (d.slots > slots) slots = d.slots;
+            if (d.tape > tape) tape = d.tape;
+            ++cnt;
+        }
         if (cnt == 0) continue;
+        if (!rev) tape = 0;
+        const size_t lds = fit_lds_bytes(mixed, rev, k, plan.D, slots, tape);
+        if (lds > kMaxDynLds) return CO_ERR_BOUNDS;
         hipStream_t ks = ctx->lanes[nb % kStreams];
         if (nb < kStreams) CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
         FitArgs fk = fa;
         fk.desc = fa.desc + pos;
-        CO_HIP(launch(k, (unsigned)cnt, tape_bytes, ks, fk));
+        fk.slots = slots;
+        fk.tape = tape;
+        CO_HIP(launch(k, (unsigned)cnt, lds, ks, fk));
         pos += cnt;
         ++nb;
     }
@@ -374,7 +397,7 @@ extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, c
     ctx->h_prog.resize(h->total_nodes > 0 ? h->total_nodes : 1);
     ctx->h_desc.resize(M > 0 ? M : 1);
     int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
-                               ctx->h_desc.data(), nullptr, nullptr);
+                               ctx->h_desc.data(), nullptr, nullptr, nullptr);
     if (rc != CO_OK || M == 0) return rc;
     const int N = h->N, D = h->n_vars, C = h->total_c;
     const size_t nX = (size_t)N * D, nY = (size_t)M * N;
@@ -404,10 +427,14 @@ extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, c
     ea.Yout = ptr<double>(ctx->Y);
     ea.N = N;
     ea.D = D;
+    int slots = 0;
+    for (int m = 0; m < M; m++)
+        if (ctx->h_desc[m].slots > slots) slots = ctx->h_desc[m].slots;
+    const size_t lds = (size_t)(D + slots) * kLanes * (precision == CO_PREC_FP64 ? 8 : 4);
     if (precision == CO_PREC_FP64)
-        eval_kernel<double><<<M, kLanes, 0, s>>>(ea);
+        eval_kernel<double><<<M, kLanes, lds, s>>>(ea);
     else
-        eval_kernel<float><<<M, kLanes, 0, s>>>(ea);
+        eval_kernel<float><<<M, kLanes, lds, s>>>(ea);
     CO_HIP(hipGetLastError());
     if (nY) CO_HIP(hipMemcpyAsync(y_out, ctx->Y.p, 8 * nY, hipMemcpyDeviceToHost, s));
     CO_HIP(hipStreamSynchronize(s));
@@ -425,7 +452,7 @@ extern "C" int co_decode(const PopHeader *h, const int32_t *nt, const float *nv,
         prog = tmp.data();
     }
     return decode_population(h, nt, nv, ci, metas, prog, order_out, bin_start_out, nullptr,
-                             stack_out, nullptr);
+                             stack_out, nullptr, nullptr);
 }
 
 extern "C" int co_upload_ex(void *handle, const PopHeader *h, const int32_t *nt,

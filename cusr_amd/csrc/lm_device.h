@@ -2,24 +2,30 @@
 //
 // One 64-lane wavefront owns one expression for the whole fit
 // (cusr/kernel/batch_lm_ad.cu:350-495 runs one host loop over all trees
-// instead). Lane l evaluates points l, l+64, l+128, ... of the expression;
-// the opcode stream is wave-uniform, so every branch of the interpreter is a
-// scalar branch and all 64 lanes stay converged. Per point a lane computes the
-// value and the gradient row, and folds r^2, J^T r and the upper triangle of
-// J^T J into registers; a butterfly over the 64 lanes then gives every lane
-// the same sums, and every lane solves the same damped K x K system, so the
-// accept/reject and lambda update run on the device with no host round trip.
+// instead). Lane l evaluates points l, l+64, l+128, ... of the expression, P
+// of them per pass of the interpreter; the program (program.h) is read with
+// scalar loads and every branch on it is a scalar branch, so the 64 lanes stay
+// converged and the fetch/decode cost is shared by 64*P points. Per point a
+// lane computes the value and the gradient row and folds r^2, J^T r and the
+// upper triangle of J^T J into registers; a butterfly over the 64 lanes then
+// gives every lane the same sums, and every lane solves the same damped
+// K x K system, so accept/reject and the lambda update stay on the device.
 //
 // Arithmetic follows one fixed order, which the CPU oracle reproduces:
 //   * lane l sums its points in ascending order from 0.0, fma(a, b, acc);
 //   * lanes combine with strides 32, 16, 8, 4, 2, 1;
-//   * operator values and partials use the formulas of op_unary/op_binary;
+//   * operator values and partials use the formulas of unary_p/binary_p and
+//     the elementary functions of include/cusr_math.h;
 //   * no fma contraction except where fma() is written (-ffp-contract=off).
 //
 // A trial point is evaluated with its Jacobian: after an accept the J^T J of
 // the new point is already there, after a reject the J^T J of the unchanged
 // accepted point is reused. The reference recomputes both (batch_lm_ad.cu:363,
 // :400); the numbers are identical because the Jacobian depends only on c.
+//
+// LDS per wavefront: the batch's inputs x[v][p][lane], the spill slots
+// [s][p][lane], the constants and the pass sums; reverse AD adds its tape
+// [t][p][lane]. All indices are uniform, so accesses are bank-conflict free.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,6 +39,28 @@ namespace cusr {
 constexpr int kLanes = 64;
 constexpr double kCexpCap64 = 485165195.4097903;  // exp(20) rounded to double
 constexpr float kCexpCap32 = 485165184.0f;         // exp(20) rounded to float
+
+// Points per lane per interpreter pass: more amortises the scalar fetch and
+// dispatch, fewer keeps registers (the J^T J sums dominate for large K) and
+// the reverse-AD tape in LDS small.
+#ifndef CUSR_P64
+#define CUSR_P64 1
+#endif
+template <typename R, int K, int AD>
+constexpr int points_per_pass() {
+    return (AD == CO_AD_REVERSE) ? 1 : (sizeof(R) == 4) ? (K <= 8 ? 4 : 2) : (K <= 8 ? CUSR_P64 : 1);
+}
+
+// scalar-cache view of the program (constant address space)
+typedef const __attribute__((address_space(4))) uint64_t *ProgPtr;
+
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ double uni(double v) {
+    int2 p = *reinterpret_cast<int2 *>(&v);
+    p.x = __builtin_amdgcn_readfirstlane(p.x);
+    p.y = __builtin_amdgcn_readfirstlane(p.y);
+    return *reinterpret_cast<double *>(&p);
+}
 
 // ------------------------------------------------------------------ math
 
@@ -54,8 +82,7 @@ template <> struct Fn<double> {
     static __device__ __forceinline__ double max_(double a, double b) { return ::fmax(a, b); }
     static __device__ __forceinline__ double min_(double a, double b) { return ::fmin(a, b); }
     static constexpr double cexp_cap = kCexpCap64;
-    static constexpr double pdiv_eps = 1e-9;
-    static constexpr double plog_eps = 1e-9;
+    static constexpr double eps9 = 1e-9;
 };
 template <> struct Fn<float> {
     static __device__ __forceinline__ void sincos_(float a, float *s, float *c) { cm_sincosf(a, s, c); }
@@ -71,93 +98,149 @@ template <> struct Fn<float> {
     static __device__ __forceinline__ float max_(float a, float b) { return ::fmaxf(a, b); }
     static __device__ __forceinline__ float min_(float a, float b) { return ::fminf(a, b); }
     static constexpr float cexp_cap = kCexpCap32;
-    static constexpr float pdiv_eps = 1e-9f;
-    static constexpr float plog_eps = 1e-9f;
+    static constexpr float eps9 = 1e-9f;
 };
 
-// Value of a unary operator and its derivative d. sel: the tangent is kept
-// where d != 0 and zeroed elsewhere instead of multiplied (flat branches).
-template <typename R>
-__device__ __forceinline__ R op_unary(int f, R a, R &d, bool &sel) {
+#define CUSR_FOR_P _Pragma("unroll") for (int p = 0; p < P; ++p)
+
+// Value r and derivative d of a unary operator for P points. z[p]: the
+// tangent is zeroed instead of multiplied (a flat branch: derivative exactly
+// 0 by definition, so 0 * inf must not leak a NaN).
+template <typename R, int P>
+__device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) {
     typedef Fn<R> F;
     const R one = R(1), zero = R(0), two = R(2);
-    R r;
-    sel = false;
+    CUSR_FOR_P z[p] = false;
     switch (f) {
-    case OP_SIN: F::sincos_(a, &r, &d); break;
-    case OP_COS: { R sn; F::sincos_(a, &sn, &r); d = -sn; break; }
-    case OP_TAN: r = F::tan_(a); d = one + r * r; break;
-    case OP_SINH: r = F::sinh_(a); d = F::cosh_(a); break;
-    case OP_COSH: r = F::cosh_(a); d = F::sinh_(a); break;
-    case OP_TANH: r = F::tanh_(a); d = one - r * r; break;
-    case OP_LOG: r = F::log_(a); d = one / a; break;
-    case OP_LOOSE_LOG: r = F::log_(F::abs_(a)); d = one / a; break;
-    case OP_EXP: r = F::exp_(a); d = r; break;
-    case OP_INV: case OP_LOOSE_INV: r = one / a; d = -(r * r); break;
-    case OP_NEG: r = -a; d = -one; break;
-    case OP_ABS: r = F::abs_(a); d = (a > zero) ? one : ((a < zero) ? -one : zero); break;
-    case OP_SQRT: r = F::sqrt_(a); d = one / (two * r); break;
+    case OP_SIN: CUSR_FOR_P F::sincos_(a[p], &r[p], &d[p]); break;
+    case OP_COS: CUSR_FOR_P { R s; F::sincos_(a[p], &s, &r[p]); d[p] = -s; } break;
+    case OP_TAN: CUSR_FOR_P { r[p] = F::tan_(a[p]); d[p] = one + r[p] * r[p]; } break;
+    case OP_SINH: CUSR_FOR_P { r[p] = F::sinh_(a[p]); d[p] = F::cosh_(a[p]); } break;
+    case OP_COSH: CUSR_FOR_P { r[p] = F::cosh_(a[p]); d[p] = F::sinh_(a[p]); } break;
+    case OP_TANH: CUSR_FOR_P { r[p] = F::tanh_(a[p]); d[p] = one - r[p] * r[p]; } break;
+    case OP_LOG: CUSR_FOR_P { r[p] = F::log_(a[p]); d[p] = one / a[p]; } break;
+    case OP_LOOSE_LOG: CUSR_FOR_P { r[p] = F::log_(F::abs_(a[p])); d[p] = one / a[p]; } break;
+    case OP_EXP: CUSR_FOR_P { r[p] = F::exp_(a[p]); d[p] = r[p]; } break;
+    case OP_INV: case OP_LOOSE_INV: CUSR_FOR_P { r[p] = one / a[p]; d[p] = -(r[p] * r[p]); } break;
+    case OP_NEG: CUSR_FOR_P { r[p] = -a[p]; d[p] = -one; } break;
+    case OP_ABS:
+        CUSR_FOR_P {
+            r[p] = F::abs_(a[p]);
+            d[p] = (a[p] > zero) ? one : ((a[p] < zero) ? -one : zero);
+        }
+        break;
+    case OP_SQRT: CUSR_FOR_P { r[p] = F::sqrt_(a[p]); d[p] = one / (two * r[p]); } break;
     case OP_LOOSE_SQRT:
-        r = F::sqrt_(F::abs_(a));
-        d = (a > zero) ? one / (two * r) : ((a < zero) ? -one / (two * r) : zero);
+        CUSR_FOR_P {
+            r[p] = F::sqrt_(F::abs_(a[p]));
+            d[p] = (a[p] > zero) ? one / (two * r[p]) : ((a[p] < zero) ? -one / (two * r[p]) : zero);
+        }
         break;
     case OP_CEXP:
-        if (a > R(20)) { r = F::cexp_cap; d = zero; sel = true; }
-        else { r = F::exp_(a); d = r; }
+        CUSR_FOR_P {
+            const bool flat = a[p] > R(20);
+            const R e = F::exp_(flat ? zero : a[p]);
+            r[p] = flat ? F::cexp_cap : e;
+            d[p] = flat ? zero : e;
+            z[p] = flat;
+        }
         break;
-    case OP_SQUARE: r = a * a; d = a + a; break;
-    case OP_PLOG: {
-        R t = F::abs_(a) + F::plog_eps;
-        r = F::log_(t);
-        d = (a > zero) ? one / t : ((a < zero) ? -one / t : zero);
+    case OP_SQUARE: CUSR_FOR_P { r[p] = a[p] * a[p]; d[p] = a[p] + a[p]; } break;
+    case OP_PLOG:
+        CUSR_FOR_P {
+            const R t = F::abs_(a[p]) + F::eps9;
+            r[p] = F::log_(t);
+            d[p] = (a[p] > zero) ? one / t : ((a[p] < zero) ? -one / t : zero);
+        }
         break;
+    case OP_IDENT: CUSR_FOR_P { r[p] = a[p]; d[p] = one; } break;
+    default: CUSR_FOR_P { r[p] = zero; d[p] = zero; } break;
     }
-    default: r = zero; d = zero; break;
-    }
-    return r;
 }
 
-// Value of a binary operator l op rv and the partials d1 = dOut/dl,
-// d2 = dOut/drv. want_d2 false skips log(l) of POW (no constant on the right).
-template <typename R>
-__device__ __forceinline__ R op_binary(int f, R l, R rv, bool want_d2, R &d1, R &d2, bool &sel) {
+// Value o = l op rv and partials d1 = do/dl, d2 = do/drv for P points.
+// want_d2 false skips log(l) of POW when no constant is on the right.
+template <typename R, int P>
+__device__ __forceinline__ void binary_p(int f, const R *l, const R *rv, bool want_d2, R *o,
+                                         R *d1, R *d2, bool *z1, bool *z2) {
     typedef Fn<R> F;
     const R one = R(1), zero = R(0);
-    R o;
-    sel = false;
+    CUSR_FOR_P { z1[p] = false; z2[p] = false; }
     switch (f) {
-    case OP_ADD: o = l + rv; d1 = one; d2 = one; break;
-    case OP_SUB: o = l - rv; d1 = one; d2 = -one; break;
-    case OP_MUL: o = l * rv; d1 = rv; d2 = l; break;
-    case OP_DIV: case OP_LOOSE_DIV: o = l / rv; d1 = one / rv; d2 = -o / rv; break;
+    case OP_ADD: CUSR_FOR_P { o[p] = l[p] + rv[p]; d1[p] = one; d2[p] = one; } break;
+    case OP_SUB: CUSR_FOR_P { o[p] = l[p] - rv[p]; d1[p] = one; d2[p] = -one; } break;
+    case OP_MUL: CUSR_FOR_P { o[p] = l[p] * rv[p]; d1[p] = rv[p]; d2[p] = l[p]; } break;
+    case OP_DIV: case OP_LOOSE_DIV:
+        CUSR_FOR_P { o[p] = l[p] / rv[p]; d1[p] = one / rv[p]; d2[p] = -o[p] / rv[p]; }
+        break;
     case OP_PDIV:
-        if (F::abs_(rv) < F::pdiv_eps) { o = one; d1 = zero; d2 = zero; sel = true; }
-        else { o = l / rv; d1 = one / rv; d2 = -o / rv; }
+        CUSR_FOR_P {
+            const bool prot = F::abs_(rv[p]) < F::eps9;
+            const R den = prot ? one : rv[p];
+            const R q = l[p] / den;
+            o[p] = prot ? one : q;
+            d1[p] = prot ? zero : one / den;
+            d2[p] = prot ? zero : -q / den;
+            z1[p] = prot;
+            z2[p] = prot;
+        }
         break;
     case OP_POW:
-        o = F::pow_(l, rv);
-        d1 = rv * F::pow_(l, rv - one);
-        d2 = want_d2 ? o * F::log_(l) : zero;
+        CUSR_FOR_P {
+            o[p] = F::pow_(l[p], rv[p]);
+            d1[p] = rv[p] * F::pow_(l[p], rv[p] - one);
+            d2[p] = want_d2 ? o[p] * F::log_(l[p]) : zero;
+        }
         break;
-    case OP_LOOSE_POW: {
-        R al = F::abs_(l);
-        R s = (l > zero) ? one : ((l < zero) ? -one : zero);
-        o = F::pow_(al, rv);
-        d1 = s * (rv * F::pow_(al, rv - one));
-        d2 = want_d2 ? o * F::log_(al) : zero;
+    case OP_LOOSE_POW:
+        CUSR_FOR_P {
+            const R al = F::abs_(l[p]);
+            const R s = (l[p] > zero) ? one : ((l[p] < zero) ? -one : zero);
+            o[p] = F::pow_(al, rv[p]);
+            d1[p] = s * (rv[p] * F::pow_(al, rv[p] - one));
+            d2[p] = want_d2 ? o[p] * F::log_(al) : zero;
+        }
         break;
+    case OP_MAX:
+        CUSR_FOR_P {
+            const bool ge = l[p] >= rv[p];
+            o[p] = F::max_(l[p], rv[p]);
+            d1[p] = ge ? one : zero;
+            d2[p] = ge ? zero : one;
+            z1[p] = !ge;
+            z2[p] = ge;
+        }
+        break;
+    case OP_MIN:
+        CUSR_FOR_P {
+            const bool le = l[p] <= rv[p];
+            o[p] = F::min_(l[p], rv[p]);
+            d1[p] = le ? one : zero;
+            d2[p] = le ? zero : one;
+            z1[p] = !le;
+            z2[p] = le;
+        }
+        break;
+    case OP_LT:
+        CUSR_FOR_P { o[p] = (l[p] < rv[p]) ? one : zero; d1[p] = zero; d2[p] = zero; z1[p] = true; z2[p] = true; }
+        break;
+    case OP_GT:
+        CUSR_FOR_P { o[p] = (l[p] > rv[p]) ? one : zero; d1[p] = zero; d2[p] = zero; z1[p] = true; z2[p] = true; }
+        break;
+    case OP_LE:
+        CUSR_FOR_P { o[p] = (l[p] <= rv[p]) ? one : zero; d1[p] = zero; d2[p] = zero; z1[p] = true; z2[p] = true; }
+        break;
+    case OP_GE:
+        CUSR_FOR_P { o[p] = (l[p] >= rv[p]) ? one : zero; d1[p] = zero; d2[p] = zero; z1[p] = true; z2[p] = true; }
+        break;
+    default: CUSR_FOR_P { o[p] = zero; d1[p] = zero; d2[p] = zero; } break;
     }
-    case OP_MAX: o = F::max_(l, rv); d1 = (l >= rv) ? one : zero; d2 = (l >= rv) ? zero : one;
-        sel = true; break;
-    case OP_MIN: o = F::min_(l, rv); d1 = (l <= rv) ? one : zero; d2 = (l <= rv) ? zero : one;
-        sel = true; break;
-    case OP_LT: o = (l < rv) ? one : zero; d1 = zero; d2 = zero; sel = true; break;
-    case OP_GT: o = (l > rv) ? one : zero; d1 = zero; d2 = zero; sel = true; break;
-    case OP_LE: o = (l <= rv) ? one : zero; d1 = zero; d2 = zero; sel = true; break;
-    case OP_GE: o = (l >= rv) ? one : zero; d1 = zero; d2 = zero; sel = true; break;
-    default: o = zero; d1 = zero; d2 = zero; break;
-    }
-    return o;
+}
+
+// operators whose derivative can be an exact structural zero (select rule)
+__device__ __forceinline__ bool op_selects(int f) {
+    return f == OP_MAX || f == OP_MIN || f == OP_LT || f == OP_GT || f == OP_LE ||
+           f == OP_GE || f == OP_PDIV || f == OP_CEXP;
 }
 
 template <typename R>
@@ -165,94 +248,161 @@ __device__ __forceinline__ R safe_mul(R a, R b) {
     return (a == R(0) || b == R(0)) ? R(0) : a * b;
 }
 
-// wave-uniform copies (values every lane already agrees on)
-__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ double uni(double v) {
-    int2 p = *reinterpret_cast<int2 *>(&v);
-    p.x = __builtin_amdgcn_readfirstlane(p.x);
-    p.y = __builtin_amdgcn_readfirstlane(p.y);
-    return *reinterpret_cast<double *>(&p);
+// ----------------------------------------------------------- the wave state
+
+// Per-wavefront LDS areas; every array is [index][p][lane].
+template <typename R, int P>
+struct WaveLds {
+    R *x;      // [D][P][64] the batch's inputs
+    R *slot;   // [slots][P][64] spilled right operands (adjoints in the reverse sweep)
+    R *tape;   // [tape][P][64] reverse-AD partials
+};
+
+template <typename R, int P>
+__device__ __forceinline__ R &lds_at(R *base, int idx, int p, int lane) {
+    return base[(idx * P + p) * kLanes + lane];
 }
 
-// -------------------------------------------------------- one point
-
-// Forward sweep over one expression at one point. JAC: 0 value only,
-// 1 forward AD into T[0..K), 2 record partials on the tape (reverse AD).
-// x: the point's inputs; cs: the wave's constants (LDS, fp64);
-// tape: this wave's tape base, slot s of lane l at tape[s*64 + l].
-template <int K, typename R, int JAC>
-__device__ __forceinline__ R forward_point(const uint64_t *__restrict__ prog, int n,
-                                           const R *x, const double *cs, R *T, R *tape,
-                                           int lane) {
-    R st[CO_MAX_STACK];
-    for (int pc = 0; pc < n; ++pc) {
-        const uint64_t w = prog[pc];
-        const int kind = ins_kind(w);
-        const int sp = ins_sp(w);
-        if (kind == NODE_VAR) {
-            st[sp] = x[ins_arg(w)];
-        } else if (kind == NODE_CONST) {
-            const int k = ins_arg(w);
-            st[sp] = (R)cs[k];
-            if (JAC == 1) T[k] = R(1);
-        } else if (kind == NODE_UFUNC) {
-            R d;
-            bool sel;
-            st[sp - 1] = op_unary<R>(ins_fid(w), st[sp - 1], d, sel);
-            if (JAC == 1) {
-                const int lo = ins_lo(w), hi = ins_hi(w);
-                if (sel) { for (int j = lo; j < hi; ++j) T[j] = (d != R(0)) ? T[j] : R(0); }
-                else { for (int j = lo; j < hi; ++j) T[j] = T[j] * d; }
-            } else if (JAC == 2) {
-                tape[ins_tape(w) * kLanes + lane] = d;
+// T[p*K + j] *= d[p] for j in [lo, hi); with sel, zero where z[p] instead.
+// The j loop is unrolled over the compile-time K with one scalar branch per j
+// (the asm marker with j as operand keeps the branches distinct, so they are
+// not merged into one dynamically indexed access), and T stays in registers
+// with static indices.
+template <int K, typename R, int P>
+__device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, const bool *z,
+                                            bool sel) {
+    if (hi <= lo) return;
+    const uint32_t mask = ((1u << hi) - 1u) & ~((1u << lo) - 1u);
+    if (!sel) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            if (mask & (1u << j)) {
+                __asm__ volatile("; scale %0" ::"n"(j));
+                CUSR_FOR_P T[p * K + j] = T[p * K + j] * d[p];
             }
-        } else {
-            R d1, d2;
-            bool sel;
-            const int lo = ins_lo(w), mid = ins_mid(w), hi = ins_hi(w);
-            const bool want_d2 = (JAC == 2) || (mid < hi);
-            const R o = op_binary<R>(ins_fid(w), st[sp - 1], st[sp - 2], want_d2, d1, d2, sel);
-            st[sp - 2] = o;
-            if (JAC == 1) {
-                if (sel) {
-                    for (int j = lo; j < mid; ++j) T[j] = (d1 != R(0)) ? T[j] : R(0);
-                    for (int j = mid; j < hi; ++j) T[j] = (d2 != R(0)) ? T[j] : R(0);
-                } else {
-                    for (int j = lo; j < mid; ++j) T[j] = T[j] * d1;
-                    for (int j = mid; j < hi; ++j) T[j] = T[j] * d2;
-                }
-            } else if (JAC == 2) {
-                const int s = ins_tape(w);
-                tape[s * kLanes + lane] = d1;
-                tape[(s + 1) * kLanes + lane] = d2;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            if (mask & (1u << j)) {
+                __asm__ volatile("; select %0" ::"n"(j));
+                CUSR_FOR_P T[p * K + j] = z[p] ? R(0) : T[p * K + j] * d[p];
             }
         }
     }
-    return st[0];
 }
 
-// Reverse sweep (prefix order = instructions from last to first) over the
-// tape written by forward_point<..., 2>: g[k] = d f / d c_k
-// (cusr/kernel/revad_interp.cuh:131-156).
-template <int K, typename R>
-__device__ __forceinline__ void reverse_point(const uint64_t *__restrict__ prog, int n,
-                                              const R *tape, R *g, int lane) {
-    R as[CO_MAX_STACK + 1];
-    R tos = R(1);
+// T[p*K + k] += v[p] for a wave-uniform k (same branch scheme as scale_range).
+template <int K, typename R, int P>
+__device__ __forceinline__ void add_tangent(R *T, int k, const R *v) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        if (j == k) {
+            __asm__ volatile("; add %0" ::"n"(j));
+            CUSR_FOR_P T[p * K + j] = T[p * K + j] + v[p];
+        }
+    }
+}
+
+// Fetch an operand of kind/idx for P points.
+template <typename R, int P>
+__device__ __forceinline__ void fetch(int kind, int idx, const R *acc, const WaveLds<R, P> &w,
+                                      const double *cs, int lane, R *out) {
+    if (kind == OPD_ACC) {
+        CUSR_FOR_P out[p] = acc[p];
+    } else if (kind == OPD_VAR) {
+        CUSR_FOR_P out[p] = lds_at<R, P>(w.x, idx, p, lane);
+    } else if (kind == OPD_CONST) {
+        const R c = (R)cs[idx];
+        CUSR_FOR_P out[p] = c;
+    } else {
+        CUSR_FOR_P out[p] = lds_at<R, P>(w.slot, idx, p, lane);
+    }
+}
+
+// Forward sweep of one program over P points whose inputs are in w.x.
+// JAC: 0 value only, 1 forward AD into T[p*K + j] (which must hold 1.0 on
+// entry: the tangent of constant k with respect to itself), 2 partials to the
+// tape.
+template <int K, typename R, int P, int JAC>
+__device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<R, P> &w,
+                                             const double *cs, int lane, R *acc, R *T) {
+    for (int pc = 0; pc < n; ++pc) {
+        const uint64_t ins = prog[pc];
+        const int fid = ins_fid(ins);
+        const int ak = ins_akind(ins), ai = ins_aidx(ins);
+        R a[P], b[P], o[P], d1[P], d2[P];
+        bool z1[P], z2[P];
+        fetch<R, P>(ak, ai, acc, w, cs, lane, a);
+        const int lo = ins_lo(ins), mid = ins_mid(ins), hi = ins_hi(ins);
+        if (ins_binary(ins)) {
+            const int bk = ins_bkind(ins), bi = ins_bidx(ins);
+            fetch<R, P>(bk, bi, acc, w, cs, lane, b);
+            binary_p<R, P>(fid, a, b, JAC == 2 || mid < hi, o, d1, d2, z1, z2);
+            if constexpr (JAC == 1) {
+                // a constant operand k owns the range [k, k+1) and its tangent
+                // starts at 1, so one rule covers leaves and subtrees; the
+                // partials of ADD (and the left one of SUB) are exactly 1
+                const bool sel = op_selects(fid);
+                if (fid != OP_ADD && fid != OP_SUB) scale_range<K, R, P>(T, lo, mid, d1, z1, sel);
+                if (fid != OP_ADD) scale_range<K, R, P>(T, mid, hi, d2, z2, sel);
+            } else if constexpr (JAC == 2) {
+                const int t = ins_tape(ins);
+                CUSR_FOR_P {
+                    lds_at<R, P>(w.tape, t, p, lane) = d1[p];
+                    lds_at<R, P>(w.tape, t + 1, p, lane) = d2[p];
+                }
+            }
+        } else {
+            unary_p<R, P>(fid, a, o, d1, z1);
+            if constexpr (JAC == 1) {
+                if (fid != OP_IDENT) scale_range<K, R, P>(T, lo, hi, d1, z1, fid == OP_CEXP);
+            } else if constexpr (JAC == 2) {
+                const int t = ins_tape(ins);
+                CUSR_FOR_P lds_at<R, P>(w.tape, t, p, lane) = d1[p];
+            }
+        }
+        if (ins_toslot(ins)) {
+            const int di = ins_didx(ins);
+            CUSR_FOR_P lds_at<R, P>(w.slot, di, p, lane) = o[p];
+        } else {
+            CUSR_FOR_P acc[p] = o[p];
+        }
+    }
+}
+
+// Reverse sweep over the tape written by forward_pass<..., 2>:
+// T[p*K + k] = d f / d c_k, T zero on entry (cusr/kernel/revad_interp.cuh:131-156). The
+// adjoints of spilled values live in the slot area (their values are dead).
+template <int K, typename R, int P>
+__device__ __forceinline__ void reverse_pass(ProgPtr prog, int n, const WaveLds<R, P> &w,
+                                             int lane, R *T) {
+    R accadj[P];
+    CUSR_FOR_P accadj[p] = R(1);
     for (int pc = n - 1; pc >= 0; --pc) {
-        const uint64_t w = prog[pc];
-        const int kind = ins_kind(w);
-        const int asp = ins_asp(w);
-        const int apop = ins_apop(w);
-        const R adj = apop ? as[asp - 1] : tos;
-        if (kind == NODE_CONST) {
-            g[ins_arg(w)] = R(0) + adj;
-        } else if (kind == NODE_UFUNC) {
-            tos = safe_mul<R>(adj, tape[ins_tape(w) * kLanes + lane]);
-        } else if (kind == NODE_BFUNC) {
-            const int s = ins_tape(w);
-            as[asp - apop] = safe_mul<R>(adj, tape[(s + 1) * kLanes + lane]);
-            tos = safe_mul<R>(adj, tape[s * kLanes + lane]);
+        const uint64_t ins = prog[pc];
+        R adj[P];
+        if (ins_toslot(ins)) {
+            const int di = ins_didx(ins);
+            CUSR_FOR_P adj[p] = lds_at<R, P>(w.slot, di, p, lane);
+        } else {
+            CUSR_FOR_P adj[p] = accadj[p];
+        }
+        const int t = ins_tape(ins);
+        const int nop = ins_binary(ins) ? 2 : 1;
+        for (int side = 0; side < nop; ++side) {
+            const int kind = side ? ins_bkind(ins) : ins_akind(ins);
+            const int idx = side ? ins_bidx(ins) : ins_aidx(ins);
+            if (kind == OPD_VAR) continue;
+            R g[P];
+            CUSR_FOR_P g[p] = safe_mul<R>(adj[p], lds_at<R, P>(w.tape, t + side, p, lane));
+            if (kind == OPD_ACC) {
+                CUSR_FOR_P accadj[p] = g[p];
+            } else if (kind == OPD_SLOT) {
+                CUSR_FOR_P lds_at<R, P>(w.slot, idx, p, lane) = g[p];
+            } else {
+                add_tangent<K, R, P>(T, idx, g);   // T starts at 0: 0 + adjoint
+            }
         }
     }
 }
@@ -260,13 +410,11 @@ __device__ __forceinline__ void reverse_point(const uint64_t *__restrict__ prog,
 // ------------------------------------------------------- one data pass
 
 struct PassArgs {
-    const uint64_t *prog;  // this expression's program
+    ProgPtr prog;       // this expression's program
     int n;
-    const double *X;       // [D][N] column-major
-    const double *y;       // this expression's targets [N]
+    const double *X;    // [D][N] column-major
+    const double *y;    // this expression's targets [N]
     int N, D;
-    float *tape32;         // this wave's tape (reverse AD), lane-interleaved
-    double *tape64;
 };
 
 constexpr int sums_width(int K) { return 1 + K + K * (K + 1) / 2; }
@@ -280,49 +428,71 @@ __device__ __forceinline__ void wave_allreduce(double (&a)[W]) {
     }
 }
 
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
 // One pass over all points at constants cs (LDS): sums[0] = sum r^2,
 // sums[1..K] = J^T r, sums[1+K..] = upper triangle of J^T J (row-major),
 // written to out (LDS) by lane 0. JAC: 0 value only, 1 forward, 2 reverse.
-template <int K, typename R, int JAC>
-__device__ void data_pass(const PassArgs &a, const double *cs, double *out, int lane) {
+template <int K, typename R, int P, int JAC>
+__device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P> &w, const double *cs,
+                          double *out, int lane) {
     constexpr int W = (JAC == 0) ? 1 : sums_width(K);
+    constexpr int KT = (K > 0) ? K : 1;
     double acc[W];
 #pragma unroll
-    for (int w = 0; w < W; ++w) acc[w] = 0.0;
-    R *tape = nullptr;
-    if constexpr (JAC == 2) {
-        if constexpr (sizeof(R) == 8) tape = (R *)a.tape64; else tape = (R *)a.tape32;
-    }
-    for (int i = lane; i < a.N; i += kLanes) {
-        R x[CO_MAX_VARS];
+    for (int q = 0; q < W; ++q) acc[q] = 0.0;
+    const int batches = (a.N + kLanes * P - 1) / (kLanes * P);
+    for (int bt = 0; bt < batches; ++bt) {
+        double yv[P];
+        bool valid[P];
+        CUSR_FOR_P {
+            const int i = lane + kLanes * (bt * P + p);
+            valid[p] = i < a.N;
+            yv[p] = valid[p] ? a.y[i] : 0.0;
+        }
 #pragma unroll
-        for (int v = 0; v < CO_MAX_VARS; ++v)
-            if (v < a.D) x[v] = (R)a.X[(size_t)v * a.N + i];
-        const double yi = a.y[i];
-        R T[K > 0 ? K : 1];
-        const R f = forward_point<K, R, JAC>(a.prog, a.n, x, cs, T, tape, lane);
-        if constexpr (JAC == 2) reverse_point<K, R>(a.prog, a.n, tape, T, lane);
-        const double r = (double)f - yi;
-        acc[0] = fma(r, r, acc[0]);
-        if constexpr (JAC != 0) {
+        for (int v = 0; v < CO_MAX_VARS; ++v) {
+            if (v < a.D) {
+                CUSR_FOR_P {
+                    const int i = lane + kLanes * (bt * P + p);
+                    lds_at<R, P>(w.x, v, p, lane) = valid[p] ? (R)a.X[(size_t)v * a.N + i] : R(0);
+                }
+            }
+        }
+        R accv[P];
+        R T[P * KT];
 #pragma unroll
-            for (int j = 0; j < K; ++j) acc[1 + j] = fma((double)T[j], r, acc[1 + j]);
-            int q = 1 + K;
+        for (int j = 0; j < P * KT; ++j) T[j] = (JAC == 1) ? R(1) : R(0);
+        forward_pass<K, R, P, JAC>(a.prog, a.n, w, cs, lane, accv, T);
+        if constexpr (JAC == 2) reverse_pass<K, R, P>(a.prog, a.n, w, lane, T);
+        CUSR_FOR_P {
+            if (valid[p]) {
+                const double r = (double)accv[p] - yv[p];
+                acc[0] = fma(r, r, acc[0]);
+                if constexpr (JAC != 0) {
 #pragma unroll
-            for (int j1 = 0; j1 < K; ++j1)
+                    for (int j = 0; j < K; ++j)
+                        acc[1 + j] = fma((double)T[p * KT + j], r, acc[1 + j]);
+                    int q = 1 + K;
 #pragma unroll
-                for (int j2 = j1; j2 < K; ++j2, ++q)
-                    acc[q] = fma((double)T[j1], (double)T[j2], acc[q]);
+                    for (int j1 = 0; j1 < K; ++j1)
+#pragma unroll
+                        for (int j2 = j1; j2 < K; ++j2, ++q)
+                            acc[q] = fma((double)T[p * KT + j1], (double)T[p * KT + j2], acc[q]);
+                }
+            }
         }
     }
     wave_allreduce<W>(acc);
     if (lane == 0) {
 #pragma unroll
-        for (int w = 0; w < W; ++w) out[w] = acc[w];
+        for (int q = 0; q < W; ++q) out[q] = acc[q];
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    wave_sync_lds();
 }
 
 // ------------------------------------------------------------ the solve
@@ -385,7 +555,7 @@ __device__ __forceinline__ bool damped_solve(const double *s, double lambda, dou
 
 struct FitArgs {
     const uint64_t *prog;
-    const ExprDesc *desc;   // by launch position
+    const ExprDesc *desc;   // by launch position (offset to the bin's start)
     const double *X;        // [D][N]
     const double *Y;        // [M][N]
     const double *C0;       // [total_c]
@@ -396,35 +566,37 @@ struct FitArgs {
     int32_t *iters;         // [M] out
     int N, D, max_iter, guard;
     double lambda0, xtol;
-    int tape_slots;         // per-wave tape slots in dynamic LDS
+    int slots, tape;        // per-wave LDS rows of this launch ([row][P][64] each)
 };
 
 // internal states, mapped to STATUS_* at the end (lm_core.cuh:46-56)
 enum { ST_RUN = 0, ST_CONV = 1, ST_NAN = 2, ST_K0 = 3, ST_CHOL = 4 };
 
 template <int K, typename R, int AD>
-__device__ void fit_one(const FitArgs &fa, const ExprDesc &e, double *lds_c, double *lds_s,
-                        void *lds_tape, int lane) {
+__device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, double *lds_c, double *lds_s,
+                        char *lds_dyn, int lane) {
+    constexpr int P = points_per_pass<R, K, AD>();
     constexpr int JAC = (K == 0) ? 0 : (AD == CO_AD_REVERSE ? 2 : 1);
+    WaveLds<R, P> wl;
+    wl.x = (R *)lds_dyn;
+    wl.slot = wl.x + (size_t)fa.D * P * kLanes;
+    wl.tape = wl.slot + (size_t)fa.slots * P * kLanes;
     PassArgs pa;
-    pa.prog = fa.prog + e.prog_off;
+    pa.prog = (ProgPtr)(fa.prog + e.prog_off);
     pa.n = e.n;
     pa.X = fa.X;
     pa.y = fa.Y + (size_t)e.y_row * fa.N;
     pa.N = fa.N;
     pa.D = fa.D;
-    pa.tape32 = (float *)lds_tape;
-    pa.tape64 = (double *)lds_tape;
 
     double *c_cur = lds_c, *c_try = lds_c + CO_MAX_K;
     double *s_cur = lds_s, *s_try = lds_s + sums_width(CO_MAX_K);
     if (lane < K) c_cur[lane] = fa.C0[e.c_off + lane];
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
+    wave_sync_lds();
 
-    data_pass<K, R, JAC>(pa, c_cur, s_cur, lane);
+    data_pass<K, R, P, JAC>(pa, wl, c_cur, s_cur, lane);
     double loss = uni(0.5 * s_cur[0]);
-    double loss_init = loss;
+    const double loss_init = loss;
     int st = (K == 0) ? ST_K0 : (isfinite(loss) ? ST_RUN : ST_NAN);
     double lambda = fa.lambda0;
     int it = 0;
@@ -442,9 +614,8 @@ __device__ void fit_one(const FitArgs &fa, const ExprDesc &e, double *lds_c, dou
                 for (int j = 0; j < K; ++j)
                     if (j == lane) c_try[j] = c_cur[j] + delta[j];
             }
-            __builtin_amdgcn_s_waitcnt(0);
-            __builtin_amdgcn_wave_barrier();
-            data_pass<K, R, JAC>(pa, c_try, s_try, lane);
+            wave_sync_lds();
+            data_pass<K, R, P, JAC>(pa, wl, c_try, s_try, lane);
             const double loss_try = uni(0.5 * s_try[0]);
             if (!isfinite(loss_try)) { st = ST_NAN; continue; }
             double dn2 = 0.0, cn2 = 0.0;
@@ -471,13 +642,17 @@ __device__ void fit_one(const FitArgs &fa, const ExprDesc &e, double *lds_c, dou
     }
     double lf = loss, li = loss_init;
     if constexpr (sizeof(R) == 4) {
-        // fp64 losses at the delivered point and at the start
-        data_pass<K, double, 0>(pa, c_cur, s_try, lane);
+        // fp64 losses at the delivered point and at the start; the fp64
+        // value pass reuses the same LDS at one point per lane
+        WaveLds<double, 1> w64;
+        w64.x = (double *)lds_dyn;
+        w64.slot = w64.x + (size_t)fa.D * kLanes;
+        w64.tape = w64.slot + (size_t)fa.slots * kLanes;
+        data_pass<K, double, 1, 0>(pa, w64, c_cur, s_try, lane);
         lf = uni(0.5 * s_try[0]);
         if (lane < K) c_try[lane] = fa.C0[e.c_off + lane];
-        __builtin_amdgcn_s_waitcnt(0);
-        __builtin_amdgcn_wave_barrier();
-        data_pass<K, double, 0>(pa, c_try, s_try, lane);
+        wave_sync_lds();
+        data_pass<K, double, 1, 0>(pa, w64, c_try, s_try, lane);
         li = uni(0.5 * s_try[0]);
     }
     bool revert = false;
@@ -498,15 +673,22 @@ __device__ void fit_one(const FitArgs &fa, const ExprDesc &e, double *lds_c, dou
 
 // One kernel per (K, precision, AD mode): each K gets its own register
 // allocation, so small-K expressions are not held to the occupancy of K = 16.
-// Launch position p of a K bin runs descriptor desc[p] (the host offsets desc
-// to the bin's start).
 template <int K, typename R, int AD>
 __global__ void __launch_bounds__(kLanes) lm_fit_kernel(FitArgs fa) {
     __shared__ double lds_c[2 * CO_MAX_K];
     __shared__ double lds_s[2 * sums_width(CO_MAX_K)];
-    extern __shared__ double lds_tape[];
+    extern __shared__ char lds_dyn[];
     const ExprDesc e = fa.desc[blockIdx.x];
-    fit_one<K, R, AD>(fa, e, lds_c, lds_s, lds_tape, (int)threadIdx.x);
+    fit_one<K, R, AD>(fa, e, lds_c, lds_s, lds_dyn, (int)threadIdx.x);
+}
+
+// Dynamic LDS bytes one wavefront of a fit launch needs (the mixed-precision
+// fp64 audit pass reuses the same bytes at one point per lane).
+template <typename R, int K, int AD>
+constexpr size_t fit_lds_bytes_t(int D, int slots, int tape) {
+    const size_t a = (size_t)(D + slots + tape) * points_per_pass<R, K, AD>() * kLanes * sizeof(R);
+    const size_t b = (size_t)(D + slots) * kLanes * sizeof(double);
+    return a > b ? a : b;
 }
 
 hipError_t launch_fit_f64_fwd(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
@@ -527,19 +709,28 @@ struct EvalArgs {
 
 template <typename R>
 __global__ void __launch_bounds__(kLanes) eval_kernel(EvalArgs ea) {
+    constexpr int P = 1;
     __shared__ double cs[CO_MAX_K];
+    extern __shared__ char lds_dyn[];
     const int lane = threadIdx.x;
     const ExprDesc e = ea.desc[blockIdx.x];
     if (lane < e.K) cs[lane] = ea.C[e.c_off + lane];
-    __syncthreads();
-    for (int i = lane; i < ea.N; i += kLanes) {
-        R x[CO_MAX_VARS];
+    WaveLds<R, P> w;
+    w.x = (R *)lds_dyn;
+    w.slot = w.x + (size_t)ea.D * kLanes;
+    w.tape = w.slot;
+    wave_sync_lds();
+    const ProgPtr prog = (ProgPtr)(ea.prog + e.prog_off);
+    const int batches = (ea.N + kLanes - 1) / kLanes;
+    for (int bt = 0; bt < batches; ++bt) {
+        const int i = lane + kLanes * bt;
+        const bool valid = i < ea.N;
 #pragma unroll
         for (int v = 0; v < CO_MAX_VARS; ++v)
-            if (v < ea.D) x[v] = (R)ea.X[(size_t)v * ea.N + i];
-        R T[1];
-        const R f = forward_point<0, R, 0>(ea.prog + e.prog_off, e.n, x, cs, T, nullptr, lane);
-        ea.Yout[(size_t)e.y_row * ea.N + i] = (double)f;
+            if (v < ea.D) lds_at<R, P>(w.x, v, 0, lane) = valid ? (R)ea.X[(size_t)v * ea.N + i] : R(0);
+        R accv[1], T[1];
+        forward_pass<0, R, P, 0>(prog, e.n, w, cs, lane, accv, T);
+        if (valid) ea.Yout[(size_t)e.y_row * ea.N + i] = (double)accv[0];
     }
 }
 

@@ -44,122 +44,171 @@ static int node_int(float v, int limit) {
     return ((float)i == v) ? i : -1;
 }
 
-struct TreeScratch {
-    std::vector<int> size, left, cc, stk;
+struct Operand {
+    int kind;      // OPD_*
+    int idx;       // var / const rank / slot
+    int producer;  // instruction that produced an ACC value, else -1
 };
 
-// Decode one expression (n nodes at nt/nv/ci) into out[0..n) in execution
-// order. Returns CO_OK, CO_ERR_BOUNDS or CO_ERR_PROGRAM.
+struct TreeScratch {
+    std::vector<int> size, left, cc;
+    std::vector<int> depth_stack;
+    std::vector<Operand> opd;
+};
+
+// Decode one expression (n nodes) into out[0..n_ins) in execution order.
+// Returns CO_OK, CO_ERR_BOUNDS or CO_ERR_PROGRAM.
 static int decode_tree(const int32_t *nt, const float *nv, const int32_t *ci, int n, int K,
-                       int D, uint64_t *out, int *stack_depth, int *tape_slots,
-                       TreeScratch &s) {
+                       int D, uint64_t *out, int *n_ins, int *stack_depth, int *tape_slots,
+                       int *slots_used, TreeScratch &s) {
     if (n <= 0) return CO_ERR_PROGRAM;
     if (n > CO_MAX_NODES) return CO_ERR_BOUNDS;
     s.size.assign(n, 0);
     s.left.assign(n, 0);
     s.cc.assign(n + 1, 0);
-    s.stk.clear();
     // prefix pass: constant ranks must be 0..K-1 in prefix order
     for (int i = 0; i < n; i++) {
         s.cc[i + 1] = s.cc[i] + (nt[i] == NODE_CONST ? 1 : 0);
         if (nt[i] == NODE_CONST && ci[i] != s.cc[i]) return CO_ERR_PROGRAM;
     }
     if (s.cc[n] != K) return CO_ERR_PROGRAM;
-    // execution pass (last node first): stack simulation and subtree sizes
+    // execution pass (last node first): validation, stack depth, subtree sizes
+    s.depth_stack.clear();
     int depth = 0;
     for (int i = n - 1; i >= 0; i--) {
-        int t = nt[i];
+        const int t = nt[i];
         if (t == NODE_VAR) {
             if (node_int(nv[i], D) < 0) return CO_ERR_PROGRAM;
-            s.stk.push_back(1);
+            s.depth_stack.push_back(1);
             s.size[i] = 1;
         } else if (t == NODE_CONST) {
-            s.stk.push_back(1);
+            s.depth_stack.push_back(1);
             s.size[i] = 1;
         } else if (t == NODE_UFUNC) {
             if (!unary_op(node_int(nv[i], 64))) return CO_ERR_PROGRAM;
-            if (s.stk.empty()) return CO_ERR_PROGRAM;
-            s.size[i] = s.stk.back() + 1;
-            s.stk.back() = s.size[i];
+            if (s.depth_stack.empty()) return CO_ERR_PROGRAM;
+            s.size[i] = s.depth_stack.back() + 1;
+            s.depth_stack.back() = s.size[i];
         } else if (t == NODE_BFUNC) {
             if (!binary_op(node_int(nv[i], 64))) return CO_ERR_PROGRAM;
-            if (s.stk.size() < 2) return CO_ERR_PROGRAM;
-            int sl = s.stk.back();   // left operand = top of stack
-            s.stk.pop_back();
-            int sr = s.stk.back();
+            if (s.depth_stack.size() < 2) return CO_ERR_PROGRAM;
+            const int sl = s.depth_stack.back();  // left operand = top of stack
+            s.depth_stack.pop_back();
+            const int sr = s.depth_stack.back();
             s.left[i] = sl;
             s.size[i] = sl + sr + 1;
-            s.stk.back() = s.size[i];
+            s.depth_stack.back() = s.size[i];
         } else {
             return CO_ERR_PROGRAM;
         }
-        if ((int)s.stk.size() > depth) depth = (int)s.stk.size();
+        if ((int)s.depth_stack.size() > depth) depth = (int)s.depth_stack.size();
     }
-    if (s.stk.size() != 1) return CO_ERR_PROGRAM;
+    if (s.depth_stack.size() != 1) return CO_ERR_PROGRAM;
     if (depth > CO_MAX_STACK) return CO_ERR_BOUNDS;
-    // second execution pass: emit instructions with stack depth and tape slots
-    int sp = 0, tape = 0;
-    for (int i = n - 1, pc = 0; i >= 0; i--, pc++) {
-        int t = nt[i];
-        uint64_t w = (uint64_t)(t & 3) << 8;
-        w |= (uint64_t)sp << 24;
+
+    // emission pass: operator instructions over ACC / SLOT / leaf operands
+    s.opd.clear();
+    int nins = 0, tape = 0, live_slots = 0, max_slots = 0;
+    for (int i = n - 1; i >= 0; i--) {
+        const int t = nt[i];
         if (t == NODE_VAR) {
-            w |= (uint64_t)node_int(nv[i], D) << 16;
-            sp++;
-        } else if (t == NODE_CONST) {
-            w |= (uint64_t)ci[i] << 16;
-            sp++;
-        } else {
-            int f = (int)nv[i];
-            int lo = s.cc[i + 1];
-            int hi = s.cc[i + s.size[i]];
-            int mid = (t == NODE_BFUNC) ? s.cc[i + 1 + s.left[i]] : hi;
-            w |= (uint64_t)f;
-            w |= (uint64_t)lo << 32 | (uint64_t)mid << 37 | (uint64_t)hi << 42;
-            w |= (uint64_t)tape << 47;
-            tape += (t == NODE_BFUNC) ? 2 : 1;
-            if (t == NODE_BFUNC) sp--;
+            s.opd.push_back({OPD_VAR, node_int(nv[i], D), -1});
+            continue;
         }
-        out[pc] = w;
+        if (t == NODE_CONST) {
+            s.opd.push_back({OPD_CONST, ci[i], -1});
+            continue;
+        }
+        const int f = (int)nv[i];
+        const bool bin = (t == NODE_BFUNC);
+        const Operand a = s.opd.back();
+        s.opd.pop_back();
+        Operand b = {OPD_ACC, 0, -1};
+        if (bin) {
+            b = s.opd.back();
+            s.opd.pop_back();
+        }
+        // spill slots are used last in, first out
+        if (a.kind == OPD_SLOT) {
+            if (a.idx != live_slots - 1) return CO_ERR_PROGRAM;
+            live_slots--;
+        }
+        if (bin && b.kind == OPD_SLOT) {
+            if (b.idx != live_slots - 1) return CO_ERR_PROGRAM;
+            live_slots--;
+        }
+        // this instruction overwrites ACC: an ACC value still waiting on the
+        // operand stack (at most one) moves to the next free slot instead
+        for (Operand &o : s.opd) {
+            if (o.kind != OPD_ACC) continue;
+            if (live_slots >= kMaxSlots) return CO_ERR_BOUNDS;
+            const int slot = live_slots++;
+            if (live_slots > max_slots) max_slots = live_slots;
+            out[o.producer] |= (uint64_t)1 << 19 | (uint64_t)slot << 20;
+            o.kind = OPD_SLOT;
+            o.idx = slot;
+            o.producer = -1;
+        }
+        const int lo = s.cc[i + 1];
+        const int hi = s.cc[i + s.size[i]];
+        const int mid = bin ? s.cc[i + 1 + s.left[i]] : hi;
+        uint64_t w = (uint64_t)f | (uint64_t)(bin ? 1 : 0) << 6;
+        w |= (uint64_t)a.kind << 7 | (uint64_t)(a.idx & 15) << 9;
+        if (bin) w |= (uint64_t)b.kind << 13 | (uint64_t)(b.idx & 15) << 15;
+        w |= (uint64_t)lo << 24 | (uint64_t)mid << 29 | (uint64_t)hi << 34;
+        w |= (uint64_t)tape << 39;
+        tape += bin ? 2 : 1;
+        out[nins] = w;
+        s.opd.push_back({OPD_ACC, 0, nins});
+        nins++;
+    }
+    if (nins == 0) {
+        // the expression is one leaf: its value is the identity of that leaf
+        const Operand a = s.opd.back();
+        const int lo = s.cc[0], hi = s.cc[n];
+        uint64_t w = (uint64_t)OP_IDENT;
+        w |= (uint64_t)a.kind << 7 | (uint64_t)(a.idx & 15) << 9;
+        w |= (uint64_t)lo << 24 | (uint64_t)hi << 29 | (uint64_t)hi << 34;
+        w |= (uint64_t)tape << 39;
+        tape += 1;
+        out[nins++] = w;
     }
     if (tape > 255) return CO_ERR_BOUNDS;
-    // reverse sweep (prefix order): adjoint source and adjoint-stack depth
-    int asp = 0;
-    for (int i = 0; i < n; i++) {
-        uint64_t &w = out[n - 1 - i];
-        int apop = (i > 0 && (nt[i - 1] == NODE_VAR || nt[i - 1] == NODE_CONST)) ? 1 : 0;
-        if (apop && asp == 0) return CO_ERR_PROGRAM;
-        w |= (uint64_t)asp << 55 | (uint64_t)apop << 61;
-        asp -= apop;
-        if (nt[i] == NODE_BFUNC) asp++;
-        if (asp > CO_MAX_STACK) return CO_ERR_BOUNDS;
-    }
-    if (asp != 0) return CO_ERR_PROGRAM;
+    if (live_slots != 0) return CO_ERR_PROGRAM;
+    *n_ins = nins;
     *stack_depth = depth;
     *tape_slots = tape;
+    *slots_used = max_slots;
     return CO_OK;
 }
 
 int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
                       const int32_t *ci, const TreeMeta *metas, uint64_t *prog,
                       int32_t *order, int32_t *bin_start, ExprDesc *descs,
-                      int32_t *stack, Plan *plan) {
+                      int32_t *stack, int32_t *n_ins, Plan *plan) {
     if (!h || !metas) return CO_ERR_NULLARG;
     if (h->total_nodes > 0 && (!nt || !nv || !ci)) return CO_ERR_NULLARG;
     if (h->M_prob < 0 || h->N < 0 || h->n_vars < 0 || h->total_nodes < 0 || h->total_c < 0)
         return CO_ERR_NULLARG;
     if (h->K_max > CO_MAX_K || h->max_stack > CO_MAX_STACK || h->n_vars > CO_MAX_VARS)
         return CO_ERR_BOUNDS;
-    int M = h->M_prob;
+    const int M = h->M_prob;
     long ksum = 0, nsum = 0;
     for (int m = 0; m < M; m++) { ksum += metas[m].K; nsum += metas[m].n_nodes; }
     if (ksum != (long)h->total_c) return CO_ERR_SUM_C;
     if (nsum != (long)h->total_nodes) return CO_ERR_SUM_NODES;
 
+    std::vector<uint64_t> tmp;
+    if (!prog) {
+        tmp.assign(h->total_nodes > 0 ? h->total_nodes : 1, 0);
+        prog = tmp.data();
+    } else if (h->total_nodes > 0) {
+        memset(prog, 0, sizeof(uint64_t) * h->total_nodes);
+    }
     TreeScratch s;
-    int max_tape = 0, max_n = 0;
+    int max_tape = 0, max_n = 0, max_slots = 0;
     std::vector<int> count(CO_MAX_K + 1, 0);
-    std::vector<int32_t> depth(M), tapes(M), poff(M);
+    std::vector<int32_t> depth(M), tapes(M), poff(M), nins(M), slots(M);
     // programs are laid out expression after expression (prefix sum of
     // n_nodes), which equals node_offset for well-formed populations and
     // keeps overlapping metas from aliasing each other's instructions
@@ -173,12 +222,13 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
         if (t.K > CO_MAX_K) return CO_ERR_BOUNDS;
         poff[m] = (int32_t)run;
         int rc = decode_tree(nt + t.node_offset, nv + t.node_offset, ci + t.node_offset,
-                             t.n_nodes, t.K, h->n_vars, prog + run, &depth[m],
-                             &tapes[m], s);
+                             t.n_nodes, t.K, h->n_vars, prog + run, &nins[m], &depth[m],
+                             &tapes[m], &slots[m], s);
         if (rc != CO_OK) return rc;
         run += t.n_nodes;
         if (tapes[m] > max_tape) max_tape = tapes[m];
-        if (t.n_nodes > max_n) max_n = t.n_nodes;
+        if (nins[m] > max_n) max_n = nins[m];
+        if (slots[m] > max_slots) max_slots = slots[m];
         count[t.K]++;
     }
     // stable K bins, ascending
@@ -190,19 +240,20 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
     if (order) memcpy(order, ord.data(), sizeof(int32_t) * M);
     if (bin_start) memcpy(bin_start, start.data(), sizeof(int32_t) * (CO_MAX_K + 2));
     if (stack) memcpy(stack, depth.data(), sizeof(int32_t) * M);
+    if (n_ins) memcpy(n_ins, nins.data(), sizeof(int32_t) * M);
     if (descs) {
         // launch position p runs expression ord[M-1-p]: largest K first, so the
         // longest-running workgroups start earliest
         for (int p = 0; p < M; p++) {
-            int m = ord[M - 1 - p];
+            const int m = ord[M - 1 - p];
             ExprDesc &d = descs[p];
             d.prog_off = poff[m];
-            d.n = metas[m].n_nodes;
+            d.n = nins[m];
             d.c_off = metas[m].c_offset;
             d.K = metas[m].K;
             d.y_row = m;
             d.tape = tapes[m];
-            d.stack = depth[m];
+            d.slots = slots[m];
             d.pad = 0;
         }
     }
@@ -214,6 +265,7 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
         plan->total_c = h->total_c;
         plan->max_tape = max_tape;
         plan->max_n = max_n;
+        plan->max_slots = max_slots;
     }
     return CO_OK;
 }

@@ -1,26 +1,35 @@
 // program.h -- decoded expression programs shared by the host planner and
 // the device interpreter.
 //
-// Each pop.bin node (nt, nv, ci; cusr/kernel/pop_format.h:6-16) becomes one
-// 64-bit instruction. Instructions are stored in execution order, i.e. the
-// last prefix node first (the evaluation order of cusr/kernel/lm_core.cuh:67),
-// and carry everything the interpreter would otherwise track at run time:
+// An expression (pop.bin nt/nv/ci, cusr/kernel/pop_format.h:6-16, prefix
+// order) is evaluated last node first (cusr/kernel/lm_core.cuh:67). In that
+// order the left operand of every operator is produced immediately before the
+// operator itself, so the decoded program is a list of operator instructions
+// over three kinds of operand:
+//   ACC   the running value, i.e. the result of the previous instruction;
+//   SLOT  a spill slot holding a right operand computed before a left subtree
+//         that itself needed instructions (slots are used last-in first-out);
+//   VAR / CONST  a leaf, folded into the instruction that consumes it.
+// Leaves therefore cost no instruction; an expression that is a single leaf
+// becomes one OP_IDENT instruction.
 //
-//   bits  0..7   fid    operator id (NODE_UFUNC / NODE_BFUNC), else 0
-//   bits  8..9   kind   NODE_VAR / NODE_CONST / NODE_UFUNC / NODE_BFUNC
-//   bits 16..23  arg    variable index (VAR) or constant rank (CONST)
-//   bits 24..31  sp     value-stack depth before the instruction
-//   bits 32..36  lo     first constant rank of the (left) operand subtree
-//   bits 37..41  mid    end of the left range = start of the right range
-//   bits 42..46  hi     end of the operand ranks (unary: [lo, hi))
-//   bits 47..54  tape   first tape slot of the node's local partials
-//   bits 55..60  asp    adjoint-stack depth before the node, reverse sweep
-//   bit  61      apop   the node's adjoint comes from the adjoint stack
-//                       (it is a right child), not from the running value
-//
+// One 64-bit instruction per operator node, in execution order:
+//   bits  0..5   fid     operator id (include/pop_format.h), OP_IDENT = 63
+//   bit   6      binary
+//   bits  7..8   a_kind  left / only operand: OPD_ACC, OPD_VAR, OPD_CONST, OPD_SLOT
+//   bits  9..12  a_idx   variable index, constant rank or slot
+//   bits 13..14  b_kind  right operand (binary only)
+//   bits 15..18  b_idx
+//   bit  19      to_slot result goes to slot d_idx instead of ACC
+//   bits 20..23  d_idx
+//   bits 24..28  lo      constant ranks of the left / only operand: [lo, mid)
+//   bits 29..33  mid     constant ranks of the right operand: [mid, hi)
+//   bits 34..38  hi      (unary: mid == hi)
+//   bits 39..46  tape    first reverse-AD tape slot of this instruction
+//                        (one slot per operand)
 // Constants are ranked in prefix order (cusr/benchmark/popio.py:87-91), so the
-// constants of any subtree form one contiguous rank range; forward AD uses
-// that to scale only the ranks an operator can touch.
+// constants of a subtree form one contiguous rank range; forward AD scales
+// only those ranks.
 #pragma once
 
 #include <stdint.h>
@@ -29,6 +38,10 @@
 
 namespace cusr {
 
+enum { OPD_ACC = 0, OPD_VAR = 1, OPD_CONST = 2, OPD_SLOT = 3 };
+constexpr int OP_IDENT = 63;
+constexpr int kMaxSlots = 16;
+
 struct ExprDesc {          // one per expression, device-resident
     int32_t prog_off;      // first instruction
     int32_t n;             // instructions
@@ -36,32 +49,37 @@ struct ExprDesc {          // one per expression, device-resident
     int32_t K;             // constants
     int32_t y_row;         // row of ym / output index (original expression index)
     int32_t tape;          // reverse-mode tape slots
-    int32_t stack;         // value-stack depth
+    int32_t slots;         // spill slots
     int32_t pad;
 };
 
-static inline __host__ __device__ int ins_fid(uint64_t w) { return (int)(w & 0xffu); }
-static inline __host__ __device__ int ins_kind(uint64_t w) { return (int)((w >> 8) & 3u); }
-static inline __host__ __device__ int ins_arg(uint64_t w) { return (int)((w >> 16) & 0xffu); }
-static inline __host__ __device__ int ins_sp(uint64_t w) { return (int)((w >> 24) & 0xffu); }
-static inline __host__ __device__ int ins_lo(uint64_t w) { return (int)((w >> 32) & 31u); }
-static inline __host__ __device__ int ins_mid(uint64_t w) { return (int)((w >> 37) & 31u); }
-static inline __host__ __device__ int ins_hi(uint64_t w) { return (int)((w >> 42) & 31u); }
-static inline __host__ __device__ int ins_tape(uint64_t w) { return (int)((w >> 47) & 0xffu); }
-static inline __host__ __device__ int ins_asp(uint64_t w) { return (int)((w >> 55) & 63u); }
-static inline __host__ __device__ int ins_apop(uint64_t w) { return (int)((w >> 61) & 1u); }
+static inline __host__ __device__ int ins_fid(uint64_t w) { return (int)(w & 63u); }
+static inline __host__ __device__ int ins_binary(uint64_t w) { return (int)((w >> 6) & 1u); }
+static inline __host__ __device__ int ins_akind(uint64_t w) { return (int)((w >> 7) & 3u); }
+static inline __host__ __device__ int ins_aidx(uint64_t w) { return (int)((w >> 9) & 15u); }
+static inline __host__ __device__ int ins_bkind(uint64_t w) { return (int)((w >> 13) & 3u); }
+static inline __host__ __device__ int ins_bidx(uint64_t w) { return (int)((w >> 15) & 15u); }
+static inline __host__ __device__ int ins_toslot(uint64_t w) { return (int)((w >> 19) & 1u); }
+static inline __host__ __device__ int ins_didx(uint64_t w) { return (int)((w >> 20) & 15u); }
+static inline __host__ __device__ int ins_lo(uint64_t w) { return (int)((w >> 24) & 31u); }
+static inline __host__ __device__ int ins_mid(uint64_t w) { return (int)((w >> 29) & 31u); }
+static inline __host__ __device__ int ins_hi(uint64_t w) { return (int)((w >> 34) & 31u); }
+static inline __host__ __device__ int ins_tape(uint64_t w) { return (int)((w >> 39) & 255u); }
 
 struct Plan {
     int32_t M, N, D, total_nodes, total_c;
-    int32_t max_tape, max_n;
+    int32_t max_tape, max_n, max_slots;
 };
 
 // Check a population and decode it. Returns a CO_* code. On success fills
-// prog[total_nodes], order[M] (K-ascending stable bins), bin_start[CO_MAX_K+2],
-// descs[M] (indexed by launch position), stack[M] (indexed by expression).
+// prog[total_nodes] (expression m's instructions start at the prefix sum of
+// n_nodes; entries past its instruction count are 0), order[M] (stable K bins,
+// ascending), bin_start[CO_MAX_K+2], descs[M] (by launch position: largest K
+// first), stack[M] (value-stack depth, by expression), n_ins[M] (instructions
+// per expression). Any output pointer may be null.
 int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
                       const int32_t *ci, const TreeMeta *metas, uint64_t *prog,
                       int32_t *order, int32_t *bin_start, ExprDesc *descs,
-                      int32_t *stack, Plan *plan);
+                      int32_t *stack, int32_t *n_ins, Plan *plan);
 
 }  // namespace cusr

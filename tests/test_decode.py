@@ -1,0 +1,181 @@
+"""Host-side decode (co_decode through the C ABI, no GPU): bit-exact round trip
+of every program back to the pop.bin nodes, stack depths, K bins, error codes.
+
+The decoded program (cusr_amd/csrc/program.h) folds leaves into operands and
+keeps a running value plus spill slots; rebuilding the prefix node list from
+it must give back exactly nt / nv / ci, and the constant-rank ranges carried
+for forward AD must equal the ranks found in each operand subtree.
+"""
+import json
+
+import numpy as np
+import pytest
+
+from cusr_amd.benchmark import popio
+from cusr_amd.kernel import co_inproc as ci
+from oracle import lm_oracle
+from tests.helpers import GOLDEN, REF_FIX, ref_pop, synth
+
+OP_IDENT = 63
+
+
+def fields(w):
+    w = int(w)
+    return dict(fid=w & 63, bin=(w >> 6) & 1, ak=(w >> 7) & 3, ai=(w >> 9) & 15,
+                bk=(w >> 13) & 3, bi=(w >> 15) & 15, ts=(w >> 19) & 1, di=(w >> 20) & 15,
+                lo=(w >> 24) & 31, mid=(w >> 29) & 31, hi=(w >> 34) & 31, tape=(w >> 39) & 255)
+
+
+def rebuild(prog):
+    """Prefix node list [(nt, nv, ci)] from a decoded program, checking ranges."""
+    acc = None
+    slots = {}
+
+    def operand(kind, idx):
+        if kind == 0:
+            return acc
+        if kind == 1:
+            return [(0, float(idx), -1)]
+        if kind == 2:
+            return [(1, 0.0, idx)]
+        return slots.pop(idx)
+
+    def ranks(sub):
+        r = [c for t, _, c in sub if t == 1]
+        return (min(r), max(r) + 1) if r else None
+
+    for w in prog:
+        f = fields(w)
+        a = operand(f["ak"], f["ai"])
+        if f["fid"] == OP_IDENT:
+            sub = a
+        elif f["bin"]:
+            b = operand(f["bk"], f["bi"])
+            ra, rb = ranks(a), ranks(b)
+            if ra:
+                assert (f["lo"], f["mid"]) == ra
+            if rb:
+                assert (f["mid"], f["hi"]) == rb
+            sub = [(3, float(f["fid"]), -1)] + a + b
+        else:
+            ra = ranks(a)
+            if ra:
+                assert (f["lo"], f["hi"]) == ra
+            sub = [(2, float(f["fid"]), -1)] + a
+        if f["ts"]:
+            assert f["di"] not in slots
+            slots[f["di"]] = sub
+        else:
+            acc = sub
+    assert not slots
+    return acc
+
+
+def _pops():
+    pops = [ref_pop(n) for n in ("pop1000.bin", "pop_fixture.bin", "pop_fixture_op.bin",
+                                  "pop_fixture_stress.bin", "pop_fixture_scale_1e0.bin")]
+    pops += [synth("C1", 128, 32)[0], synth("C2", 256, 32)[0], synth("C3", 64, 32)[0],
+             synth("C5", 128, 32)[0]]
+    return pops
+
+
+@pytest.mark.parametrize("idx", range(9))
+def test_program_round_trip(idx):
+    pop = _pops()[idx]
+    rc, prog, order, bins, stack = ci.decode(pop)
+    assert rc == 0
+    off = 0
+    for m in range(pop["M"]):
+        o, n, _, K = (int(v) for v in pop["metas"][m])
+        nins = np.count_nonzero(prog[off:off + n])
+        nodes = rebuild(prog[off:off + nins])
+        assert [t for t, _, _ in nodes] == pop["nt"][o:o + n].tolist()
+        # nv of a CONST node carries nothing (the value lives in c_init)
+        nv = pop["nv"][o:o + n].astype(float)
+        nv[pop["nt"][o:o + n] == 1] = 0.0
+        assert [v for _, v, _ in nodes] == nv.tolist()
+        assert [c for _, _, c in nodes] == pop["ci"][o:o + n].tolist()
+        off += n
+
+
+@pytest.mark.parametrize("idx", range(9))
+def test_stack_depth_and_k_bins(idx):
+    pop = _pops()[idx]
+    rc, prog, order, bins, stack = ci.decode(pop)
+    assert rc == 0
+    K = pop["metas"][:, 3]
+    assert np.array_equal(order, np.argsort(K, kind="stable"))
+    assert np.array_equal(bins, np.concatenate([[0], np.cumsum(np.bincount(K, minlength=17))]))
+    for m in range(pop["M"]):
+        o, n, _, _ = (int(v) for v in pop["metas"][m])
+        assert stack[m] == popio.stack_depth(pop["nt"][o:o + n])
+    orc_rc, orc_stack = lm_oracle.check_pop(pop)
+    assert orc_rc == 0 and np.array_equal(orc_stack, stack)
+
+
+def test_reference_header_stats():
+    """pop1000.bin header matches the reference golden manifest."""
+    pop = ref_pop("pop1000.bin")
+    man = json.loads((REF_FIX / "golden_manifest.json").read_text())
+    h = man["variants"]["ad"]["pop1000"]["header"]
+    for k_ref, k in (("M_prob", "M"), ("total_nodes", "total_nodes"), ("total_c", "total_c"),
+                     ("N", "N"), ("n_vars", "n_vars"), ("K_max", "K_max"),
+                     ("max_stack", "max_stack")):
+        assert pop[k] == h[k_ref]
+    size = (REF_FIX / "pop1000.bin").stat().st_size
+    assert size == popio.pop_bytes(pop["M"], pop["total_nodes"], pop["total_c"], pop["N"],
+                                   pop["n_vars"]) == 4273688
+
+
+def _tiny():
+    # x0 * c0 + c1  ->  prefix [ADD, MUL, x0, c0, c1]
+    trees = [([3, 3, 0, 1, 1], [1, 3, 0, 0, 0], [-1, -1, -1, 0, 1], [1.0, 2.0])]
+    xs = np.linspace(-1, 1, 8).reshape(8, 1)
+    return popio.build_pop(trees, xs, np.zeros((1, 8)))
+
+
+def _code(pop):
+    return ci.decode(pop)[0]
+
+
+def test_error_codes():
+    good = _tiny()
+    assert _code(good) == 0
+    bad = dict(good); bad["total_c"] = 3
+    assert _code(bad) == ci.CO_ERR_SUM_C
+    bad = dict(good); bad["total_nodes"] = 6
+    assert _code(bad) == ci.CO_ERR_SUM_NODES
+    bad = dict(good); bad["nv"] = good["nv"].copy(); bad["nv"][0] = 29.0   # unknown op id
+    assert _code(bad) == ci.CO_ERR_PROGRAM
+    bad = dict(good); bad["nt"] = good["nt"].copy(); bad["nt"][0] = 4      # ternary node
+    assert _code(bad) == ci.CO_ERR_PROGRAM
+    bad = dict(good); bad["ci"] = good["ci"].copy(); bad["ci"][3] = 1      # ranks out of order
+    bad["ci"][4] = 0
+    assert _code(bad) == ci.CO_ERR_PROGRAM
+    bad = dict(good); bad["nv"] = good["nv"].copy(); bad["nv"][2] = 1.0    # var index >= n_vars
+    assert _code(bad) == ci.CO_ERR_PROGRAM
+    bad = dict(good); bad["nt"] = good["nt"].copy(); bad["nt"][1] = 2      # MUL as unary: stack
+    assert _code(bad) == ci.CO_ERR_PROGRAM
+    bad = dict(good); bad["K_max"] = 17
+    assert _code(bad) == ci.CO_ERR_BOUNDS
+    bad = dict(good); bad["n_vars"] = 9
+    assert _code(bad) == ci.CO_ERR_BOUNDS
+
+
+def test_bounds_k17():
+    nt = [3] * 16 + [1] * 17
+    nv = [1.0] * 16 + [0.0] * 17
+    cis = [-1] * 16 + list(range(17))
+    pop = popio.build_pop([(nt, nv, cis, np.zeros(17))], np.zeros((4, 1)), np.zeros((1, 4)))
+    assert pop["K_max"] == 17
+    assert _code(pop) == ci.CO_ERR_BOUNDS
+
+
+def test_library_exports_every_header_symbol():
+    import re
+    hdr = (GOLDEN.parents[1] / "include" / "cusr_co.h").read_text()
+    names = set(re.findall(r"^\s*(?:int|void)\s+(co_\w+)\s*\(", hdr, re.M))
+    assert names == set(ci.EXPORTED)
+    lib = ci.load_library()
+    for n in names:
+        assert hasattr(lib, n), n
