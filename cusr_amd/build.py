@@ -47,16 +47,21 @@ def _run(cmd):
     return err
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
+def build(jobs: int | None = None, verbose: bool = False, defines=(), out: Path | None = None,
+          cli: bool = True) -> Path:
+    """Compile everything; `defines` adds -D flags (tuning variants) and `out`
+    redirects the library (the CLI is only built for the default library)."""
     BUILD.mkdir(exist_ok=True)
+    extra = [f"-D{d}" for d in defines]
+    lib = Path(out) if out is not None else LIB
     jobs = jobs or min(8, os.cpu_count() or 4)
     compiles = []
     for rtype, ad, name in FIT_VARIANTS:
         obj = BUILD / f"fit_{name}.o"
-        compiles.append([HIPCC, *DEVICE_FLAGS, "-x", "hip", f"-DCUSR_FIT_R={rtype}",
+        compiles.append([HIPCC, *DEVICE_FLAGS, *extra, "-x", "hip", f"-DCUSR_FIT_R={rtype}",
                          f"-DCUSR_FIT_AD={ad}", f"-DCUSR_FIT_LAUNCH={name}", "-c",
                          str(CSRC / "fit_kernels.hip"), "-o", str(obj)])
-    compiles.append([HIPCC, *DEVICE_FLAGS, "-x", "hip", "-c", str(CSRC / "co_lib.hip"),
+    compiles.append([HIPCC, *DEVICE_FLAGS, *extra, "-x", "hip", "-c", str(CSRC / "co_lib.hip"),
                      "-o", str(BUILD / "co_lib.o")])
     compiles.append([HIPCC, *DEVICE_FLAGS, "-x", "hip", "-c", str(CSRC / "program.cpp"),
                      "-o", str(BUILD / "program.o")])
@@ -65,18 +70,21 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
             if verbose and err.strip():
                 print(err, file=sys.stderr)
     objs = [str(c[c.index("-o") + 1]) for c in compiles]
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs])
-    os.replace(tmp, LIB)
-    _run(["g++", "-O2", "-std=c++17", f"-I{REPO / 'include'}", "-o", str(CLI),
-          str(CSRC / "batch_lm_main.cpp"), f"-L{KDIR}", "-lcusr_co_ad",
-          "-Wl,-rpath,$ORIGIN"])
-    return LIB
+    os.replace(tmp, lib)
+    if cli and out is None:
+        _run(["g++", "-O2", "-std=c++17", f"-I{REPO / 'include'}", "-o", str(CLI),
+              str(CSRC / "batch_lm_main.cpp"), f"-L{KDIR}", "-lcusr_co_ad",
+              "-Wl,-rpath,$ORIGIN"])
+    return lib
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("-D", dest="defines", action="append", default=[])
+    ap.add_argument("--out", default=None)
     a = ap.parse_args()
-    print(build(a.jobs, a.verbose))
+    print(build(a.jobs, a.verbose, a.defines, a.out))

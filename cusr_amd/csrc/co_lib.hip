@@ -119,16 +119,26 @@ unsigned blocks_for(size_t n, unsigned t) { return (unsigned)((n + t - 1) / t); 
 // dynamic LDS per workgroup the fit kernels may request
 constexpr size_t kMaxDynLds = 64 * 1024;
 
-size_t fit_lds_bytes(bool mixed, bool rev, int K, int D, int slots, int tape) {
-    const bool small = K <= 8;
-    if (mixed) {
-        if (rev) return fit_lds_bytes_t<float, 1, CO_AD_REVERSE>(D, slots, tape);
-        return small ? fit_lds_bytes_t<float, 1, CO_AD_FORWARD>(D, slots, tape)
-                     : fit_lds_bytes_t<float, 16, CO_AD_FORWARD>(D, slots, tape);
+template <typename R, int AD>
+size_t lds_for_k(int K, int D, int slots, int tape) {
+    switch (K) {
+#define CUSR_LDS_CASE(k) \
+    case k: return fit_lds_bytes_t<R, k, AD>(D, slots, tape);
+    CUSR_LDS_CASE(0) CUSR_LDS_CASE(1) CUSR_LDS_CASE(2) CUSR_LDS_CASE(3) CUSR_LDS_CASE(4)
+    CUSR_LDS_CASE(5) CUSR_LDS_CASE(6) CUSR_LDS_CASE(7) CUSR_LDS_CASE(8) CUSR_LDS_CASE(9)
+    CUSR_LDS_CASE(10) CUSR_LDS_CASE(11) CUSR_LDS_CASE(12) CUSR_LDS_CASE(13)
+    CUSR_LDS_CASE(14) CUSR_LDS_CASE(15) CUSR_LDS_CASE(16)
+#undef CUSR_LDS_CASE
+    default: return 0;
     }
-    if (rev) return fit_lds_bytes_t<double, 1, CO_AD_REVERSE>(D, slots, tape);
-    return small ? fit_lds_bytes_t<double, 1, CO_AD_FORWARD>(D, slots, tape)
-                 : fit_lds_bytes_t<double, 16, CO_AD_FORWARD>(D, slots, tape);
+}
+
+size_t fit_lds_bytes(bool mixed, bool rev, int K, int D, int slots, int tape) {
+    if (mixed)
+        return rev ? lds_for_k<float, CO_AD_REVERSE>(K, D, slots, tape)
+                   : lds_for_k<float, CO_AD_FORWARD>(K, D, slots, tape);
+    return rev ? lds_for_k<double, CO_AD_REVERSE>(K, D, slots, tape)
+               : lds_for_k<double, CO_AD_FORWARD>(K, D, slots, tape);
 }
 
 // Check, decode and upload one population into the context (fp32 or fp64

@@ -43,12 +43,19 @@ constexpr float kCexpCap32 = 485165184.0f;         // exp(20) rounded to float
 // Points per lane per interpreter pass: more amortises the scalar fetch and
 // dispatch, fewer keeps registers (the J^T J sums dominate for large K) and
 // the reverse-AD tape in LDS small.
-#ifndef CUSR_P64
-#define CUSR_P64 1
+#ifndef CUSR_P64_K4
+#define CUSR_P64_K4 4   // fp64 forward, K <= 4
+#endif
+#ifndef CUSR_P64_K8
+#define CUSR_P64_K8 4   // fp64 forward, 5 <= K <= 8
 #endif
 template <typename R, int K, int AD>
 constexpr int points_per_pass() {
-    return (AD == CO_AD_REVERSE) ? 1 : (sizeof(R) == 4) ? (K <= 8 ? 4 : 2) : (K <= 8 ? CUSR_P64 : 1);
+    return (AD == CO_AD_REVERSE) ? 1
+           : (sizeof(R) == 4)    ? (K <= 8 ? 4 : 2)
+           : (K <= 4)            ? CUSR_P64_K4
+           : (K <= 8)            ? CUSR_P64_K8
+                                 : 1;
 }
 
 // scalar-cache view of the program (constant address space)
@@ -673,8 +680,11 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
 
 // One kernel per (K, precision, AD mode): each K gets its own register
 // allocation, so small-K expressions are not held to the occupancy of K = 16.
+#ifndef CUSR_WAVES_PER_EU
+#define CUSR_WAVES_PER_EU 1
+#endif
 template <int K, typename R, int AD>
-__global__ void __launch_bounds__(kLanes) lm_fit_kernel(FitArgs fa) {
+__global__ void __launch_bounds__(kLanes, CUSR_WAVES_PER_EU) lm_fit_kernel(FitArgs fa) {
     __shared__ double lds_c[2 * CO_MAX_K];
     __shared__ double lds_s[2 * sums_width(CO_MAX_K)];
     extern __shared__ char lds_dyn[];

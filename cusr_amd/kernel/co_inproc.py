@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import atexit
 import ctypes
+import os
 import threading
 from pathlib import Path
 
@@ -159,7 +160,10 @@ _LIBS: dict[str, ctypes.CDLL] = {}
 
 
 def load_library(variant: str = "ad", path: str | Path | None = None) -> ctypes.CDLL:
-    """dlopen the built library (no device call). Raises if it is not built."""
+    """dlopen the built library (no device call). Raises if it is not built.
+    CUSR_CO_LIB in the environment names another build of the same library."""
+    if path is None and os.environ.get("CUSR_CO_LIB"):
+        path = os.environ["CUSR_CO_LIB"]
     p = Path(path) if path is not None else lib_path(variant)
     key = str(p.resolve()) if p.exists() else str(p)
     if key not in _LIBS:

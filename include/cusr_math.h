@@ -36,8 +36,25 @@
 
 #if defined(__HIPCC__) || defined(__HIP__)
 #define CM_FN static inline __host__ __device__
+#define CM_TABLE static __constant__ const
 #else
 #define CM_FN static inline
+#define CM_TABLE static const
+#endif
+
+/* Coefficient tables. On the device a table is read through a pointer the
+ * optimizer cannot see through (an empty asm that "changes" it), so each
+ * call loads its coefficients into scalar registers with scalar loads instead
+ * of the compiler keeping every coefficient of every function resident in
+ * vector registers for the whole kernel. The values are the same on the host. */
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(CUSR_MATH_FOLD_TABLES)
+typedef const __attribute__((address_space(4))) double *cm_dtab;
+typedef const __attribute__((address_space(4))) float *cm_ftab;
+#define CM_TAB(T, name) ({ T t_ = (T)(name); __asm__ volatile("" : "+s"(t_)); t_; })
+#else
+typedef const double *cm_dtab;
+typedef const float *cm_ftab;
+#define CM_TAB(T, name) ((T)(name))
 #endif
 
 #ifdef __cplusplus
@@ -87,54 +104,46 @@ CM_FN float cm_pow2if(int k) { return cm_flt((uint32_t)(k + 127) << 23); }
 
 /* ------------------------------------------------------------------- exp */
 
+/* 1/ln2, ln2 head (32 bits), ln2 tail, then 1/13!, 1/12!, ..., 1/2!, 1, 1 */
+CM_TABLE double cm_exp_tab[17] = {
+    1.4426950408889634, 0.6931471803691238, 1.9082149288430703e-10,
+    1.6059043836821613e-10, 2.08767569878681e-09, 2.505210838544172e-08,
+    2.755731922398589e-07, 2.7557319223985893e-06, 2.48015873015873e-05,
+    0.0001984126984126984, 0.001388888888888889, 0.008333333333333333,
+    0.041666666666666664, 0.16666666666666666, 0.5, 1.0, 1.0};
+
 CM_FN double cm_exp(double x) {
     if (cm_isnan(x)) return x;
     if (x > 709.782712893384) return CM_INF;
     if (x < -745.1332191019412) return 0.0;
-    const double inv_ln2 = 1.4426950408889634;
-    const double ln2_hi = 0.6931471803691238;
-    const double ln2_lo = 1.9082149288430703e-10;
-    double kf = cm_rint_small(x * inv_ln2);
-    double r = CM_FMA(-kf, ln2_hi, x);
-    r = CM_FMA(-kf, ln2_lo, r);
-    double p = 1.6059043836821613e-10;            /* 1/13! */
-    p = CM_FMA(p, r, 2.08767569878681e-09);       /* 1/12! */
-    p = CM_FMA(p, r, 2.505210838544172e-08);
-    p = CM_FMA(p, r, 2.755731922398589e-07);
-    p = CM_FMA(p, r, 2.7557319223985893e-06);
-    p = CM_FMA(p, r, 2.48015873015873e-05);
-    p = CM_FMA(p, r, 0.0001984126984126984);
-    p = CM_FMA(p, r, 0.001388888888888889);
-    p = CM_FMA(p, r, 0.008333333333333333);
-    p = CM_FMA(p, r, 0.041666666666666664);
-    p = CM_FMA(p, r, 0.16666666666666666);
-    p = CM_FMA(p, r, 0.5);
-    p = CM_FMA(p, r, 1.0);
-    p = CM_FMA(p, r, 1.0);
+    cm_dtab t = CM_TAB(cm_dtab, cm_exp_tab);
+    double kf = cm_rint_small(x * t[0]);
+    double r = CM_FMA(-kf, t[1], x);
+    r = CM_FMA(-kf, t[2], r);
+    double p = t[3];
+    for (int i = 4; i < 17; i++) p = CM_FMA(p, r, t[i]);
     int k = (int)kf;
     if (k >= -1020 && k <= 1022) return p * cm_pow2i(k);
     if (k > 1022) return (p * cm_pow2i(k - 2)) * 4.0;
     return (p * cm_pow2i(k + 1000)) * cm_pow2i(-1000);
 }
 
+/* 1/ln2, ln2 head (16 bits), ln2 tail, then 1/7!, ..., 1/2!, 1, 1 */
+CM_TABLE float cm_expf_tab[11] = {
+    1.4426950216293335f, 0.693145751953125f, 1.4285906217992306e-06f,
+    0.00019841270113829523f, 0.0013888889225199819f, 0.008333333767950535f,
+    0.0416666679084301f, 0.1666666716337204f, 0.5f, 1.0f, 1.0f};
+
 CM_FN float cm_expf(float x) {
     if (x != x) return x;
     if (x > 88.72283f) return CM_INFF;
     if (x < -103.97208f) return 0.0f;
-    const float inv_ln2 = 1.4426950216293335f;
-    const float ln2_hi = 0.693145751953125f;
-    const float ln2_lo = 1.4285906217992306e-06f;
-    float kf = cm_rint_smallf(x * inv_ln2);
-    float r = CM_FMAF(-kf, ln2_hi, x);
-    r = CM_FMAF(-kf, ln2_lo, r);
-    float p = 0.00019841270113829523f;            /* 1/7! */
-    p = CM_FMAF(p, r, 0.0013888889225199819f);
-    p = CM_FMAF(p, r, 0.008333333767950535f);
-    p = CM_FMAF(p, r, 0.0416666679084301f);
-    p = CM_FMAF(p, r, 0.1666666716337204f);
-    p = CM_FMAF(p, r, 0.5f);
-    p = CM_FMAF(p, r, 1.0f);
-    p = CM_FMAF(p, r, 1.0f);
+    cm_ftab t = CM_TAB(cm_ftab, cm_expf_tab);
+    float kf = cm_rint_smallf(x * t[0]);
+    float r = CM_FMAF(-kf, t[1], x);
+    r = CM_FMAF(-kf, t[2], r);
+    float p = t[3];
+    for (int i = 4; i < 11; i++) p = CM_FMAF(p, r, t[i]);
     int k = (int)kf;
     if (k >= -124 && k <= 126) return p * cm_pow2if(k);
     if (k > 126) return (p * cm_pow2if(k - 2)) * 4.0f;
@@ -142,6 +151,12 @@ CM_FN float cm_expf(float x) {
 }
 
 /* ------------------------------------------------------------------- log */
+
+/* 2/23, 2/21, ..., 2/3, then ln2 head and tail */
+CM_TABLE double cm_log_tab[13] = {
+    0.08695652173913043, 0.09523809523809523, 0.10526315789473684, 0.11764705882352941,
+    0.13333333333333333, 0.15384615384615385, 0.18181818181818182, 0.2222222222222222,
+    0.2857142857142857, 0.4, 0.6666666666666666, 0.6931471803691238, 1.9082149288430703e-10};
 
 CM_FN double cm_log(double x) {
     if (cm_isnan(x)) return x;
@@ -160,24 +175,19 @@ CM_FN double cm_log(double x) {
     double f = m - 1.0;
     double s = f / (2.0 + f);
     double z = s * s;
-    double R = 0.08695652173913043;               /* 2/23 */
-    R = CM_FMA(R, z, 0.09523809523809523);
-    R = CM_FMA(R, z, 0.10526315789473684);
-    R = CM_FMA(R, z, 0.11764705882352941);
-    R = CM_FMA(R, z, 0.13333333333333333);
-    R = CM_FMA(R, z, 0.15384615384615385);
-    R = CM_FMA(R, z, 0.18181818181818182);
-    R = CM_FMA(R, z, 0.2222222222222222);
-    R = CM_FMA(R, z, 0.2857142857142857);
-    R = CM_FMA(R, z, 0.4);
-    R = CM_FMA(R, z, 0.6666666666666666);
+    cm_dtab t = CM_TAB(cm_dtab, cm_log_tab);
+    double R = t[0];
+    for (int i = 1; i < 11; i++) R = CM_FMA(R, z, t[i]);
     R = R * z;
     double hfsq = 0.5 * (f * f);
     double dk = (double)e;
-    const double ln2_hi = 0.6931471803691238;
-    const double ln2_lo = 1.9082149288430703e-10;
-    return dk * ln2_hi - ((hfsq - (s * (hfsq + R) + dk * ln2_lo)) - f);
+    return dk * t[11] - ((hfsq - (s * (hfsq + R) + dk * t[12])) - f);
 }
+
+/* 2/13, ..., 2/3, then ln2 head and tail */
+CM_TABLE float cm_logf_tab[8] = {
+    0.1538461595773697f, 0.1818181872367859f, 0.2222222238779068f, 0.2857142984867096f,
+    0.4000000059604645f, 0.6666666865348816f, 0.693145751953125f, 1.4285906217992306e-06f};
 
 CM_FN float cm_logf(float x) {
     if (x != x) return x;
@@ -196,45 +206,39 @@ CM_FN float cm_logf(float x) {
     float f = m - 1.0f;
     float s = f / (2.0f + f);
     float z = s * s;
-    float R = 0.1538461595773697f;                /* 2/13 */
-    R = CM_FMAF(R, z, 0.1818181872367859f);
-    R = CM_FMAF(R, z, 0.2222222238779068f);
-    R = CM_FMAF(R, z, 0.2857142984867096f);
-    R = CM_FMAF(R, z, 0.4000000059604645f);
-    R = CM_FMAF(R, z, 0.6666666865348816f);
+    cm_ftab t = CM_TAB(cm_ftab, cm_logf_tab);
+    float R = t[0];
+    for (int i = 1; i < 6; i++) R = CM_FMAF(R, z, t[i]);
     R = R * z;
     float hfsq = 0.5f * (f * f);
     float dk = (float)e;
-    const float ln2_hi = 0.693145751953125f;
-    const float ln2_lo = 1.4285906217992306e-06f;
-    return dk * ln2_hi - ((hfsq - (s * (hfsq + R) + dk * ln2_lo)) - f);
+    return dk * t[6] - ((hfsq - (s * (hfsq + R) + dk * t[7])) - f);
 }
 
 /* --------------------------------------------------------------- sin/cos */
 
-CM_FN double cm_sin_kernel(double r) {
+/* sin: 1/17!, -1/15!, ..., -1/3!; cos: -1/18!, 1/16!, ..., 1/4!;
+ * then 2/pi and pi/2 as three doubles */
+CM_TABLE double cm_trig_tab[20] = {
+    2.8114572543455206e-15, -7.647163731819816e-13, 1.6059043836821613e-10,
+    -2.505210838544172e-08, 2.7557319223985893e-06, -0.0001984126984126984,
+    0.008333333333333333, -0.16666666666666666,
+    -1.5619206968586225e-16, 4.779477332387385e-14, -1.1470745597729725e-11,
+    2.08767569878681e-09, -2.755731922398589e-07, 2.48015873015873e-05,
+    -0.001388888888888889, 0.041666666666666664,
+    0.6366197723675814, 1.5707963267948966, 6.123233995736766e-17, -1.4973849048591698e-33};
+
+CM_FN double cm_sin_kernel(double r, cm_dtab t) {
     double z = r * r;
-    double p = 2.8114572543455206e-15;            /* 1/17! */
-    p = CM_FMA(p, z, -7.647163731819816e-13);
-    p = CM_FMA(p, z, 1.6059043836821613e-10);
-    p = CM_FMA(p, z, -2.505210838544172e-08);
-    p = CM_FMA(p, z, 2.7557319223985893e-06);
-    p = CM_FMA(p, z, -0.0001984126984126984);
-    p = CM_FMA(p, z, 0.008333333333333333);
-    p = CM_FMA(p, z, -0.16666666666666666);
+    double p = t[0];
+    for (int i = 1; i < 8; i++) p = CM_FMA(p, z, t[i]);
     return CM_FMA(r * z, p, r);
 }
 
-CM_FN double cm_cos_kernel(double r) {
+CM_FN double cm_cos_kernel(double r, cm_dtab t) {
     double z = r * r;
-    double p = -1.5619206968586225e-16;           /* -1/18! */
-    p = CM_FMA(p, z, 4.779477332387385e-14);
-    p = CM_FMA(p, z, -1.1470745597729725e-11);
-    p = CM_FMA(p, z, 2.08767569878681e-09);
-    p = CM_FMA(p, z, -2.755731922398589e-07);
-    p = CM_FMA(p, z, 2.48015873015873e-05);
-    p = CM_FMA(p, z, -0.001388888888888889);
-    p = CM_FMA(p, z, 0.041666666666666664);
+    double p = t[8];
+    for (int i = 9; i < 16; i++) p = CM_FMA(p, z, t[i]);
     double hz = 0.5 * z;
     double w = 1.0 - hz;
     return w + (((1.0 - w) - hz) + z * (z * p));
@@ -244,13 +248,14 @@ CM_FN double cm_cos_kernel(double r) {
 CM_FN void cm_sincos(double x, double *s, double *c) {
     if (cm_isnan(x) || cm_fabs(x) == CM_INF) { *s = CM_NAN; *c = CM_NAN; return; }
     if (cm_fabs(x) >= 1125899906842624.0) { *s = 0.0; *c = 1.0; return; } /* 2^50 */
-    double kf = cm_rint_small(x * 0.6366197723675814);
-    double r = CM_FMA(-kf, 1.5707963267948966, x);
-    r = CM_FMA(-kf, 6.123233995736766e-17, r);
-    r = CM_FMA(-kf, -1.4973849048591698e-33, r);
+    cm_dtab t = CM_TAB(cm_dtab, cm_trig_tab);
+    double kf = cm_rint_small(x * t[16]);
+    double r = CM_FMA(-kf, t[17], x);
+    r = CM_FMA(-kf, t[18], r);
+    r = CM_FMA(-kf, t[19], r);
     double q4 = kf - 4.0 * cm_rint_small(kf * 0.25 - 0.375); /* kf mod 4, in 0..3 */
     int q = (int)q4;
-    double sr = cm_sin_kernel(r), cr = cm_cos_kernel(r);
+    double sr = cm_sin_kernel(r, t), cr = cm_cos_kernel(r, t);
     switch (q & 3) {
     case 0: *s = sr; *c = cr; break;
     case 1: *s = cr; *c = -sr; break;
@@ -263,23 +268,26 @@ CM_FN double cm_sin(double x) { double s, c; cm_sincos(x, &s, &c); return s; }
 CM_FN double cm_cos(double x) { double s, c; cm_sincos(x, &s, &c); return c; }
 CM_FN double cm_tan(double x) { double s, c; cm_sincos(x, &s, &c); return s / c; }
 
-CM_FN float cm_sin_kernelf(float r) {
+/* sin: -1/11!, ..., -1/3!; cos: 1/12!, ..., 1/4!; then 2/pi and pi/2 as
+ * three floats */
+CM_TABLE float cm_trigf_tab[14] = {
+    -2.5052107943679403e-08f, 2.7557318844628753e-06f, -0.00019841270113829523f,
+    0.008333333767950535f, -0.1666666716337204f,
+    2.0876755879584152e-09f, -2.755731998149713e-07f, 2.4801587642286904e-05f,
+    -0.0013888889225199819f, 0.0416666679084301f,
+    0.6366197466850281f, 1.5707963705062866f, -4.371138828673793e-08f, -1.7151245100058819e-15f};
+
+CM_FN float cm_sin_kernelf(float r, cm_ftab t) {
     float z = r * r;
-    float p = -2.5052107943679403e-08f;           /* -1/11! */
-    p = CM_FMAF(p, z, 2.7557318844628753e-06f);
-    p = CM_FMAF(p, z, -0.00019841270113829523f);
-    p = CM_FMAF(p, z, 0.008333333767950535f);
-    p = CM_FMAF(p, z, -0.1666666716337204f);
+    float p = t[0];
+    for (int i = 1; i < 5; i++) p = CM_FMAF(p, z, t[i]);
     return CM_FMAF(r * z, p, r);
 }
 
-CM_FN float cm_cos_kernelf(float r) {
+CM_FN float cm_cos_kernelf(float r, cm_ftab t) {
     float z = r * r;
-    float p = 2.0876755879584152e-09f;            /* 1/12! */
-    p = CM_FMAF(p, z, -2.755731998149713e-07f);
-    p = CM_FMAF(p, z, 2.4801587642286904e-05f);
-    p = CM_FMAF(p, z, -0.0013888889225199819f);
-    p = CM_FMAF(p, z, 0.0416666679084301f);
+    float p = t[5];
+    for (int i = 6; i < 10; i++) p = CM_FMAF(p, z, t[i]);
     float hz = 0.5f * z;
     float w = 1.0f - hz;
     return w + (((1.0f - w) - hz) + z * (z * p));
@@ -288,13 +296,14 @@ CM_FN float cm_cos_kernelf(float r) {
 CM_FN void cm_sincosf(float x, float *s, float *c) {
     if (x != x || cm_fabsf(x) == CM_INFF) { *s = CM_NANF; *c = CM_NANF; return; }
     if (cm_fabsf(x) >= 2097152.0f) { *s = 0.0f; *c = 1.0f; return; } /* 2^21 */
-    float kf = cm_rint_smallf(x * 0.6366197466850281f);
-    float r = CM_FMAF(-kf, 1.5707963705062866f, x);
-    r = CM_FMAF(-kf, -4.371138828673793e-08f, r);
-    r = CM_FMAF(-kf, -1.7151245100058819e-15f, r);
+    cm_ftab t = CM_TAB(cm_ftab, cm_trigf_tab);
+    float kf = cm_rint_smallf(x * t[10]);
+    float r = CM_FMAF(-kf, t[11], x);
+    r = CM_FMAF(-kf, t[12], r);
+    r = CM_FMAF(-kf, t[13], r);
     float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
     int q = (int)q4;
-    float sr = cm_sin_kernelf(r), cr = cm_cos_kernelf(r);
+    float sr = cm_sin_kernelf(r, t), cr = cm_cos_kernelf(r, t);
     switch (q & 3) {
     case 0: *s = sr; *c = cr; break;
     case 1: *s = cr; *c = -sr; break;
@@ -309,21 +318,21 @@ CM_FN float cm_tanf(float x) { float s, c; cm_sincosf(x, &s, &c); return s / c; 
 
 /* ------------------------------------------------------ hyperbolic, pow */
 
+/* 1/19!, 1/17!, ..., 1/3! */
+CM_TABLE double cm_sinh_tab[9] = {
+    8.22063524662433e-18, 2.8114572543455206e-15, 7.647163731819816e-13,
+    1.6059043836821613e-10, 2.505210838544172e-08, 2.7557319223985893e-06,
+    0.0001984126984126984, 0.008333333333333333, 0.16666666666666666};
+
 CM_FN double cm_sinh(double x) {
     if (cm_isnan(x)) return x;
     double a = cm_fabs(x);
     double r;
     if (a < 1.0) {
+        cm_dtab t = CM_TAB(cm_dtab, cm_sinh_tab);
         double z = a * a;
-        double p = 8.22063524662433e-18;          /* 1/19! */
-        p = CM_FMA(p, z, 2.8114572543455206e-15);
-        p = CM_FMA(p, z, 7.647163731819816e-13);
-        p = CM_FMA(p, z, 1.6059043836821613e-10);
-        p = CM_FMA(p, z, 2.505210838544172e-08);
-        p = CM_FMA(p, z, 2.7557319223985893e-06);
-        p = CM_FMA(p, z, 0.0001984126984126984);
-        p = CM_FMA(p, z, 0.008333333333333333);
-        p = CM_FMA(p, z, 0.16666666666666666);
+        double p = t[0];
+        for (int i = 1; i < 9; i++) p = CM_FMA(p, z, t[i]);
         r = CM_FMA(a * z, p, a);
     } else if (a < 709.0) {
         double e = cm_exp(a);
@@ -359,17 +368,20 @@ CM_FN double cm_tanh(double x) {
     return x < 0.0 ? -r : r;
 }
 
+/* 1/11!, ..., 1/3! */
+CM_TABLE float cm_sinhf_tab[5] = {
+    2.5052107943679403e-08f, 2.7557318844628753e-06f, 0.00019841270113829523f,
+    0.008333333767950535f, 0.1666666716337204f};
+
 CM_FN float cm_sinhf(float x) {
     if (x != x) return x;
     float a = cm_fabsf(x);
     float r;
     if (a < 1.0f) {
+        cm_ftab t = CM_TAB(cm_ftab, cm_sinhf_tab);
         float z = a * a;
-        float p = 2.5052107943679403e-08f;        /* 1/11! */
-        p = CM_FMAF(p, z, 2.7557318844628753e-06f);
-        p = CM_FMAF(p, z, 0.00019841270113829523f);
-        p = CM_FMAF(p, z, 0.008333333767950535f);
-        p = CM_FMAF(p, z, 0.1666666716337204f);
+        float p = t[0];
+        for (int i = 1; i < 5; i++) p = CM_FMAF(p, z, t[i]);
         r = CM_FMAF(a * z, p, a);
     } else if (a < 88.0f) {
         float e = cm_expf(a);
