@@ -718,3 +718,38 @@ int orc_pass_api(const PopHeader *h, const int32_t *nt, const float *nv, const i
     free(p);
     return CO_OK;
 }
+
+/* Elementary functions of include/cusr_math.h over arrays, for the accuracy
+ * tests against the C library. fn: 0 exp, 1 log, 2 sin, 3 cos, 4 tan, 5 sinh,
+ * 6 cosh, 7 tanh, 8 pow(x, y); +16 for the fp32 versions (inputs rounded to
+ * float, results widened). */
+int orc_math(int fn, int n, const double *x, const double *y, double *out) {
+    for (int i = 0; i < n; i++) {
+        double a = x[i], b = y ? y[i] : 0.0;
+        float af = (float)a, bf = (float)b;
+        double r;
+        switch (fn) {
+        case 0: r = cm_exp(a); break;
+        case 1: r = cm_log(a); break;
+        case 2: r = cm_sin(a); break;
+        case 3: r = cm_cos(a); break;
+        case 4: r = cm_tan(a); break;
+        case 5: r = cm_sinh(a); break;
+        case 6: r = cm_cosh(a); break;
+        case 7: r = cm_tanh(a); break;
+        case 8: r = cm_pow(a, b); break;
+        case 16: r = cm_expf(af); break;
+        case 17: r = cm_logf(af); break;
+        case 18: r = cm_sinf(af); break;
+        case 19: r = cm_cosf(af); break;
+        case 20: r = cm_tanf(af); break;
+        case 21: r = cm_sinhf(af); break;
+        case 22: r = cm_coshf(af); break;
+        case 23: r = cm_tanhf(af); break;
+        case 24: r = cm_powf(af, bf); break;
+        default: return CO_ERR_NULLARG;
+        }
+        out[i] = r;
+    }
+    return CO_OK;
+}

@@ -166,3 +166,20 @@ def pass_sums(pop, m, c, xs=None, y=None, precision=CO_PREC_FP64, ad_mode=CO_AD_
     if rc != 0:
         raise RuntimeError(f"orc_pass_api returned {rc}")
     return loss.value, jtj[:K, :K], jtr[:K]
+
+
+MATH = {"exp": 0, "log": 1, "sin": 2, "cos": 3, "tan": 4, "sinh": 5, "cosh": 6, "tanh": 7,
+        "pow": 8}
+
+
+def math_fn(name, x, y=None, fp32=False):
+    """include/cusr_math.h function `name` over arrays (fp32 variant if fp32)."""
+    code = MATH[name] + (16 if fp32 else 0)
+    xa, px = _p(x, np.float64)
+    ya, py = (_p(y, np.float64) if y is not None else (None, None))
+    out = np.zeros(xa.size)
+    rc = lib().orc_math(ctypes.c_int(code), ctypes.c_int(xa.size), px, py,
+                        out.ctypes.data_as(ctypes.c_void_p))
+    if rc != 0:
+        raise RuntimeError(f"orc_math returned {rc}")
+    return out
