@@ -1,0 +1,126 @@
+"""Summarise a rocprofv3 database (rocpd SQLite) as a markdown table.
+
+    python -m cusr_amd.benchmark.prof_summary trace  <run_results.db> [--match lm_fit]
+    python -m cusr_amd.benchmark.prof_summary pmc    <run_results.db> [--match lm_fit]
+    python -m cusr_amd.benchmark.prof_summary traffic <fetch.db> <write.db> --kernel NAME
+           --copy-bytes B [--out JSON --workload-key KEY]
+
+trace: per kernel, calls and average / min / max / total duration plus the
+register and grid figures of the dispatch. pmc: per kernel, the average of
+every counter per dispatch. traffic: HBM bytes per dispatch of one kernel from
+a FETCH_SIZE run and a WRITE_SIZE run, each scaled by the ratio of the known
+bytes of the copy calibration kernel (bench.py --copy-calibration: the
+elementwise kernel with the largest grid) to what the same counter read for it.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import json
+import sqlite3
+import statistics
+
+
+def _rows(db, sql):
+    con = sqlite3.connect(db)
+    try:
+        return con.execute(sql).fetchall()
+    finally:
+        con.close()
+
+
+def trace(db, match=None):
+    rows = _rows(db, "select name, duration, vgpr_count, accum_vgpr_count, sgpr_count, "
+                     "scratch_size, lds_size, grid_x, workgroup_x from kernels")
+    by = collections.defaultdict(list)
+    meta = {}
+    for name, dur, vg, ag, sg, scr, lds, gx, wx in rows:
+        if match and match not in name:
+            continue
+        by[name].append(dur / 1e6)
+        meta[name] = (vg, ag, sg, scr, lds, gx // max(wx, 1))
+    out = ["| kernel | calls | avg ms | min ms | max ms | total ms | VGPR | AGPR | SGPR "
+           "| scratch B | LDS B | workgroups |", "|" + "---|" * 12]
+    for name in sorted(by, key=lambda n: -sum(by[n])):
+        d = by[name]
+        vg, ag, sg, scr, lds, wg = meta[name]
+        out.append(f"| `{name}` | {len(d)} | {statistics.mean(d):.3f} | {min(d):.3f} | "
+                   f"{max(d):.3f} | {sum(d):.2f} | {vg} | {ag} | {sg} | {scr} | {lds} | {wg} |")
+    return "\n".join(out)
+
+
+def pmc_per_dispatch(db, match=None):
+    rows = _rows(db, "select kernel_name, dispatch_id, counter_name, sum(value) "
+                     "from counters_collection group by kernel_name, dispatch_id, counter_name")
+    acc = collections.defaultdict(lambda: collections.defaultdict(list))
+    for name, _disp, ctr, val in rows:
+        if match and match not in name:
+            continue
+        acc[name][ctr].append(val)
+    return {k: {c: statistics.mean(v) for c, v in d.items()} for k, d in acc.items()}
+
+
+def pmc(db, match=None):
+    d = pmc_per_dispatch(db, match)
+    ctrs = sorted({c for v in d.values() for c in v})
+    out = ["| kernel | " + " | ".join(ctrs) + " |", "|" + "---|" * (len(ctrs) + 1)]
+    for name in sorted(d):
+        out.append(f"| `{name}` | " + " | ".join(f"{d[name].get(c, float('nan')):.6g}"
+                                                 for c in ctrs) + " |")
+    return "\n".join(out)
+
+
+def _copy_kernel(d):
+    cands = [k for k in d if "elementwise" in k]
+    if not cands:
+        raise SystemExit("no copy calibration kernel in the database")
+    return cands[0]
+
+
+def traffic(fetch_db, write_db, kernel, copy_bytes):
+    f = pmc_per_dispatch(fetch_db)
+    w = pmc_per_dispatch(write_db)
+    ck = _copy_kernel(f)
+    # FETCH_SIZE and WRITE_SIZE are in KiB per dispatch
+    f_scale = copy_bytes / (1024.0 * f[ck]["FETCH_SIZE"])
+    w_scale = copy_bytes / (1024.0 * w[_copy_kernel(w)]["WRITE_SIZE"])
+    kf = [k for k in f if kernel in k]
+    kw = [k for k in w if kernel in k]
+    if len(kf) != 1 or len(kw) != 1:
+        raise SystemExit(f"kernel {kernel!r} matches {kf} / {kw}")
+    fetch_b = 1024.0 * f[kf[0]]["FETCH_SIZE"] * f_scale
+    write_b = 1024.0 * w[kw[0]]["WRITE_SIZE"] * w_scale
+    return {"kernel": kf[0], "fetch_bytes": fetch_b, "write_bytes": write_b,
+            "bytes_per_launch": fetch_b + write_b, "fetch_scale": f_scale,
+            "write_scale": w_scale, "copy_kernel": ck, "copy_bytes": copy_bytes,
+            "fetch_kib_raw": f[kf[0]]["FETCH_SIZE"], "write_kib_raw": w[kw[0]]["WRITE_SIZE"],
+            "copy_fetch_kib_raw": f[ck]["FETCH_SIZE"],
+            "copy_write_kib_raw": w[_copy_kernel(w)]["WRITE_SIZE"]}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("mode", choices=["trace", "pmc", "traffic"])
+    ap.add_argument("dbs", nargs="+")
+    ap.add_argument("--match", default=None)
+    ap.add_argument("--kernel", default=None)
+    ap.add_argument("--copy-bytes", type=float, default=float(1 << 30))
+    ap.add_argument("--out", default=None)
+    ap.add_argument("--workload-key", default=None)
+    a = ap.parse_args()
+    if a.mode == "trace":
+        print(trace(a.dbs[0], a.match))
+    elif a.mode == "pmc":
+        print(pmc(a.dbs[0], a.match))
+    else:
+        t = traffic(a.dbs[0], a.dbs[1], a.kernel, a.copy_bytes)
+        if a.workload_key:
+            t["workload_key"] = a.workload_key
+        print(json.dumps(t, indent=1))
+        if a.out:
+            with open(a.out, "w") as fh:
+                json.dump(t, fh, indent=1)
+
+
+if __name__ == "__main__":
+    main()

@@ -70,9 +70,12 @@ struct Ctx {
     hipEvent_t ev_start = nullptr;
     hipEvent_t ev_done[kStreams] = {};
     hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr;  // timing pair around the fit launches
+    hipEvent_t ev_b0[CO_MAX_K + 1] = {}, ev_b1[CO_MAX_K + 1] = {};  // per K-bin launch
+    bool bin_launched[CO_MAX_K + 1] = {};
     Plan plan = {};
     bool resident = false;
     double last_kernel_ms = -1.0;
+    double last_bin_ms[CO_MAX_K + 1] = {};
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
     std::vector<uint64_t> h_prog;
     std::vector<ExprDesc> h_desc;
@@ -227,6 +230,10 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     const Plan &plan = ctx->plan;
     const int M = plan.M, C = plan.total_c;
     ctx->last_kernel_ms = 0.0;
+    for (int k = 0; k <= CO_MAX_K; ++k) {
+        ctx->bin_launched[k] = false;
+        ctx->last_bin_ms[k] = -1.0;
+    }
     if (M == 0) return CO_OK;
     hipStream_t s = ctx->stream;
     FitArgs fa;
@@ -273,7 +280,10 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         fk.desc = fa.desc + pos;
         fk.slots = slots;
         fk.tape = tape;
+        CO_HIP(hipEventRecord(ctx->ev_b0[k], ks));
         CO_HIP(launch(k, (unsigned)cnt, lds, ks, fk));
+        CO_HIP(hipEventRecord(ctx->ev_b1[k], ks));
+        ctx->bin_launched[k] = true;
         pos += cnt;
         ++nb;
     }
@@ -293,6 +303,11 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     float ms = 0.0f;
     CO_HIP(hipEventElapsedTime(&ms, ctx->ev_t0, ctx->ev_t1));
     ctx->last_kernel_ms = ms;
+    for (int k = 0; k <= CO_MAX_K; ++k) {
+        if (!ctx->bin_launched[k]) continue;
+        CO_HIP(hipEventElapsedTime(&ms, ctx->ev_b0[k], ctx->ev_b1[k]));
+        ctx->last_bin_ms[k] = ms;
+    }
     return CO_OK;
 }
 
@@ -342,6 +357,10 @@ extern "C" int co_init(int device_id, void **handle_out) {
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t0);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t1);
+    for (int k = 0; k <= CO_MAX_K && e == hipSuccess; ++k) {
+        e = hipEventCreate(&ctx->ev_b0[k]);
+        if (e == hipSuccess) e = hipEventCreate(&ctx->ev_b1[k]);
+    }
     for (int i = 0; i < kStreams && e == hipSuccess; ++i)
         e = hipEventCreateWithFlags(&ctx->ev_done[i], hipEventDisableTiming);
     if (e != hipSuccess) {
@@ -490,6 +509,13 @@ extern "C" int co_last_kernel_ms(void *handle, double *fit_ms_out) {
     return CO_OK;
 }
 
+extern "C" int co_last_bin_ms(void *handle, double *bin_ms_out) {
+    if (!handle || !bin_ms_out) return CO_ERR_NULLARG;
+    const Ctx *ctx = (const Ctx *)handle;
+    for (int k = 0; k <= CO_MAX_K; ++k) bin_ms_out[k] = ctx->last_bin_ms[k];
+    return CO_OK;
+}
+
 extern "C" int co_last_split(double *setup_ms_out, double *loop_ms_out) {
     if (setup_ms_out) *setup_ms_out = g_setup_ms;
     if (loop_ms_out) *loop_ms_out = g_loop_ms;
@@ -512,5 +538,9 @@ extern "C" void co_teardown(void *handle) {
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_t0) (void)hipEventDestroy(ctx->ev_t0);
     if (ctx->ev_t1) (void)hipEventDestroy(ctx->ev_t1);
+    for (int k = 0; k <= CO_MAX_K; ++k) {
+        if (ctx->ev_b0[k]) (void)hipEventDestroy(ctx->ev_b0[k]);
+        if (ctx->ev_b1[k]) (void)hipEventDestroy(ctx->ev_b1[k]);
+    }
     delete ctx;
 }

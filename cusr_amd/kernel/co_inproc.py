@@ -96,7 +96,7 @@ _HERE = Path(__file__).resolve().parent
 # every extern "C" symbol of include/cusr_co.h
 EXPORTED = ("co_init", "co_optimize", "co_last_split", "co_teardown", "co_options_default",
             "co_optimize_ex", "co_eval_ex", "co_upload_ex", "co_fit_resident",
-            "co_last_kernel_ms", "co_decode")
+            "co_last_kernel_ms", "co_last_bin_ms", "co_decode")
 
 
 def lib_path(variant: str = "ad") -> Path:
@@ -145,6 +145,8 @@ def _bind(lib) -> None:
     lib.co_fit_resident.restype = ctypes.c_int
     lib.co_last_kernel_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
     lib.co_last_kernel_ms.restype = ctypes.c_int
+    lib.co_last_bin_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
+    lib.co_last_bin_ms.restype = ctypes.c_int
     lib.co_decode.argtypes = [ctypes.POINTER(PopHeader)] + [_VP] * 8
     lib.co_decode.restype = ctypes.c_int
     lib.co_last_split.argtypes = [ctypes.POINTER(dbl), ctypes.POINTER(dbl)]
@@ -363,6 +365,14 @@ class InProcessCO:
         if rc != CO_OK:
             raise COError(rc, "co_last_kernel_ms")
         return v.value
+
+    def last_bin_ms(self) -> np.ndarray:
+        """Per-K-bin kernel durations of the last fit (ms, -1 for empty bins)."""
+        v = (ctypes.c_double * (CO_MAX_K + 1))()
+        rc = self._lib.co_last_bin_ms(self._handle, v)
+        if rc != CO_OK:
+            raise COError(rc, "co_last_bin_ms")
+        return np.asarray(v[:], dtype=np.float64)
 
     def last_split(self):
         """(setup_ms, loop_ms) of the last fit on this process."""

@@ -140,6 +140,12 @@ int co_fit_resident(void *handle, const CoOptions *opt,
  * handle's stream before the first and after the last fit kernel. */
 int co_last_kernel_ms(void *handle, double *fit_ms_out);
 
+/* Per-launch device time of the last fit: bin_ms_out[k] (CO_MAX_K + 1
+ * entries) is the duration of the fit kernel of the K = k bin, from HIP events
+ * recorded around that launch on the stream it ran on; -1 for bins with no
+ * expressions. No counterpart in the reference (measurement only). */
+int co_last_bin_ms(void *handle, double *bin_ms_out);
+
 /* Host-only decode of a population, no device needed: runs every check
  * co_optimize runs before touching the device and returns its code
  * (0, 2, -2, -3, -4, -6). When it returns 0 and the pointers are non-NULL:
