@@ -70,28 +70,31 @@ def cpu_baseline(pop, sample, min_seconds=10.0, max_seconds=30.0):
             "wall_s": wall}
 
 
-def copy_calibration(gib=1.0):
-    """One plain copy kernel of known size (torch elementwise y = x * 1 over
-    `gib` GiB of fp64) for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE."""
-    import torch
-
-    n = int(gib * (1 << 30)) // 8
-    x = torch.ones(n, dtype=torch.float64, device="cuda:0")
-    y = x * 1.0
-    torch.cuda.synchronize()
-    print(f"[bench] copy calibration: {8 * n} bytes read, {8 * n} bytes written",
-          file=sys.stderr, flush=True)
-    del x, y
+def copy_calibration(co, pop):
+    """One plain copy kernel of known size for scaling rocprofv3 FETCH_SIZE /
+    WRITE_SIZE: the reference's fp32 entry point (co_optimize, zero
+    iterations) widens y on the device with one elementwise kernel that reads
+    4*M*N and writes 8*M*N bytes (widen_kernel, the largest of its launches)."""
+    n = int(pop["M"]) * int(pop["N"])
+    co.optimize(pop, 0)
+    print(f"[bench] copy calibration: widen_kernel over {n} values, {4 * n} bytes read, "
+          f"{8 * n} bytes written", file=sys.stderr, flush=True)
 
 
-def load_traffic(workload_key):
-    """HBM bytes per launch of the dominant kernel, from the committed
-    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel)."""
+def load_traffic(workload_key, kernel):
+    """HBM bytes per launch of `kernel`, from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel), when that
+    summary was taken on this workload."""
     p = REPO / "profiles" / "lm_fit_c2_traffic.json"
     if not p.exists():
         return None
     d = json.loads(p.read_text())
-    return d if d.get("workload_key") == workload_key else None
+    if d.get("workload_key") != workload_key:
+        return None
+    for name, v in d["kernels"].items():
+        if kernel in name:
+            return v["bytes_per_launch"]
+    return None
 
 
 def main():
@@ -103,7 +106,7 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=16384)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run one 1 GiB copy kernel (for rocprofv3 --pmc scaling)")
+                    help="also run one copy kernel of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build measures "
@@ -125,7 +128,7 @@ def main():
     print(f"[bench] generated {cfg.name}: M={pop['M']} N={pop['N']} nodes={pop['total_nodes']} "
           f"K_max={pop['K_max']} in {t_gen:.1f}s", file=sys.stderr, flush=True)
     if args.copy_calibration:
-        copy_calibration()
+        copy_calibration(co, pop)
     fit_kw = dict(ad_mode=cfg.ad_mode, precision=cfg.precision)
     co.upload(pop)
     for _ in range(args.warmup):
@@ -139,6 +142,10 @@ def main():
     wall = time.perf_counter() - t0
     ms_per_step = 1e3 * wall / args.steps
     res = co.fit_resident(cfg.max_iter, **fit_kw)
+    # end-to-end from host buffers (upload over PCIe + fit + read-back), untimed above
+    t_e2e = time.perf_counter()
+    co.optimize_ex(pop, cfg.max_iter, **fit_kw)
+    e2e_ms = 1e3 * (time.perf_counter() - t_e2e)
     K = pop["metas"][:, 3]
     n_fit = int(np.count_nonzero(K > 0))
     value = n_fit / (ms_per_step / 1e3)
@@ -157,8 +164,8 @@ def main():
           file=sys.stderr, flush=True)
     print("[bench] per-bin kernel ms: " + " ".join(f"K{k}={v:.2f}" for k, v in enumerate(bins)
                                                   if v >= 0), file=sys.stderr, flush=True)
-    workload_key = f"{cfg.name}:{pop['M']}x{pop['N']}:seed{cfg.seed}:it{cfg.max_iter}:{kname}"
-    traffic = load_traffic(workload_key)
+    workload_key = f"{cfg.name}:{pop['M']}x{pop['N']}:seed{cfg.seed}:it{cfg.max_iter}"
+    traffic = load_traffic(workload_key, kname)
 
     cpu = None
     if not args.no_cpu:
@@ -189,7 +196,7 @@ def main():
                    "max_iter": cfg.max_iter, "seed": cfg.seed},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic["bytes_per_launch"] if traffic else None,
+                     "traffic": traffic,
                      "kernel": kname, "expressions_in_launch": int(np.sum(K == kdom)),
                      "launch_ms": float(bins[kdom]),
                      "algorithmic_bytes_per_launch": wdom["bytes"],
@@ -201,6 +208,7 @@ def main():
         "fit": {"status_counts": status_counts, "mean_iters": float(res["iters"].mean()),
                 "device_ms_per_fit": kms, "fits_per_s_device": n_fit / (kms / 1e3),
                 "hbm_gbs_whole_fit": wall_fit["bytes"] / (kms / 1e3) / 1e9,
+                "e2e_ms_from_host": e2e_ms, "fits_per_s_from_host": n_fit / (e2e_ms / 1e3),
                 "fp64_tflops_whole_fit": wall_fit["flops"] / (kms / 1e3) / 1e12,
                 "bin_ms": {str(k): float(v) for k, v in enumerate(bins) if v >= 0}},
     }

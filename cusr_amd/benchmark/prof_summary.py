@@ -3,14 +3,15 @@
     python -m cusr_amd.benchmark.prof_summary trace  <run_results.db> [--match lm_fit]
     python -m cusr_amd.benchmark.prof_summary pmc    <run_results.db> [--match lm_fit]
     python -m cusr_amd.benchmark.prof_summary traffic <fetch.db> <write.db> --kernel NAME
-           --copy-bytes B [--out JSON --workload-key KEY]
+           --calib-fetch-bytes F --calib-write-bytes W [--out JSON --workload-key KEY]
 
 trace: per kernel, calls and average / min / max / total duration plus the
 register and grid figures of the dispatch. pmc: per kernel, the average of
-every counter per dispatch. traffic: HBM bytes per dispatch of one kernel from
+every counter per dispatch. traffic: HBM bytes per dispatch of each matching kernel from
 a FETCH_SIZE run and a WRITE_SIZE run, each scaled by the ratio of the known
 bytes of the copy calibration kernel (bench.py --copy-calibration: the
-elementwise kernel with the largest grid) to what the same counter read for it.
+widen_kernel dispatch with the largest grid) to what the same counter read
+for it.
 """
 from __future__ import annotations
 
@@ -70,32 +71,38 @@ def pmc(db, match=None):
     return "\n".join(out)
 
 
-def _copy_kernel(d):
-    cands = [k for k in d if "elementwise" in k]
-    if not cands:
-        raise SystemExit("no copy calibration kernel in the database")
-    return cands[0]
+def _calib(db, counter):
+    """Counter value of the largest widen_kernel dispatch."""
+    rows = _rows(db, "select dispatch_id, max(grid_size), sum(value) from counters_collection "
+                     f"where kernel_name like '%widen_kernel%' and counter_name = '{counter}' "
+                     "group by dispatch_id order by max(grid_size) desc limit 1")
+    if not rows:
+        raise SystemExit("no copy calibration kernel (widen_kernel) in " + db)
+    return rows[0][2]
 
 
-def traffic(fetch_db, write_db, kernel, copy_bytes):
-    f = pmc_per_dispatch(fetch_db)
-    w = pmc_per_dispatch(write_db)
-    ck = _copy_kernel(f)
+def traffic(fetch_db, write_db, kernel, calib_fetch, calib_write):
+    """Per kernel whose name contains `kernel`: HBM bytes per dispatch."""
+    f = pmc_per_dispatch(fetch_db, kernel)
+    w = pmc_per_dispatch(write_db, kernel)
+    if not f or sorted(f) != sorted(w):
+        raise SystemExit(f"kernel {kernel!r} matches {sorted(f)} / {sorted(w)}")
     # FETCH_SIZE and WRITE_SIZE are in KiB per dispatch
-    f_scale = copy_bytes / (1024.0 * f[ck]["FETCH_SIZE"])
-    w_scale = copy_bytes / (1024.0 * w[_copy_kernel(w)]["WRITE_SIZE"])
-    kf = [k for k in f if kernel in k]
-    kw = [k for k in w if kernel in k]
-    if len(kf) != 1 or len(kw) != 1:
-        raise SystemExit(f"kernel {kernel!r} matches {kf} / {kw}")
-    fetch_b = 1024.0 * f[kf[0]]["FETCH_SIZE"] * f_scale
-    write_b = 1024.0 * w[kw[0]]["WRITE_SIZE"] * w_scale
-    return {"kernel": kf[0], "fetch_bytes": fetch_b, "write_bytes": write_b,
-            "bytes_per_launch": fetch_b + write_b, "fetch_scale": f_scale,
-            "write_scale": w_scale, "copy_kernel": ck, "copy_bytes": copy_bytes,
-            "fetch_kib_raw": f[kf[0]]["FETCH_SIZE"], "write_kib_raw": w[kw[0]]["WRITE_SIZE"],
-            "copy_fetch_kib_raw": f[ck]["FETCH_SIZE"],
-            "copy_write_kib_raw": w[_copy_kernel(w)]["WRITE_SIZE"]}
+    cf, cw = _calib(fetch_db, "FETCH_SIZE"), _calib(write_db, "WRITE_SIZE")
+    f_scale = calib_fetch / (1024.0 * cf)
+    w_scale = calib_write / (1024.0 * cw)
+    out = {"calib_kernel": "widen_kernel", "calib_fetch_bytes": calib_fetch,
+           "calib_write_bytes": calib_write, "calib_fetch_kib_raw": cf,
+           "calib_write_kib_raw": cw, "fetch_scale": f_scale, "write_scale": w_scale,
+           "kernels": {}}
+    for name in sorted(f):
+        fetch_b = 1024.0 * f[name]["FETCH_SIZE"] * f_scale
+        write_b = 1024.0 * w[name]["WRITE_SIZE"] * w_scale
+        out["kernels"][name] = {"fetch_bytes": fetch_b, "write_bytes": write_b,
+                                "bytes_per_launch": fetch_b + write_b,
+                                "fetch_kib_raw": f[name]["FETCH_SIZE"],
+                                "write_kib_raw": w[name]["WRITE_SIZE"]}
+    return out
 
 
 def main():
@@ -104,7 +111,8 @@ def main():
     ap.add_argument("dbs", nargs="+")
     ap.add_argument("--match", default=None)
     ap.add_argument("--kernel", default=None)
-    ap.add_argument("--copy-bytes", type=float, default=float(1 << 30))
+    ap.add_argument("--calib-fetch-bytes", type=float, default=None)
+    ap.add_argument("--calib-write-bytes", type=float, default=None)
     ap.add_argument("--out", default=None)
     ap.add_argument("--workload-key", default=None)
     a = ap.parse_args()
@@ -113,7 +121,7 @@ def main():
     elif a.mode == "pmc":
         print(pmc(a.dbs[0], a.match))
     else:
-        t = traffic(a.dbs[0], a.dbs[1], a.kernel, a.copy_bytes)
+        t = traffic(a.dbs[0], a.dbs[1], a.kernel, a.calib_fetch_bytes, a.calib_write_bytes)
         if a.workload_key:
             t["workload_key"] = a.workload_key
         print(json.dumps(t, indent=1))
