@@ -43,19 +43,18 @@ constexpr float kCexpCap32 = 485165184.0f;         // exp(20) rounded to float
 // Points per lane per interpreter pass: more amortises the scalar fetch and
 // dispatch, fewer keeps registers (the J^T J sums dominate for large K) and
 // the reverse-AD tape in LDS small.
-#ifndef CUSR_P64_K4
-#define CUSR_P64_K4 4   // fp64 forward, K <= 4
+// Per-K tables for fp64 forward AD, K = 0..16 (overridable for tuning).
+#ifndef CUSR_P64_TABLE
+#define CUSR_P64_TABLE 4, 4, 4, 4, 4, 4, 4, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
-#ifndef CUSR_P64_K8
-#define CUSR_P64_K8 4   // fp64 forward, 5 <= K <= 8
+#ifndef CUSR_P32_TABLE
+#define CUSR_P32_TABLE 4, 4, 4, 4, 4, 4, 4, 4, 4, 2, 2, 2, 2, 2, 2, 2, 2
 #endif
+constexpr int kP64[CO_MAX_K + 1] = {CUSR_P64_TABLE};
+constexpr int kP32[CO_MAX_K + 1] = {CUSR_P32_TABLE};
 template <typename R, int K, int AD>
 constexpr int points_per_pass() {
-    return (AD == CO_AD_REVERSE) ? 1
-           : (sizeof(R) == 4)    ? (K <= 8 ? 4 : 2)
-           : (K <= 4)            ? CUSR_P64_K4
-           : (K <= 8)            ? CUSR_P64_K8
-                                 : 1;
+    return (AD == CO_AD_REVERSE) ? 1 : (sizeof(R) == 4) ? kP32[K] : kP64[K];
 }
 
 // scalar-cache view of the program (constant address space)
@@ -453,22 +452,26 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
 #pragma unroll
     for (int q = 0; q < W; ++q) acc[q] = 0.0;
     const int batches = (a.N + kLanes * P - 1) / (kLanes * P);
+    const int last = a.N - 1;
     for (int bt = 0; bt < batches; ++bt) {
+        // Every load of the batch is issued before the first one is used:
+        // points past N read point N-1 (in bounds, never accumulated), so no
+        // load sits behind a branch and one memory latency covers the batch.
         double yv[P];
         bool valid[P];
+        int ic[P];
         CUSR_FOR_P {
             const int i = lane + kLanes * (bt * P + p);
             valid[p] = i < a.N;
-            yv[p] = valid[p] ? a.y[i] : 0.0;
+            ic[p] = valid[p] ? i : last;
         }
-#pragma unroll
-        for (int v = 0; v < CO_MAX_VARS; ++v) {
-            if (v < a.D) {
-                CUSR_FOR_P {
-                    const int i = lane + kLanes * (bt * P + p);
-                    lds_at<R, P>(w.x, v, p, lane) = valid[p] ? (R)a.X[(size_t)v * a.N + i] : R(0);
-                }
-            }
+        CUSR_FOR_P yv[p] = a.y[ic[p]];
+#pragma unroll 2
+        for (int v = 0; v < a.D; ++v) {
+            const double *col = a.X + (size_t)v * a.N;
+            double xv[P];
+            CUSR_FOR_P xv[p] = col[ic[p]];
+            CUSR_FOR_P lds_at<R, P>(w.x, v, p, lane) = (R)xv[p];
         }
         R accv[P];
         R T[P * KT];
@@ -680,11 +683,21 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
 
 // One kernel per (K, precision, AD mode): each K gets its own register
 // allocation, so small-K expressions are not held to the occupancy of K = 16.
-#ifndef CUSR_WAVES_PER_EU
-#define CUSR_WAVES_PER_EU 1
+// Minimum waves per SIMD the register allocation must allow, per K (fp64
+// forward / everything else); 2 caps a kernel at 256 VGPRs.
+#ifndef CUSR_W64_TABLE
+#define CUSR_W64_TABLE 1, 1, 1, 2, 2, 2, 2, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
+#ifndef CUSR_WAVES_OTHER
+#define CUSR_WAVES_OTHER 1
+#endif
+constexpr int kW64[CO_MAX_K + 1] = {CUSR_W64_TABLE};
+template <typename R, int K, int AD>
+constexpr int waves_per_eu() {
+    return (sizeof(R) == 8 && AD == CO_AD_FORWARD) ? kW64[K] : CUSR_WAVES_OTHER;
+}
 template <int K, typename R, int AD>
-__global__ void __launch_bounds__(kLanes, CUSR_WAVES_PER_EU) lm_fit_kernel(FitArgs fa) {
+__global__ void __launch_bounds__(kLanes, (waves_per_eu<R, K, AD>())) lm_fit_kernel(FitArgs fa) {
     __shared__ double lds_c[2 * CO_MAX_K];
     __shared__ double lds_s[2 * sums_width(CO_MAX_K)];
     extern __shared__ char lds_dyn[];

@@ -36,24 +36,39 @@
 
 #if defined(__HIPCC__) || defined(__HIP__)
 #define CM_FN static inline __host__ __device__
-#define CM_TABLE static __constant__ const
 #else
 #define CM_FN static inline
-#define CM_TABLE static const
 #endif
 
-/* Coefficient tables. On the device a table is read through a pointer the
- * optimizer cannot see through (an empty asm that "changes" it), so each
- * call loads its coefficients into scalar registers with scalar loads instead
- * of the compiler keeping every coefficient of every function resident in
- * vector registers for the whole kernel. The values are the same on the host. */
+/* Coefficient tables. The device pass keeps them in constant memory, read
+ * only from __device__ accessors: a __constant__ variable referenced from a
+ * __host__ __device__ function is made host-visible and addressed through the
+ * GOT (one more dependent scalar load per use). The accessor hands out a
+ * pointer the optimizer cannot see through (an empty asm that "changes" it),
+ * so each call loads its coefficients into scalar registers with scalar loads
+ * instead of the compiler keeping every coefficient of every function resident
+ * in vector registers for the whole kernel. Every other compile (the host pass
+ * of hipcc, gcc for the oracle) sees plain static arrays of the same values. */
 #if defined(__HIP_DEVICE_COMPILE__) && !defined(CUSR_MATH_FOLD_TABLES)
 typedef const __attribute__((address_space(4))) double *cm_dtab;
 typedef const __attribute__((address_space(4))) float *cm_ftab;
-#define CM_TAB(T, name) ({ T t_ = (T)(name); __asm__ volatile("" : "+s"(t_)); t_; })
+#define CM_TABLE static __constant__ const
+#define CM_ACCESSOR(T, name)                                              \
+    static __device__ __forceinline__ T name##_ptr() {                    \
+        T t_ = (T)(name);                                                 \
+        __asm__ volatile("" : "+s"(t_));                                  \
+        return t_;                                                        \
+    }
+#define CM_TAB(T, name) (name##_ptr())
 #else
 typedef const double *cm_dtab;
 typedef const float *cm_ftab;
+#if defined(__HIP_DEVICE_COMPILE__)
+#define CM_TABLE static __constant__ const
+#else
+#define CM_TABLE static const
+#endif
+#define CM_ACCESSOR(T, name)
 #define CM_TAB(T, name) ((T)(name))
 #endif
 
@@ -111,6 +126,7 @@ CM_TABLE double cm_exp_tab[17] = {
     2.755731922398589e-07, 2.7557319223985893e-06, 2.48015873015873e-05,
     0.0001984126984126984, 0.001388888888888889, 0.008333333333333333,
     0.041666666666666664, 0.16666666666666666, 0.5, 1.0, 1.0};
+CM_ACCESSOR(cm_dtab, cm_exp_tab)
 
 CM_FN double cm_exp(double x) {
     if (cm_isnan(x)) return x;
@@ -133,6 +149,7 @@ CM_TABLE float cm_expf_tab[11] = {
     1.4426950216293335f, 0.693145751953125f, 1.4285906217992306e-06f,
     0.00019841270113829523f, 0.0013888889225199819f, 0.008333333767950535f,
     0.0416666679084301f, 0.1666666716337204f, 0.5f, 1.0f, 1.0f};
+CM_ACCESSOR(cm_ftab, cm_expf_tab)
 
 CM_FN float cm_expf(float x) {
     if (x != x) return x;
@@ -157,6 +174,7 @@ CM_TABLE double cm_log_tab[13] = {
     0.08695652173913043, 0.09523809523809523, 0.10526315789473684, 0.11764705882352941,
     0.13333333333333333, 0.15384615384615385, 0.18181818181818182, 0.2222222222222222,
     0.2857142857142857, 0.4, 0.6666666666666666, 0.6931471803691238, 1.9082149288430703e-10};
+CM_ACCESSOR(cm_dtab, cm_log_tab)
 
 CM_FN double cm_log(double x) {
     if (cm_isnan(x)) return x;
@@ -188,6 +206,7 @@ CM_FN double cm_log(double x) {
 CM_TABLE float cm_logf_tab[8] = {
     0.1538461595773697f, 0.1818181872367859f, 0.2222222238779068f, 0.2857142984867096f,
     0.4000000059604645f, 0.6666666865348816f, 0.693145751953125f, 1.4285906217992306e-06f};
+CM_ACCESSOR(cm_ftab, cm_logf_tab)
 
 CM_FN float cm_logf(float x) {
     if (x != x) return x;
@@ -227,6 +246,7 @@ CM_TABLE double cm_trig_tab[20] = {
     2.08767569878681e-09, -2.755731922398589e-07, 2.48015873015873e-05,
     -0.001388888888888889, 0.041666666666666664,
     0.6366197723675814, 1.5707963267948966, 6.123233995736766e-17, -1.4973849048591698e-33};
+CM_ACCESSOR(cm_dtab, cm_trig_tab)
 
 CM_FN double cm_sin_kernel(double r, cm_dtab t) {
     double z = r * r;
@@ -276,6 +296,7 @@ CM_TABLE float cm_trigf_tab[14] = {
     2.0876755879584152e-09f, -2.755731998149713e-07f, 2.4801587642286904e-05f,
     -0.0013888889225199819f, 0.0416666679084301f,
     0.6366197466850281f, 1.5707963705062866f, -4.371138828673793e-08f, -1.7151245100058819e-15f};
+CM_ACCESSOR(cm_ftab, cm_trigf_tab)
 
 CM_FN float cm_sin_kernelf(float r, cm_ftab t) {
     float z = r * r;
@@ -323,6 +344,7 @@ CM_TABLE double cm_sinh_tab[9] = {
     8.22063524662433e-18, 2.8114572543455206e-15, 7.647163731819816e-13,
     1.6059043836821613e-10, 2.505210838544172e-08, 2.7557319223985893e-06,
     0.0001984126984126984, 0.008333333333333333, 0.16666666666666666};
+CM_ACCESSOR(cm_dtab, cm_sinh_tab)
 
 CM_FN double cm_sinh(double x) {
     if (cm_isnan(x)) return x;
@@ -372,6 +394,7 @@ CM_FN double cm_tanh(double x) {
 CM_TABLE float cm_sinhf_tab[5] = {
     2.5052107943679403e-08f, 2.7557318844628753e-06f, 0.00019841270113829523f,
     0.008333333767950535f, 0.1666666716337204f};
+CM_ACCESSOR(cm_ftab, cm_sinhf_tab)
 
 CM_FN float cm_sinhf(float x) {
     if (x != x) return x;
