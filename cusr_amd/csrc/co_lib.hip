@@ -76,6 +76,7 @@ struct Ctx {
     bool resident = false;
     double last_kernel_ms = -1.0;
     double last_bin_ms[CO_MAX_K + 1] = {};
+    size_t max_dyn_lds = 0;  // dynamic LDS one workgroup may use on this device
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
     std::vector<uint64_t> h_prog;
     std::vector<ExprDesc> h_desc;
@@ -119,8 +120,9 @@ T *ptr(DevBuf &b) { return (T *)b.p; }
 
 unsigned blocks_for(size_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
 
-// dynamic LDS per workgroup the fit kernels may request
-constexpr size_t kMaxDynLds = 64 * 1024;
+// static LDS of the fit kernel (constants and pass sums), kept out of the
+// dynamic budget
+constexpr size_t kStaticLds = 2 * CO_MAX_K * 8 + 2 * 153 * 8;
 
 template <typename R, int AD>
 size_t lds_for_k(int K, int D, int slots, int tape) {
@@ -255,6 +257,8 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     fa.xtol = opt.xtol;
     const bool rev = opt.ad_mode == CO_AD_REVERSE;
     const bool mixed = opt.precision == CO_PREC_MIXED;
+    const int parts = opt.partitions ? opt.partitions : co_partitions_for_n(plan.N);
+    if (parts != 1 && parts != 2 && parts != 4) return CO_ERR_NULLARG;
     const FitLauncher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
                                      : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
     // descriptors are in launch order, largest K first; one launch per K bin,
@@ -272,14 +276,23 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         }
         if (cnt == 0) continue;
         if (!rev) tape = 0;
-        const size_t lds = fit_lds_bytes(mixed, rev, k, plan.D, slots, tape);
-        if (lds > kMaxDynLds) return CO_ERR_BOUNDS;
+        // per-wavefront areas, then the partition sums; fewer wavefronts per
+        // workgroup (each summing several partitions) when LDS is short
+        const size_t wave_bytes = (fit_lds_bytes(mixed, rev, k, plan.D, slots, tape) + 15) & ~(size_t)15;
+        const size_t part_bytes = parts > 1 ? (size_t)parts * (1 + k + k * (k + 1) / 2) * 8 : 0;
+        int pwaves = parts;
+        while (pwaves > 1 && pwaves * wave_bytes + part_bytes > ctx->max_dyn_lds) pwaves /= 2;
+        const size_t lds = pwaves * wave_bytes + part_bytes;
+        if (lds > ctx->max_dyn_lds) return CO_ERR_BOUNDS;
         hipStream_t ks = ctx->lanes[nb % kStreams];
         if (nb < kStreams) CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
         FitArgs fk = fa;
         fk.desc = fa.desc + pos;
         fk.slots = slots;
         fk.tape = tape;
+        fk.parts = parts;
+        fk.pwaves = pwaves;
+        fk.wave_bytes = (int)wave_bytes;
         CO_HIP(hipEventRecord(ctx->ev_b0[k], ks));
         CO_HIP(launch(k, (unsigned)cnt, lds, ks, fk));
         CO_HIP(hipEventRecord(ctx->ev_b1[k], ks));
@@ -351,7 +364,12 @@ extern "C" int co_init(int device_id, void **handle_out) {
     Ctx *ctx = new (std::nothrow) Ctx();
     if (!ctx) return CO_ERR_OOM;
     ctx->device = device_id;
-    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    int lds_per_block = 0;
+    hipError_t e = hipDeviceGetAttribute(&lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock,
+                                         device_id);
+    if (e == hipSuccess)
+        ctx->max_dyn_lds = lds_per_block > (int)kStaticLds ? (size_t)lds_per_block - kStaticLds : 0;
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     for (int i = 0; i < kStreams && e == hipSuccess; ++i)
         e = hipStreamCreateWithFlags(&ctx->lanes[i], hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming);

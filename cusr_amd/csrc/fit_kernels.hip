@@ -10,10 +10,12 @@
 namespace cusr {
 
 hipError_t CUSR_FIT_LAUNCH(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa) {
+    if (fa.pwaves < 1 || fa.pwaves > CO_MAX_PARTITIONS || fa.parts % fa.pwaves != 0)
+        return hipErrorInvalidValue;
     switch (K) {
 #define CUSR_CASE(k)                                                                   \
     case k:                                                                            \
-        lm_fit_kernel<k, CUSR_FIT_R, CUSR_FIT_AD><<<grid, kLanes, lds, s>>>(fa);       \
+        lm_fit_kernel<k, CUSR_FIT_R, CUSR_FIT_AD><<<grid, kLanes * fa.pwaves, lds, s>>>(fa); \
         break;
         CUSR_CASE(0) CUSR_CASE(1) CUSR_CASE(2) CUSR_CASE(3) CUSR_CASE(4) CUSR_CASE(5)
         CUSR_CASE(6) CUSR_CASE(7) CUSR_CASE(8) CUSR_CASE(9) CUSR_CASE(10) CUSR_CASE(11)

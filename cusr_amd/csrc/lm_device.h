@@ -421,6 +421,10 @@ struct PassArgs {
     const double *X;    // [D][N] column-major
     const double *y;    // this expression's targets [N]
     int N, D;
+    int parts;          // point partitions G (64-point granule g -> partition g mod G)
+    int pwaves;         // wavefronts of the workgroup; wave w sums partitions w, w+pwaves, ...
+    int wave;           // this wavefront
+    double *part;       // LDS [parts][sums_width(K)] partition sums (parts > 1)
 };
 
 constexpr int sums_width(int K) { return 1 + K + K * (K + 1) / 2; }
@@ -440,6 +444,12 @@ __device__ __forceinline__ void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 }
 
+// LDS visibility for every wavefront of the workgroup (pwaves uniform).
+__device__ __forceinline__ void block_sync(int pwaves) {
+    if (pwaves > 1) __syncthreads();
+    else wave_sync_lds();
+}
+
 // One pass over all points at constants cs (LDS): sums[0] = sum r^2,
 // sums[1..K] = J^T r, sums[1+K..] = upper triangle of J^T J (row-major),
 // written to out (LDS) by lane 0. JAC: 0 value only, 1 forward, 2 reverse.
@@ -448,11 +458,15 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
                           double *out, int lane) {
     constexpr int W = (JAC == 0) ? 1 : sums_width(K);
     constexpr int KT = (K > 0) ? K : 1;
+    const int granules = (a.N + kLanes - 1) / kLanes;
+    const int last = a.N - 1;
+    for (int part = a.wave; part < a.parts; part += a.pwaves) {
     double acc[W];
 #pragma unroll
     for (int q = 0; q < W; ++q) acc[q] = 0.0;
-    const int batches = (a.N + kLanes * P - 1) / (kLanes * P);
-    const int last = a.N - 1;
+    // granules part, part + G, part + 2G, ... of this partition, P per batch
+    const int ng = (part < granules) ? (granules - part + a.parts - 1) / a.parts : 0;
+    const int batches = (ng + P - 1) / P;
     for (int bt = 0; bt < batches; ++bt) {
         // Every load of the batch is issued before the first one is used:
         // points past N read point N-1 (in bounds, never accumulated), so no
@@ -461,8 +475,9 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
         bool valid[P];
         int ic[P];
         CUSR_FOR_P {
-            const int i = lane + kLanes * (bt * P + p);
-            valid[p] = i < a.N;
+            const int gi = bt * P + p;
+            const int i = (part + a.parts * gi) * kLanes + lane;
+            valid[p] = gi < ng && i < a.N;
             ic[p] = valid[p] ? i : last;
         }
         CUSR_FOR_P yv[p] = a.y[ic[p]];
@@ -498,11 +513,27 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
         }
     }
     wave_allreduce<W>(acc);
+    double *dst = (a.parts == 1) ? out : a.part + part * W;
     if (lane == 0) {
 #pragma unroll
-        for (int q = 0; q < W; ++q) out[q] = acc[q];
+        for (int q = 0; q < W; ++q) dst[q] = acc[q];
     }
-    wave_sync_lds();
+    }
+    if (a.parts == 1) {
+        wave_sync_lds();
+        return;
+    }
+    // partition sums added in partition order by one lane
+    __syncthreads();
+    if (a.wave == 0 && lane == 0) {
+#pragma unroll
+        for (int q = 0; q < W; ++q) {
+            double v = a.part[q];
+            for (int g = 1; g < a.parts; ++g) v = v + a.part[g * W + q];
+            out[q] = v;
+        }
+    }
+    __syncthreads();
 }
 
 // ------------------------------------------------------------ the solve
@@ -577,6 +608,9 @@ struct FitArgs {
     int N, D, max_iter, guard;
     double lambda0, xtol;
     int slots, tape;        // per-wave LDS rows of this launch ([row][P][64] each)
+    int parts;              // point partitions per expression (1, 2 or 4)
+    int pwaves;             // wavefronts per workgroup (divides parts)
+    int wave_bytes;         // dynamic LDS of one wavefront; partition sums follow
 };
 
 // internal states, mapped to STATUS_* at the end (lm_core.cuh:46-56)
@@ -584,11 +618,13 @@ enum { ST_RUN = 0, ST_CONV = 1, ST_NAN = 2, ST_K0 = 3, ST_CHOL = 4 };
 
 template <int K, typename R, int AD>
 __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, double *lds_c, double *lds_s,
-                        char *lds_dyn, int lane) {
+                        char *lds_dyn, int lane, int wave) {
     constexpr int P = points_per_pass<R, K, AD>();
     constexpr int JAC = (K == 0) ? 0 : (AD == CO_AD_REVERSE ? 2 : 1);
+    char *my_lds = lds_dyn + (size_t)wave * fa.wave_bytes;
+    const bool lead = wave == 0;     // the wavefront that writes shared state
     WaveLds<R, P> wl;
-    wl.x = (R *)lds_dyn;
+    wl.x = (R *)my_lds;
     wl.slot = wl.x + (size_t)fa.D * P * kLanes;
     wl.tape = wl.slot + (size_t)fa.slots * P * kLanes;
     PassArgs pa;
@@ -598,11 +634,15 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     pa.y = fa.Y + (size_t)e.y_row * fa.N;
     pa.N = fa.N;
     pa.D = fa.D;
+    pa.parts = fa.parts;
+    pa.pwaves = fa.pwaves;
+    pa.wave = wave;
+    pa.part = (double *)(lds_dyn + (size_t)fa.pwaves * fa.wave_bytes);
 
     double *c_cur = lds_c, *c_try = lds_c + CO_MAX_K;
     double *s_cur = lds_s, *s_try = lds_s + sums_width(CO_MAX_K);
-    if (lane < K) c_cur[lane] = fa.C0[e.c_off + lane];
-    wave_sync_lds();
+    if (lead && lane < K) c_cur[lane] = fa.C0[e.c_off + lane];
+    block_sync(fa.pwaves);
 
     data_pass<K, R, P, JAC>(pa, wl, c_cur, s_cur, lane);
     double loss = uni(0.5 * s_cur[0]);
@@ -619,12 +659,15 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
                 if (lambda > 1e12) st = ST_CHOL;
                 continue;
             }
-            if (lane < K) {
+            // every wavefront is done reading c_try (the norm below) before
+            // the lead overwrites it
+            if (fa.pwaves > 1) __syncthreads();
+            if (lead && lane < K) {
 #pragma unroll
                 for (int j = 0; j < K; ++j)
                     if (j == lane) c_try[j] = c_cur[j] + delta[j];
             }
-            wave_sync_lds();
+            block_sync(fa.pwaves);
             data_pass<K, R, P, JAC>(pa, wl, c_try, s_try, lane);
             const double loss_try = uni(0.5 * s_try[0]);
             if (!isfinite(loss_try)) { st = ST_NAN; continue; }
@@ -655,13 +698,14 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
         // fp64 losses at the delivered point and at the start; the fp64
         // value pass reuses the same LDS at one point per lane
         WaveLds<double, 1> w64;
-        w64.x = (double *)lds_dyn;
+        w64.x = (double *)my_lds;
         w64.slot = w64.x + (size_t)fa.D * kLanes;
         w64.tape = w64.slot + (size_t)fa.slots * kLanes;
         data_pass<K, double, 1, 0>(pa, w64, c_cur, s_try, lane);
         lf = uni(0.5 * s_try[0]);
-        if (lane < K) c_try[lane] = fa.C0[e.c_off + lane];
-        wave_sync_lds();
+        if (fa.pwaves > 1) __syncthreads();
+        if (lead && lane < K) c_try[lane] = fa.C0[e.c_off + lane];
+        block_sync(fa.pwaves);
         data_pass<K, double, 1, 0>(pa, w64, c_try, s_try, lane);
         li = uni(0.5 * s_try[0]);
     }
@@ -671,6 +715,7 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
         if (st == ST_CONV) st = ST_RUN;
         lf = li;
     }
+    if (!lead) return;
     if (lane < K) fa.C[e.c_off + lane] = revert ? fa.C0[e.c_off + lane] : c_cur[lane];
     if (lane == 0) {
         // ST_RUN -> STATUS_MAXITER, ST_CONV -> STATUS_CONVERGED, the rest keep their code
@@ -697,12 +742,15 @@ constexpr int waves_per_eu() {
     return (sizeof(R) == 8 && AD == CO_AD_FORWARD) ? kW64[K] : CUSR_WAVES_OTHER;
 }
 template <int K, typename R, int AD>
-__global__ void __launch_bounds__(kLanes, (waves_per_eu<R, K, AD>())) lm_fit_kernel(FitArgs fa) {
+__global__ void __launch_bounds__(kLanes * CO_MAX_PARTITIONS, (waves_per_eu<R, K, AD>()))
+lm_fit_kernel(FitArgs fa) {
     __shared__ double lds_c[2 * CO_MAX_K];
     __shared__ double lds_s[2 * sums_width(CO_MAX_K)];
     extern __shared__ char lds_dyn[];
     const ExprDesc e = fa.desc[blockIdx.x];
-    fit_one<K, R, AD>(fa, e, lds_c, lds_s, lds_dyn, (int)threadIdx.x);
+    const int lane = (int)threadIdx.x & (kLanes - 1);
+    const int wave = uni((int)threadIdx.x >> 6);
+    fit_one<K, R, AD>(fa, e, lds_c, lds_s, lds_dyn, lane, wave);
 }
 
 // Dynamic LDS bytes one wavefront of a fit launch needs (the mixed-precision

@@ -83,7 +83,8 @@ class CoOptions(ctypes.Structure):
     _fields_ = [("struct_size", ctypes.c_int32), ("ad_mode", ctypes.c_int32),
                 ("precision", ctypes.c_int32), ("max_iter", ctypes.c_int32),
                 ("lambda0", ctypes.c_double), ("xtol", ctypes.c_double),
-                ("fp64_guard", ctypes.c_int32), ("reserved", ctypes.c_int32 * 7)]
+                ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
+                ("reserved", ctypes.c_int32 * 6)]
 
 
 assert ctypes.sizeof(PopHeader) == 64
@@ -263,14 +264,16 @@ class InProcessCO:
 
     def optimize_ex(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                     precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
-                    fp64_guard: bool = True, c_init=None, xs=None, ym=None) -> dict:
-        """fp64 fit; c_init/xs/ym override the pop's (fp32) arrays when given."""
+                    fp64_guard: bool = True, partitions: int = 0, c_init=None, xs=None,
+                    ym=None) -> dict:
+        """fp64 fit; c_init/xs/ym override the pop's (fp32) arrays when given.
+        partitions: point partitions per expression (0: by N)."""
         self._check()
         M, C = int(pop["M"]), int(pop["total_c"])
         h = _header(pop)
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
-                            fp64_guard=1 if fp64_guard else 0)
+                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions))
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
         ci, pci = _arr(pop["ci"], np.int32)
@@ -332,13 +335,13 @@ class InProcessCO:
 
     def fit_resident(self, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                      precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
-                     fp64_guard: bool = True, outputs: bool = True):
+                     fp64_guard: bool = True, outputs: bool = True, partitions: int = 0):
         """Fit the uploaded population again; outputs=False leaves results on the device."""
         self._check()
         M, C = self._resident
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
-                            fp64_guard=1 if fp64_guard else 0)
+                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions))
         if not outputs:
             rc = self._lib.co_fit_resident(self._handle, ctypes.byref(o), None, None, None, None, None)
             if rc != CO_OK:

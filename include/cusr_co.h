@@ -62,8 +62,22 @@ typedef struct CoOptions {
     double xtol;
     int32_t fp64_guard; /* 1: deliver c_init where the fp64 loss at c_final is
                            non-finite or worse (cusr/kernel/lm_core.cuh:299-351) */
-    int32_t reserved[7];
+    int32_t partitions; /* point partitions per expression (1, 2 or 4; 0: by N,
+                           co_partitions_for_n). Part of the arithmetic order:
+                           the sums of each partition are formed separately and
+                           added in partition order. */
+    int32_t reserved[6];
 } CoOptions;
+
+/* Point partitions of an expression with N points when CoOptions.partitions
+ * is 0: 64-point granule g belongs to partition g mod G, each partition is
+ * summed by its own wavefront, so long expressions use several wavefronts.
+ * A function of N only, so an expression fits the same alone or in any
+ * population. */
+static inline int co_partitions_for_n(int N) {
+    return N >= 16384 ? 4 : (N >= 8192 ? 2 : 1);
+}
+#define CO_MAX_PARTITIONS 4
 
 /* --- reference ABI (cusr/kernel/co_lib.h:45-71) ------------------------ */
 

@@ -445,17 +445,23 @@ typedef struct {
 } PassOut;
 
 /* Sums over points in the canonical lane order (see the file header). */
+/* One pass in the device's order (cusr_amd/csrc/lm_device.h data_pass):
+ * 64-point granule g belongs to partition g mod G; point i of a partition
+ * goes to lane i mod 64, which sums its points in ascending order from 0.0
+ * with fma; each partition combines its lanes with strides 32..1; the
+ * partitions are then added in order 0, 1, ..., G-1. */
 static void orc_pass(const Tree *t, int N, int D, const double *xs, const double *y,
-                     const double *c, int prec, int jac, PassOut *out) {
+                     const double *c, int prec, int jac, int G, PassOut *out) {
     int K = t->K;
     int nq = K * (K + 1) / 2;
     int width = 1 + K + nq;
-    double *acc = (double *)calloc((size_t)ORC_LANES * width, sizeof(double));
+    double *acc = (double *)calloc((size_t)G * ORC_LANES * width, sizeof(double));
     double g64[ORC_MAXK];
     float g32[ORC_MAXK];
     double x[64];
     for (int i = 0; i < N; i++) {
-        double *a = acc + (size_t)(i % ORC_LANES) * width;
+        int part = (i / ORC_LANES) % G;
+        double *a = acc + ((size_t)part * ORC_LANES + (size_t)(i % ORC_LANES)) * width;
         for (int k = 0; k < D; k++) x[k] = xs[(size_t)i * D + k];
         double f;
         if (prec == CO_PREC_FP64) {
@@ -474,13 +480,21 @@ static void orc_pass(const Tree *t, int N, int D, const double *xs, const double
                 for (int j2 = j1; j2 < K; j2++, q++) a[q] = fma(g64[j1], g64[j2], a[q]);
         }
     }
-    for (int s = ORC_LANES / 2; s >= 1; s >>= 1) {
-        /* every lane becomes p[l] + p[l^s]; lanes l and l^s hold the same value */
-        for (int l = 0; l < ORC_LANES; l++) {
-            if (l & s) continue;
-            double *pa = acc + (size_t)l * width, *pb = acc + (size_t)(l ^ s) * width;
-            for (int w = 0; w < width; w++) { double v = pa[w] + pb[w]; pa[w] = v; pb[w] = v; }
+    for (int part = 0; part < G; part++) {
+        double *pacc = acc + (size_t)part * ORC_LANES * width;
+        for (int s = ORC_LANES / 2; s >= 1; s >>= 1) {
+            /* every lane becomes p[l] + p[l^s]; lanes l and l^s hold the same value */
+            for (int l = 0; l < ORC_LANES; l++) {
+                if (l & s) continue;
+                double *pa = pacc + (size_t)l * width, *pb = pacc + (size_t)(l ^ s) * width;
+                for (int w = 0; w < width; w++) { double v = pa[w] + pb[w]; pa[w] = v; pb[w] = v; }
+            }
         }
+    }
+    /* partition sums (lane 0 of each) added in partition order */
+    for (int part = 1; part < G; part++) {
+        const double *pp = acc + (size_t)part * ORC_LANES * width;
+        for (int w = 0; w < width; w++) acc[w] = acc[w] + pp[w];
     }
     out->loss = 0.5 * acc[0];
     if (jac) {
@@ -490,6 +504,12 @@ static void orc_pass(const Tree *t, int N, int D, const double *xs, const double
             for (int j2 = j1; j2 < K; j2++, q++) out->jtj[j1 * K + j2] = acc[q];
     }
     free(acc);
+}
+
+/* Partitions of an N-point expression under options o. */
+static int orc_partitions(const CoOptions *o, int N) {
+    int G = o->partitions ? o->partitions : co_partitions_for_n(N);
+    return G;
 }
 
 /* ------------------------------------------------------------- the solve */
@@ -558,7 +578,8 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
     for (int k = 0; k < K; k++) c[k] = c0[k];
     int st = 0; /* 0 running, 1 conv, 2 nan, 3 K0, 4 chol */
     int it = 0;
-    orc_pass(t, N, D, xs, y, c, o->precision, K > 0 ? jac : 0, cur);
+    const int G = orc_partitions(o, N);
+    orc_pass(t, N, D, xs, y, c, o->precision, K > 0 ? jac : 0, G, cur);
     double li = cur->loss;
     if (K == 0) st = 3;
     else if (!isfinite(cur->loss)) st = 2;
@@ -571,7 +592,7 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
             continue;
         }
         for (int k = 0; k < K; k++) ct[k] = c[k] + delta[k];
-        orc_pass(t, N, D, xs, y, ct, o->precision, jac, tri);
+        orc_pass(t, N, D, xs, y, ct, o->precision, jac, G, tri);
         if (!isfinite(tri->loss)) { st = 2; continue; }
         double dn2 = 0.0, cn2 = 0.0;
         for (int k = 0; k < K; k++) {
@@ -596,9 +617,9 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
     if (o->precision != CO_PREC_FP64) {
         /* fp64 losses at the delivered point and at the start */
         PassOut *p = tri;
-        orc_pass(t, N, D, xs, y, c, CO_PREC_FP64, 0, p);
+        orc_pass(t, N, D, xs, y, c, CO_PREC_FP64, 0, G, p);
         lf = p->loss;
-        orc_pass(t, N, D, xs, y, c0, CO_PREC_FP64, 0, p);
+        orc_pass(t, N, D, xs, y, c0, CO_PREC_FP64, 0, G, p);
         li = p->loss;
     }
     if (o->fp64_guard && K > 0) {
@@ -699,8 +720,8 @@ int orc_solve_api(int K, const double *jtj_upper, const double *jtr, double lamb
  * expression at c (tests use it to pin the reduction order). */
 int orc_pass_api(const PopHeader *h, const int32_t *nt, const float *nv, const int32_t *ci,
                  const TreeMeta *metas, int m, const double *c, const double *xs,
-                 const double *y, int prec, int ad_mode, double *loss, double *jtj,
-                 double *jtr) {
+                 const double *y, int prec, int ad_mode, int partitions, double *loss,
+                 double *jtj, double *jtr) {
     int rc = orc_check_pop(h, nt, nv, ci, metas, NULL);
     if (rc) return rc;
     const TreeMeta *mt = &metas[m];
@@ -708,7 +729,8 @@ int orc_pass_api(const PopHeader *h, const int32_t *nt, const float *nv, const i
     Tree t = {nt + mt->node_offset, nv + mt->node_offset, ci + mt->node_offset,
               mt->n_nodes, mt->K};
     PassOut *p = (PassOut *)malloc(sizeof(PassOut));
-    orc_pass(&t, h->N, h->n_vars, xs, y, c, prec, mt->K > 0 ? (ad_mode ? 2 : 1) : 0, p);
+    const int G = partitions ? partitions : co_partitions_for_n(h->N);
+    orc_pass(&t, h->N, h->n_vars, xs, y, c, prec, mt->K > 0 ? (ad_mode ? 2 : 1) : 0, G, p);
     *loss = p->loss;
     for (int j = 0; j < mt->K; j++) {
         jtr[j] = p->jtr[j];

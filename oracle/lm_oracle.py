@@ -29,7 +29,8 @@ class CoOptions(ctypes.Structure):
     _fields_ = [("struct_size", ctypes.c_int32), ("ad_mode", ctypes.c_int32),
                 ("precision", ctypes.c_int32), ("max_iter", ctypes.c_int32),
                 ("lambda0", ctypes.c_double), ("xtol", ctypes.c_double),
-                ("fp64_guard", ctypes.c_int32), ("reserved", ctypes.c_int32 * 7)]
+                ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
+                ("reserved", ctypes.c_int32 * 6)]
 
 
 def build() -> None:
@@ -69,11 +70,12 @@ def _prog(pop):
 
 
 def options(ad_mode=CO_AD_FORWARD, precision=CO_PREC_FP64, max_iter=50,
-            lambda0=1e-3, xtol=1e-6, fp64_guard=1) -> CoOptions:
+            lambda0=1e-3, xtol=1e-6, fp64_guard=1, partitions=0) -> CoOptions:
     o = CoOptions()
     o.struct_size = ctypes.sizeof(CoOptions)
     o.ad_mode, o.precision, o.max_iter = ad_mode, precision, max_iter
     o.lambda0, o.xtol, o.fp64_guard = lambda0, xtol, fp64_guard
+    o.partitions = partitions
     return o
 
 
@@ -149,7 +151,8 @@ def solve(jtj, jtr, lam):
     return None if rc != 0 else d
 
 
-def pass_sums(pop, m, c, xs=None, y=None, precision=CO_PREC_FP64, ad_mode=CO_AD_FORWARD):
+def pass_sums(pop, m, c, xs=None, y=None, precision=CO_PREC_FP64, ad_mode=CO_AD_FORWARD,
+              partitions=0):
     """(loss, JtJ, Jtr) of expression m at constants c (canonical order)."""
     keep, ptrs = _prog(pop)
     K = int(pop["metas"][m][3])
@@ -161,7 +164,8 @@ def pass_sums(pop, m, c, xs=None, y=None, precision=CO_PREC_FP64, ad_mode=CO_AD_
     jtr = np.zeros(max(K, 1))
     h = _header(pop)
     rc = lib().orc_pass_api(ctypes.byref(h), *ptrs, ctypes.c_int(m), pcc, px, pyy,
-                            ctypes.c_int(precision), ctypes.c_int(ad_mode), ctypes.byref(loss),
+                            ctypes.c_int(precision), ctypes.c_int(ad_mode),
+                            ctypes.c_int(partitions), ctypes.byref(loss),
                             jtj.ctypes.data_as(ctypes.c_void_p), jtr.ctypes.data_as(ctypes.c_void_p))
     if rc != 0:
         raise RuntimeError(f"orc_pass_api returned {rc}")

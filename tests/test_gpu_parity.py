@@ -16,11 +16,13 @@ def _say(msg):
     print(msg, flush=True)
 
 
-def _fit_both(co, pop, max_iter, ad_mode=0, precision=0):
+def _fit_both(co, pop, max_iter, ad_mode=0, precision=0, partitions=0):
     c0, xs, ym = f64(pop)
-    _say(f"case M={pop['M']} N={pop['N']} ad={ad_mode} prec={precision} max_iter={max_iter}")
-    g = co.optimize_ex(pop, max_iter, ad_mode=ad_mode, precision=precision)
-    o = lm_oracle.fit(pop, max_iter=max_iter, ad_mode=ad_mode, precision=precision)
+    _say(f"case M={pop['M']} N={pop['N']} ad={ad_mode} prec={precision} max_iter={max_iter} "
+         f"partitions={partitions}")
+    g = co.optimize_ex(pop, max_iter, ad_mode=ad_mode, precision=precision, partitions=partitions)
+    o = lm_oracle.fit(pop, max_iter=max_iter, ad_mode=ad_mode, precision=precision,
+                      partitions=partitions)
     return g, o
 
 
@@ -130,3 +132,29 @@ def test_operators_bit_exact(co, precision):
     bad = [(ops[m], int(np.sum(~same[m]))) for m in range(len(ops)) if not same[m].all()]
     _say(f"mismatching ops (id, count): {bad}")
     assert not bad
+
+
+@pytest.mark.parametrize("parts,ad_mode,precision", [(2, 0, 0), (4, 0, 0), (4, 1, 0), (2, 0, 1)])
+def test_point_partitions_match_oracle(co, parts, ad_mode, precision):
+    """Several wavefronts per expression: granule g of 64 points goes to
+    partition g mod G, partition sums are added in order (N = 1000: the last
+    granule is ragged and partitions hold different granule counts)."""
+    pop, _ = synth("C2", 96, 1000)
+    g, o = _fit_both(co, pop, 15, ad_mode=ad_mode, precision=precision, partitions=parts)
+    st, d = _report(g, o)
+    _say(f"partitions {parts}: status agree {st:.4f}; loss rel max {d.max():.3e}; "
+         f"exact {np.mean(d == 0):.4f}")
+    tol = 1e-9 if precision == 0 else 1e-4
+    assert np.mean(d <= tol) >= 0.99
+    assert st >= 0.98
+
+
+def test_large_n_auto_partitions(co):
+    """C4-shaped expressions (D = 5, N = 20,000 -> 4 partitions by N)."""
+    pop, _ = synth("C4", 24, 20000)
+    assert pop["N"] >= 16384
+    g, o = _fit_both(co, pop, 8)
+    st, d = _report(g, o)
+    _say(f"large N: status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
+    assert np.mean(d <= 1e-9) >= 0.95
+    assert st >= 0.95

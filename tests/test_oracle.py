@@ -427,3 +427,24 @@ def test_reference_interpreters_agree_with_oracle():
                                   <= 1e-3 * np.maximum(1.0, np.abs(Jo[m, i, :K][fin]))))
             agree += ok
     assert total > 500 and agree / total > 0.99
+
+
+def test_partitioned_sums_agree():
+    """Partition order changes only the rounding of the sums: 1, 2 and 4
+    partitions agree to 1e-12, and are identical when N fits one granule."""
+    pop, _ = synth("C2", 16, 1000)
+    for m in range(pop["M"]):
+        K = int(pop["metas"][m][3])
+        c = pop["c_init"][pop["metas"][m][2]:pop["metas"][m][2] + K].astype(np.float64)
+        base = lm_oracle.pass_sums(pop, m, c, partitions=1)
+        for G in (2, 4):
+            got = lm_oracle.pass_sums(pop, m, c, partitions=G)
+            assert got[0] == pytest.approx(base[0], rel=1e-12)
+            assert np.allclose(got[1], base[1], rtol=1e-11, atol=1e-12 * np.abs(base[1]).max())
+    small, _ = synth("C1", 4, 64)
+    for m in range(small["M"]):
+        K = int(small["metas"][m][3])
+        c = small["c_init"][small["metas"][m][2]:small["metas"][m][2] + K].astype(np.float64)
+        a = lm_oracle.pass_sums(small, m, c, partitions=1)
+        b = lm_oracle.pass_sums(small, m, c, partitions=4)
+        assert a[0] == b[0] and np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2])
