@@ -1,24 +1,30 @@
-"""Benchmark of the batched LM fitter on the headline configuration.
+"""Benchmark of the batched LM fitter.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--cpu-sample S]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-cpu]
+                    [--rounds R] [--copy-calibration]
 
-One step = one full LM fit (all iterations, on-device accept/reject) of the
-synthetic C2 population: 16,384 seeded expressions, depth <= 6, <= 31 nodes,
-K uniform 1..8, D = 3, N = 1,024, 50 iterations, forward AD, fp64. The
-population is uploaded before timing (inputs resident in HBM); each timed step
-re-fits it from the same starting constants. Prints one JSON line.
+Default (the headline metric): one step = one full LM fit (all iterations,
+on-device accept/reject) of the synthetic C2 population: 16,384 seeded
+expressions, depth <= 6, <= 31 nodes, K uniform 1..8, D = 3, N = 1,024,
+50 iterations, forward AD, fp64. The population is uploaded before timing
+(inputs resident in HBM); each timed step re-fits it from the same starting
+constants. Prints one JSON line. --config C1/C3/C4 measure the other resident
+configurations the same way; --config C5 runs the GP inner-solver shape: R
+rounds of fresh 65,536-expression populations (generated untimed), each timed
+end to end from host buffers (upload, 10 mixed-precision iterations,
+read-back), the per-round latency being the step.
 
 roofline: the dominant launch is the fit kernel of the K bin that runs
 longest; its algorithmic HBM bytes (cusr_amd/benchmark/accounting.py: per LM
 iteration of each active expression two point-passes that each read y, X once
 per pass, the bytecode) over its duration from HIP events recorded around
-that launch on the stream it runs on. The same object carries the fp64 VALU
-figure (algorithmic flops over the same duration), the roof this kernel is
-actually under. traffic: measured HBM bytes of that launch, from the
-rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under profiles/, when it
-was taken on this workload. cpu_baseline: the reference CPU path (scipy LM per
-expression over a process pool) on the same population, repeated to 10-30 s,
-on this host's cores.
+that launch on the stream it runs on. The same object carries the VALU figure
+(algorithmic flops over the same duration), the roof this kernel is actually
+under. traffic: measured HBM bytes of that launch, from the rocprofv3
+FETCH_SIZE / WRITE_SIZE summary committed under profiles/, when it was taken
+on this workload. cpu_baseline: the reference CPU path (scipy LM per
+expression over a process pool) on a sample of the same population sized to
+10-30 s, on this host's cores.
 """
 from __future__ import annotations
 
@@ -36,12 +42,19 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
 FP64_VECTOR_PEAK_TFLOPS = 78.6
+FP32_VECTOR_PEAK_TFLOPS = 157.3
+HEADLINE_METRIC = "expressions fitted/sec (16k exprs, K=1-8, N=1024, fp64) + achieved HBM GB/s"
 
 
-def cpu_baseline(pop, sample, min_seconds=10.0, max_seconds=30.0):
+def _say(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(pop, target_s=15.0, min_s=10.0, max_s=30.0):
     """scipy LM (the reference CPU path, restated in oracle/scipy_pop.py) on
-    the first `sample` expressions, repeated until at least `min_seconds` of
-    wall time (never starting a repeat that would pass `max_seconds`)."""
+    the first expressions of the population: a warm-up slice measures the
+    rate, the sample is sized to about target_s, and repeated until min_s of
+    wall time (never starting a repeat that would pass max_s)."""
     from cusr_amd.benchmark import popio
     from oracle.scipy_pop import ScipyPop
 
@@ -50,7 +63,11 @@ def cpu_baseline(pop, sample, min_seconds=10.0, max_seconds=30.0):
     try:
         warm = popio.slice_pop(pop, min(2 * nproc, pop["M"]))
         sp.fit_pop(warm)                       # pool start-up + imports
-        sub = popio.slice_pop(pop, min(sample, pop["M"]))
+        t0 = time.perf_counter()
+        r = sp.fit_pop(warm)
+        rate = max(r["n_fit"], 1) / max(time.perf_counter() - t0, 1e-3)
+        n = int(min(pop["M"], max(nproc, rate * target_s)))
+        sub = popio.slice_pop(pop, n)
         fits, wall, reps = 0, 0.0, 0
         while True:
             t0 = time.perf_counter()
@@ -59,15 +76,14 @@ def cpu_baseline(pop, sample, min_seconds=10.0, max_seconds=30.0):
             fits += r["n_fit"]
             wall += dt
             reps += 1
-            if wall >= min_seconds or wall + dt > max_seconds:
+            if wall >= min_s or wall + dt > max_s:
                 break
     finally:
         sp.close()
     return {"value": fits / wall, "unit": "fits/s", "cores": nproc, "kind": "port",
-            "sample": (f"first {sub['M']} expressions of the same C2 population "
+            "sample": (f"first {sub['M']} expressions of the same population "
                        f"({r['n_fit']} with K>0) x {reps}, scipy least_squares lm "
-                       f"xtol=ftol=1e-10 max_nfev=200, {wall:.1f} s wall on {nproc} processes"),
-            "wall_s": wall}
+                       f"xtol=ftol=1e-10 max_nfev=200, {wall:.1f} s wall on {nproc} processes")}
 
 
 def copy_calibration(co, pop):
@@ -77,8 +93,8 @@ def copy_calibration(co, pop):
     4*M*N and writes 8*M*N bytes (widen_kernel, the largest of its launches)."""
     n = int(pop["M"]) * int(pop["N"])
     co.optimize(pop, 0)
-    print(f"[bench] copy calibration: widen_kernel over {n} values, {4 * n} bytes read, "
-          f"{8 * n} bytes written", file=sys.stderr, flush=True)
+    _say(f"copy calibration: widen_kernel over {n} values, {4 * n} bytes read, "
+         f"{8 * n} bytes written")
 
 
 def load_traffic(workload_key, kernel):
@@ -97,39 +113,41 @@ def load_traffic(workload_key, kernel):
     return None
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="C2")
-    ap.add_argument("--cpu-sample", type=int, default=16384)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run one copy kernel of known size (for rocprofv3 --pmc scaling)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build measures "
-              "one GPU's share and does not launch multi-GPU runs.", file=sys.stderr)
-        sys.exit(2)
+def workload_text(cfg, pop):
+    return (f"{cfg.name}: {pop['M']} expressions, depth<={cfg.depth}, <={cfg.max_nodes} nodes, "
+            f"K {cfg.k_lo}-{cfg.k_hi}, D={cfg.D}, N={cfg.N}, {cfg.max_iter} LM iterations, "
+            f"{'reverse' if cfg.ad_mode else 'forward'} AD, "
+            f"{'mixed fp32/fp64' if cfg.precision else 'fp64'}")
 
-    from cusr_amd.benchmark import accounting, gen_synth
-    from cusr_amd.kernel import co_inproc
 
-    cfg = gen_synth.CONFIGS[args.config]
-    co = co_inproc.get_inproc_co(0, "ad")
+def roofline(pop, cfg, iters, bins, kname_of):
+    """Dominant launch (longest K bin) against HBM, with its VALU figure."""
+    from cusr_amd.benchmark import accounting
 
-    def gpu_eval(p, c, xs):
-        return co.evaluate(p, c, xs)
+    K = pop["metas"][:, 3]
+    kdom = int(np.argmax(bins))
+    w = accounting.algorithmic_work(pop, iters, cfg.ad_mode, subset=(K == kdom))
+    dom_s = bins[kdom] / 1e3
+    achieved = w["bytes"] / dom_s / 1e9
+    vpeak = FP64_VECTOR_PEAK_TFLOPS if cfg.precision == 0 else FP32_VECTOR_PEAK_TFLOPS
+    tflops = w["flops"] / dom_s / 1e12
+    kname = kname_of(kdom)
+    key = f"{cfg.name}:{pop['M']}x{pop['N']}:seed{cfg.seed}:it{cfg.max_iter}"
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(key, kname),
+            "kernel": kname, "expressions_in_launch": int(np.sum(K == kdom)),
+            "launch_ms": float(bins[kdom]), "algorithmic_bytes_per_launch": w["bytes"],
+            "valu": {"achieved": tflops, "peak": vpeak, "unit": "TFLOP/s",
+                     "frac": tflops / vpeak, "algorithmic_flops_per_launch": w["flops"]}}
 
-    t_gen = time.perf_counter()
-    pop, _ = gen_synth.generate(cfg, gpu_eval)
-    t_gen = time.perf_counter() - t_gen
-    print(f"[bench] generated {cfg.name}: M={pop['M']} N={pop['N']} nodes={pop['total_nodes']} "
-          f"K_max={pop['K_max']} in {t_gen:.1f}s", file=sys.stderr, flush=True)
+
+def run_resident(args, cfg, co, pop):
+    """C1-C4: fit the HBM-resident population `steps` times."""
+    from cusr_amd.benchmark import accounting
+
+    fit_kw = dict(ad_mode=cfg.ad_mode, precision=cfg.precision)
     if args.copy_calibration:
         copy_calibration(co, pop)
-    fit_kw = dict(ad_mode=cfg.ad_mode, precision=cfg.precision)
     co.upload(pop)
     for _ in range(args.warmup):
         co.fit_resident(cfg.max_iter, outputs=False, **fit_kw)
@@ -142,7 +160,7 @@ def main():
     wall = time.perf_counter() - t0
     ms_per_step = 1e3 * wall / args.steps
     res = co.fit_resident(cfg.max_iter, **fit_kw)
-    # end-to-end from host buffers (upload over PCIe + fit + read-back), untimed above
+    # end to end from host buffers (upload over PCIe + fit + read-back), untimed above
     t_e2e = time.perf_counter()
     co.optimize_ex(pop, cfg.max_iter, **fit_kw)
     e2e_ms = 1e3 * (time.perf_counter() - t_e2e)
@@ -151,66 +169,112 @@ def main():
     value = n_fit / (ms_per_step / 1e3)
     kms = float(np.mean(fit_ms))
     bins = np.mean(np.asarray(bin_ms), axis=0)
-    kdom = int(np.argmax(bins))                       # dominant launch: longest K bin
-    wdom = accounting.algorithmic_work(pop, res["iters"], cfg.ad_mode, subset=(K == kdom))
-    wall_fit = accounting.algorithmic_work(pop, res["iters"], cfg.ad_mode)
-    dom_s = bins[kdom] / 1e3
-    achieved = wdom["bytes"] / dom_s / 1e9
     rname = "double" if cfg.precision == 0 else "float"
-    kname = f"lm_fit_kernel<{kdom}, {rname}, {cfg.ad_mode}>"
+    roof = roofline(pop, cfg, res["iters"], bins,
+                    lambda k: f"lm_fit_kernel<{k}, {rname}, {cfg.ad_mode}>")
+    whole = accounting.algorithmic_work(pop, res["iters"], cfg.ad_mode)
     status_counts = np.bincount(res["status"], minlength=5).tolist()
-    print(f"[bench] {args.steps} steps: {ms_per_step:.2f} ms/step, device {kms:.2f} ms/fit, "
-          f"{value:.0f} fits/s, statuses {status_counts}, mean iters {res['iters'].mean():.1f}",
-          file=sys.stderr, flush=True)
-    print("[bench] per-bin kernel ms: " + " ".join(f"K{k}={v:.2f}" for k, v in enumerate(bins)
-                                                  if v >= 0), file=sys.stderr, flush=True)
-    workload_key = f"{cfg.name}:{pop['M']}x{pop['N']}:seed{cfg.seed}:it{cfg.max_iter}"
-    traffic = load_traffic(workload_key, kname)
+    _say(f"{args.steps} steps: {ms_per_step:.2f} ms/step, device {kms:.2f} ms/fit, "
+         f"{value:.0f} fits/s, statuses {status_counts}, mean iters {res['iters'].mean():.1f}")
+    _say("per-bin kernel ms: " + " ".join(f"K{k}={v:.2f}" for k, v in enumerate(bins) if v >= 0))
+    fit = {"status_counts": status_counts, "mean_iters": float(res["iters"].mean()),
+           "device_ms_per_fit": kms, "fits_per_s_device": n_fit / (kms / 1e3),
+           "hbm_gbs_whole_fit": whole["bytes"] / (kms / 1e3) / 1e9,
+           "tflops_whole_fit": whole["flops"] / (kms / 1e3) / 1e12,
+           "e2e_ms_from_host": e2e_ms, "fits_per_s_from_host": n_fit / (e2e_ms / 1e3),
+           "bin_ms": {str(k): float(v) for k, v in enumerate(bins) if v >= 0}}
+    return value, ms_per_step, roof, fit
+
+
+def run_rounds(args, cfg, co, gen):
+    """C5: fresh populations per round, each timed from host buffers."""
+    lat, fits, rounds, last = [], 0, [], None
+    for r in range(args.rounds):
+        pop = gen(r)
+        if r == 0:
+            co.optimize_ex(pop, 0, precision=cfg.precision)     # first-use costs, untimed
+        t0 = time.perf_counter()
+        res = co.optimize_ex(pop, cfg.max_iter, ad_mode=cfg.ad_mode, precision=cfg.precision)
+        dt = 1e3 * (time.perf_counter() - t0)
+        n_fit = int(np.count_nonzero(pop["metas"][:, 3] > 0))
+        lat.append(dt)
+        fits += n_fit
+        rounds.append({"round": r, "ms": dt, "device_ms": co.last_kernel_ms(), "fits": n_fit,
+                       "status_counts": np.bincount(res["status"], minlength=5).tolist()})
+        _say(f"round {r}: {dt:.1f} ms end to end, device {co.last_kernel_ms():.1f} ms, "
+             f"{n_fit} fits")
+        last = (pop, res, co.last_bin_ms())
+    value = fits / (sum(lat) / 1e3)
+    pop, res, bins = last
+    roof = roofline(pop, cfg, res["iters"], bins, lambda k: f"lm_fit_kernel<{k}, float, 0>")
+    fit = {"rounds": rounds, "mean_round_ms": float(np.mean(lat)),
+           "p50_round_ms": float(np.median(lat))}
+    return value, float(np.mean(lat)), roof, fit, pop
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--rounds", type=int, default=3, help="C5 rounds (the spec runs 20)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one copy kernel of known size (for rocprofv3 --pmc scaling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build measures "
+              "one GPU's share and does not launch multi-GPU runs.", file=sys.stderr)
+        sys.exit(2)
+
+    from cusr_amd.benchmark import gen_synth
+    from cusr_amd.kernel import co_inproc
+
+    cfg = gen_synth.CONFIGS[args.config]
+    co = co_inproc.get_inproc_co(0, "ad")
+
+    def gen(round_index=0):
+        t = time.perf_counter()
+        pop, _ = gen_synth.generate(cfg, lambda p, c, xs: co.evaluate(p, c, xs),
+                                    round_index=round_index)
+        _say(f"generated {cfg.name} round {round_index}: M={pop['M']} N={pop['N']} "
+             f"nodes={pop['total_nodes']} K_max={pop['K_max']} in {time.perf_counter() - t:.1f}s")
+        return pop
+
+    if cfg.rounds > 1:
+        value, ms_per_step, roof, fit, pop = run_rounds(args, cfg, co, gen)
+        steps, warmup = args.rounds, 1
+    else:
+        pop = gen()
+        value, ms_per_step, roof, fit = run_resident(args, cfg, co, pop)
+        steps, warmup = args.steps, args.warmup
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(pop, args.cpu_sample)
-        print(f"[bench] cpu baseline {cpu['value']:.1f} fits/s on {cpu['cores']} cores",
-              file=sys.stderr, flush=True)
-        cpu.pop("wall_s", None)
+        cpu = cpu_baseline(pop)
+        _say(f"cpu baseline {cpu['value']:.1f} fits/s on {cpu['cores']} cores")
 
+    metric = HEADLINE_METRIC if cfg.name == "C2" else \
+        f"expressions fitted/sec ({cfg.name}) + achieved HBM GB/s"
     line = {
-        "metric": "expressions fitted/sec (16k exprs, K=1-8, N=1024, fp64) + achieved HBM GB/s",
+        "metric": metric,
         "value": value,
         "unit": "fits/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f64" if cfg.precision == 0 else "f32+f64",
-        "data": "synthetic: seeded C2 population, targets from the true constants + noise",
-        "config": {"workload": (f"{cfg.name}: {pop['M']} expressions, depth<={cfg.depth}, "
-                                f"<={cfg.max_nodes} nodes, K {cfg.k_lo}-{cfg.k_hi}, D={cfg.D}, "
-                                f"N={cfg.N}, {cfg.max_iter} LM iterations, "
-                                f"{'reverse' if cfg.ad_mode else 'forward'} AD, "
-                                f"{'mixed' if cfg.precision else 'fp64'}"),
-                   "expressions": int(pop["M"]), "points": int(pop["N"]),
-                   "max_iter": cfg.max_iter, "seed": cfg.seed},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic,
-                     "kernel": kname, "expressions_in_launch": int(np.sum(K == kdom)),
-                     "launch_ms": float(bins[kdom]),
-                     "algorithmic_bytes_per_launch": wdom["bytes"],
-                     "valu": {"achieved": wdom["flops"] / dom_s / 1e12,
-                              "peak": FP64_VECTOR_PEAK_TFLOPS, "unit": "TFLOP/s",
-                              "frac": wdom["flops"] / dom_s / 1e12 / FP64_VECTOR_PEAK_TFLOPS,
-                              "algorithmic_flops_per_launch": wdom["flops"]}},
+        "data": f"synthetic: seeded {cfg.name} population, targets from true constants + noise",
+        "config": {"workload": workload_text(cfg, pop), "expressions": int(pop["M"]),
+                   "points": int(pop["N"]), "max_iter": cfg.max_iter, "seed": cfg.seed},
+        "roofline": roof,
         "cpu_baseline": cpu,
-        "fit": {"status_counts": status_counts, "mean_iters": float(res["iters"].mean()),
-                "device_ms_per_fit": kms, "fits_per_s_device": n_fit / (kms / 1e3),
-                "hbm_gbs_whole_fit": wall_fit["bytes"] / (kms / 1e3) / 1e9,
-                "e2e_ms_from_host": e2e_ms, "fits_per_s_from_host": n_fit / (e2e_ms / 1e3),
-                "fp64_tflops_whole_fit": wall_fit["flops"] / (kms / 1e3) / 1e12,
-                "bin_ms": {str(k): float(v) for k, v in enumerate(bins) if v >= 0}},
+        "fit": fit,
     }
     print(json.dumps(line), flush=True)
 

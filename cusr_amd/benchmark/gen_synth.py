@@ -162,14 +162,14 @@ def generate(cfg: SynthConfig, evaluator, round_index: int = 0, max_rounds: int 
     for _ in range(max_rounds):
         for m in todo:
             slots[m], truth[m], noises[m] = _draw_slot(rng, cfg, N)
-        cand = popio.build_pop([slots[m] for m in todo], xs, np.zeros((len(todo), N)))
-        c64 = np.concatenate([truth[m] for m in todo]) if cand["total_c"] else np.zeros(0)
-        y = evaluator(cand, c64, xs64)
         if cfg.shared_target:
             bad = np.zeros(len(todo), bool)   # any expression is a valid GP candidate
             for j, m in enumerate(todo):
                 noises[m] = None
         else:
+            cand = popio.build_pop([slots[m] for m in todo], xs, np.zeros((len(todo), N)))
+            c64 = np.concatenate([truth[m] for m in todo]) if cand["total_c"] else np.zeros(0)
+            y = evaluator(cand, c64, xs64)
             bad = ~np.all(np.isfinite(y) & (np.abs(y) <= 1e6), axis=1)
             for j, m in enumerate(todo):
                 if not bad[j]:
