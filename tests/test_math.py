@@ -1,0 +1,113 @@
+"""include/cusr_math.h against the C library (numpy's libm), no GPU.
+
+The device and the CPU oracle both compile these functions, so device/oracle
+agreement is by construction (tests/test_gpu_parity.py checks it on the GPU);
+what this file pins is their accuracy: the largest error in units of the last
+place against libm over wide argument ranges, and the special values.
+"""
+import numpy as np
+import pytest
+
+from oracle import lm_oracle
+
+# (name, arguments, max ulp fp64, max ulp fp32)
+RNG = np.random.default_rng(2024)
+
+
+def _logu(lo, hi, n):
+    return np.exp(RNG.uniform(np.log(lo), np.log(hi), n))
+
+
+def _sym(a):
+    return np.concatenate([a, -a])
+
+
+CASES = {
+    "exp": (np.concatenate([RNG.uniform(-700, 700, 20000), RNG.uniform(-1, 1, 5000)]), 1, 2),
+    "log": (np.concatenate([_logu(1e-300, 1e300, 20000), RNG.uniform(0.5, 2, 5000)]), 1, 2),
+    "sin": (_sym(np.concatenate([_logu(1e-8, 1e5, 20000), RNG.uniform(0, 10, 5000)])), 1, 2),
+    "cos": (_sym(np.concatenate([_logu(1e-8, 1e5, 20000), RNG.uniform(0, 10, 5000)])), 1, 2),
+    "tan": (_sym(np.concatenate([_logu(1e-8, 1e4, 20000), RNG.uniform(0, 1.5, 5000)])), 3, 3),
+    "sinh": (_sym(np.concatenate([_logu(1e-8, 700, 20000), RNG.uniform(0, 2, 5000)])), 2, 3),
+    "cosh": (_sym(_logu(1e-8, 700, 20000)), 2, 3),
+    "tanh": (_sym(np.concatenate([_logu(1e-8, 20, 20000), RNG.uniform(0, 2, 5000)])), 4, 3),
+}
+
+
+def _ulps(got, want, dtype):
+    got = got.astype(dtype).astype(np.float64)
+    want_t = want.astype(dtype)
+    sp = np.spacing(np.abs(want_t)).astype(np.float64)
+    fin = np.isfinite(want_t) & (want_t != 0)
+    return np.abs(got[fin] - want_t[fin].astype(np.float64)) / sp[fin]
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_fp64_accuracy(name):
+    x, ulp64, _ = CASES[name]
+    got = lm_oracle.math_fn(name, x)
+    want = getattr(np, name)(x)
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isfinite(got), fin), name
+    e = _ulps(got, want, np.float64)
+    assert e.max() <= ulp64, (name, e.max())
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_fp32_accuracy(name):
+    x, _, ulp32 = CASES[name]
+    x = x[np.abs(x) < (88.0 if name in ("exp", "sinh", "cosh") else 3e38)]
+    x32 = x.astype(np.float32)
+    if name == "log":
+        x32 = x32[x32 > 0]
+    if name in ("sin", "cos", "tan"):
+        x32 = x32[np.abs(x32) < 2.0 ** 21]
+    got = lm_oracle.math_fn(name, x32.astype(np.float64), fp32=True)
+    want = getattr(np, name)(x32.astype(np.float64))      # the exact fp32 argument, in fp64
+    e = _ulps(got, want, np.float32)
+    assert e.max() <= ulp32, (name, e.max())
+
+
+def test_pow_accuracy():
+    a = _logu(1e-3, 1e3, 20000)
+    b = RNG.uniform(-20, 20, 20000)
+    got = lm_oracle.math_fn("pow", a, b)
+    want = np.power(a, b)
+    # exp(y log x) without an extra-precision log: the error of log x is
+    # amplified by |y log x| (documented in include/cusr_math.h)
+    amp = np.abs(b * np.log(a))
+    fin = np.isfinite(want) & (want != 0)
+    e = np.abs(got[fin] - want[fin]) / np.spacing(np.abs(want[fin]))
+    assert np.all(e <= 1.6 * (1.0 + amp[fin])), (e / (1.0 + amp[fin])).max()
+    small = fin & (amp < 1.0)
+    assert (np.abs(got[small] - want[small]) / np.spacing(np.abs(want[small]))).max() <= 6
+    # negative base with integral exponent keeps the sign; fractional gives NaN
+    neg = lm_oracle.math_fn("pow", np.array([-2.0, -2.0, -8.0]), np.array([3.0, 2.0, 0.5]))
+    assert neg[0] == -8.0 and neg[1] == 4.0 and np.isnan(neg[2])
+
+
+def test_special_values():
+    nan, inf = np.nan, np.inf
+    f = lm_oracle.math_fn
+    assert np.isnan(f("exp", np.array([nan])))[0]
+    assert f("exp", np.array([inf]))[0] == inf and f("exp", np.array([-inf]))[0] == 0.0
+    assert f("exp", np.array([710.0]))[0] == inf and f("exp", np.array([-746.0]))[0] == 0.0
+    assert f("log", np.array([0.0]))[0] == -inf and np.isnan(f("log", np.array([-1.0])))[0]
+    assert f("log", np.array([inf]))[0] == inf and f("log", np.array([1.0]))[0] == 0.0
+    assert f("log", np.array([5e-324]))[0] == pytest.approx(np.log(5e-324), rel=1e-15)
+    for name in ("sin", "cos", "tan"):
+        assert np.all(np.isnan(f(name, np.array([nan, inf, -inf]))))
+    # |x| >= 2^50: no significant digits of the reduced argument; sin 0, cos 1
+    assert f("sin", np.array([2.0 ** 51]))[0] == 0.0 and f("cos", np.array([2.0 ** 51]))[0] == 1.0
+    assert f("sin", np.array([0.0]))[0] == 0.0 and f("cos", np.array([0.0]))[0] == 1.0
+    assert f("tanh", np.array([inf]))[0] == 1.0 and f("tanh", np.array([-inf]))[0] == -1.0
+
+
+def test_exact_small_cases():
+    """Values every correct implementation must give exactly."""
+    f = lm_oracle.math_fn
+    assert f("exp", np.array([0.0]))[0] == 1.0
+    assert f("exp", np.array([1.0]))[0] == np.exp(1.0)
+    assert f("log", np.array([2.0]))[0] == np.log(2.0)
+    assert f("pow", np.array([2.0]), np.array([10.0]))[0] == 1024.0
+    assert f("sinh", np.array([0.0]))[0] == 0.0 and f("cosh", np.array([0.0]))[0] == 1.0
