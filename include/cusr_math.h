@@ -26,7 +26,7 @@
  *   tan   sin/cos of the same reduction.
  *   sinh, cosh, tanh  Taylor series for |x| < 1 (sinh), exp otherwise.
  *   pow   exp(y log|x|) with the sign of x for integral y; no extra-precision
- *         log, so the error is about 1.5 (1 + |y ln x|) ulp.
+ *         log, so the error stays below 2 (1 + |y ln x|) ulp.
  * Accuracy against the C library is checked by tests/test_math.py.
  */
 #ifndef CUSR_MATH_H

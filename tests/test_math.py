@@ -78,7 +78,7 @@ def test_pow_accuracy():
     amp = np.abs(b * np.log(a))
     fin = np.isfinite(want) & (want != 0)
     e = np.abs(got[fin] - want[fin]) / np.spacing(np.abs(want[fin]))
-    assert np.all(e <= 1.6 * (1.0 + amp[fin])), (e / (1.0 + amp[fin])).max()
+    assert np.all(e <= 2.0 * (1.0 + amp[fin])), (e / (1.0 + amp[fin])).max()
     small = fin & (amp < 1.0)
     assert (np.abs(got[small] - want[small]) / np.spacing(np.abs(want[small]))).max() <= 6
     # negative base with integral exponent keeps the sign; fractional gives NaN
