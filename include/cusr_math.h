@@ -25,8 +25,10 @@
  *         information in the format and the functions return sin = 0, cos = 1.
  *   tan   sin/cos of the same reduction.
  *   sinh, cosh, tanh  Taylor series for |x| < 1 (sinh), exp otherwise.
- *   pow   exp(y log|x|) with the sign of x for integral y; no extra-precision
- *         log, so the error stays below 2 (1 + |y ln x|) ulp.
+ *   pow   integral |y| <= 64: binary powering (x^2, x^3 exact when
+ *         representable); otherwise exp(y log|x|) with no extra-precision
+ *         log, so the error stays below 2 (1 + |y ln x|) ulp. The sign of x
+ *         is kept for odd integral y.
  * Accuracy against the C library is checked by tests/test_math.py.
  */
 #ifndef CUSR_MATH_H
@@ -465,6 +467,18 @@ CM_FN double cm_pow(double x, double y) {
     if (ax == CM_INF) return (y < 0.0) ? sign * 0.0 : sign * CM_INF;
     if (y == CM_INF) return (ax < 1.0) ? 0.0 : CM_INF;
     if (y == -CM_INF) return (ax < 1.0) ? CM_INF : 0.0;
+    if (kind != 0 && cm_fabs(y) <= 64.0) {
+        /* small integral exponent: binary powering, exact when the result is
+         * representable in a few products (x^2, x^3, ...) */
+        int n = (int)cm_fabs(y);
+        double b = ax, r = 1.0;
+        while (n) {
+            if (n & 1) r = r * b;
+            b = b * b;
+            n >>= 1;
+        }
+        return sign * ((y < 0.0) ? 1.0 / r : r);
+    }
     return sign * cm_exp(y * cm_log(ax));
 }
 
@@ -492,6 +506,16 @@ CM_FN float cm_powf(float x, float y) {
     if (ax == CM_INFF) return (y < 0.0f) ? sign * 0.0f : sign * CM_INFF;
     if (y == CM_INFF) return (ax < 1.0f) ? 0.0f : CM_INFF;
     if (y == -CM_INFF) return (ax < 1.0f) ? CM_INFF : 0.0f;
+    if (kind != 0 && cm_fabsf(y) <= 64.0f) {
+        int n = (int)cm_fabsf(y);
+        float b = ax, r = 1.0f;
+        while (n) {
+            if (n & 1) r = r * b;
+            b = b * b;
+            n >>= 1;
+        }
+        return sign * ((y < 0.0f) ? 1.0f / r : r);
+    }
     return sign * cm_expf(y * cm_logf(ax));
 }
 

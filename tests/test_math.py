@@ -110,4 +110,8 @@ def test_exact_small_cases():
     assert f("exp", np.array([1.0]))[0] == np.exp(1.0)
     assert f("log", np.array([2.0]))[0] == np.log(2.0)
     assert f("pow", np.array([2.0]), np.array([10.0]))[0] == 1024.0
+    assert f("pow", np.array([3.0]), np.array([-2.0]))[0] == 1.0 / 9.0
+    assert f("pow", np.array([1.5]), np.array([2.0]))[0] == 2.25
+    x = RNG.uniform(-3, 3, 1000)
+    assert np.array_equal(f("pow", x, np.full(1000, 2.0)), x * x)
     assert f("sinh", np.array([0.0]))[0] == 0.0 and f("cosh", np.array([0.0]))[0] == 1.0
