@@ -4,8 +4,10 @@
 
 Outputs (next to the ctypes loader, like the reference's make targets,
 cusr/kernel/Makefile:77-81):
-    cusr_amd/kernel/libcusr_co_ad.so   C ABI of include/cusr_co.h
-    cusr_amd/kernel/batch_lm_ad        CLI with the reference's arguments/blobs
+    cusr_amd/kernel/libcusr_co_ad.so   C ABI of include/cusr_co.h, AD variant LM ordering
+    cusr_amd/kernel/libcusr_co_fd.so   same kernels, the FD variant's LM ordering by default
+    cusr_amd/kernel/batch_lm_ad        CLI with the reference's arguments/blobs (AD ordering)
+    cusr_amd/kernel/batch_lm           the same CLI over libcusr_co_fd.so
 Objects go to cusr_amd/_build/. Every call recompiles.
 """
 from __future__ import annotations
@@ -23,7 +25,9 @@ CSRC = ROOT / "csrc"
 BUILD = ROOT / "_build"
 KDIR = ROOT / "kernel"
 LIB = KDIR / "libcusr_co_ad.so"
+LIB_FD = KDIR / "libcusr_co_fd.so"
 CLI = KDIR / "batch_lm_ad"
+CLI_FD = KDIR / "batch_lm"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -65,18 +69,28 @@ def build(jobs: int | None = None, verbose: bool = False, defines=(), out: Path 
                      "-o", str(BUILD / "co_lib.o")])
     compiles.append([HIPCC, *DEVICE_FLAGS, "-x", "hip", "-c", str(CSRC / "program.cpp"),
                      "-o", str(BUILD / "program.o")])
+    default = out is None
+    if default:
+        compiles.append([HIPCC, *DEVICE_FLAGS, *extra, "-x", "hip", "-DCUSR_DEFAULT_ORDER=1", "-c",
+                         str(CSRC / "co_lib.hip"), "-o", str(BUILD / "co_lib_fd.o")])
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         for err in ex.map(_run, compiles):
             if verbose and err.strip():
                 print(err, file=sys.stderr)
     objs = [str(c[c.index("-o") + 1]) for c in compiles]
-    tmp = lib.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs])
-    os.replace(tmp, lib)
-    if cli and out is None:
-        _run(["g++", "-O2", "-std=c++17", f"-I{REPO / 'include'}", "-o", str(CLI),
-              str(CSRC / "batch_lm_main.cpp"), f"-L{KDIR}", "-lcusr_co_ad",
-              "-Wl,-rpath,$ORIGIN"])
+    fit_objs = [o for o in objs if "co_lib" not in Path(o).name]
+    links = [(lib, fit_objs + [str(BUILD / "co_lib.o")])]
+    if default:
+        links.append((LIB_FD, fit_objs + [str(BUILD / "co_lib_fd.o")]))
+    for target, lobjs in links:
+        tmp = target.with_suffix(".so.tmp")
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *lobjs])
+        os.replace(tmp, target)
+    if cli and default:
+        for exe, name in ((CLI, "cusr_co_ad"), (CLI_FD, "cusr_co_fd")):
+            _run(["g++", "-O2", "-std=c++17", f"-I{REPO / 'include'}", "-o", str(exe),
+                  str(CSRC / "batch_lm_main.cpp"), f"-L{KDIR}", f"-l{name}",
+                  "-Wl,-rpath,$ORIGIN"])
     return lib
 
 

@@ -41,6 +41,13 @@ __global__ void widen_kernel(const float *src, double *dst, size_t n) {
 
 using namespace cusr;
 
+// LM ordering of co_optimize and of co_options_default: the library named
+// libcusr_co_fd.so is built with the FD variant's ordering, libcusr_co_ad.so
+// with the AD variant's (the reference's two variants, co_lib.cu:3-7).
+#ifndef CUSR_DEFAULT_ORDER
+#define CUSR_DEFAULT_ORDER CO_ORDER_IMPROVE_FIRST
+#endif
+
 namespace {
 
 double now_ms() {
@@ -228,6 +235,8 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
     if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
     if (opt.max_iter < 0) return CO_ERR_NULLARG;
+    if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
+        return CO_ERR_NULLARG;
     CO_HIP(hipSetDevice(ctx->device));
     const Plan &plan = ctx->plan;
     const int M = plan.M, C = plan.total_c;
@@ -253,6 +262,7 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     fa.D = plan.D;
     fa.max_iter = opt.max_iter;
     fa.guard = opt.fp64_guard ? 1 : 0;
+    fa.lm_order = opt.lm_order;
     fa.lambda0 = opt.lambda0;
     fa.xtol = opt.xtol;
     const bool rev = opt.ad_mode == CO_AD_REVERSE;
@@ -333,6 +343,8 @@ int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t
     if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
     if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
     if (opt.max_iter < 0) return CO_ERR_NULLARG;
+    if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
+        return CO_ERR_NULLARG;
     int rc = upload_population(ctx, h, nt, nv, ci, metas, c, xs, ym, in32);
     if (rc != CO_OK) return rc;
     const double t1 = now_ms();
@@ -354,6 +366,7 @@ extern "C" void co_options_default(CoOptions *o) {
     o->lambda0 = 1e-3;
     o->xtol = 1e-6;
     o->fp64_guard = 1;
+    o->lm_order = CUSR_DEFAULT_ORDER;
 }
 
 extern "C" int co_init(int device_id, void **handle_out) {

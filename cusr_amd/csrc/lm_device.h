@@ -605,7 +605,7 @@ struct FitArgs {
     double *loss_init;      // [M] out
     double *loss_final;     // [M] out
     int32_t *iters;         // [M] out
-    int N, D, max_iter, guard;
+    int N, D, max_iter, guard, lm_order;
     double lambda0, xtol;
     int slots, tape;        // per-wave LDS rows of this launch ([row][P][64] each)
     int parts;              // point partitions per expression (1, 2 or 4)
@@ -678,15 +678,28 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
                 cn2 = fma(c_try[j], c_try[j], cn2);
             }
             const double dn = ::sqrt(dn2), cn = ::sqrt(cn2);
-            if (loss_try <= loss) {
+            const bool small = dn < fa.xtol * (cn + fa.xtol);
+            bool accept, conv;
+            if (fa.lm_order == CO_ORDER_CONVERGE_FIRST) {
+                // FD variant (co_lib.cu:457-473): a small step converges
+                // whatever the loss; otherwise only a strict decrease
+                conv = small;
+                accept = small || loss_try < loss;
+            } else {
+                // AD variant (batch_lm_ad.cu:456-473): improvement first
+                accept = loss_try <= loss;
+                conv = accept && small;
+            }
+            if (accept) {
                 double *t = c_cur; c_cur = c_try; c_try = t;
                 t = s_cur; s_cur = s_try; s_try = t;
                 loss = loss_try;
-                if (dn < fa.xtol * (cn + fa.xtol)) st = ST_CONV;
-                else {
-                    lambda = lambda * 0.1;
-                    if (lambda < 1e-12) lambda = 1e-12;
-                }
+            }
+            if (conv) {
+                st = ST_CONV;
+            } else if (accept) {
+                lambda = lambda * 0.1;
+                if (lambda < 1e-12) lambda = 1e-12;
             } else {
                 lambda = lambda * 10.0;
                 if (lambda > 1e12) st = ST_NAN;

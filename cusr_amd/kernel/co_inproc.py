@@ -42,6 +42,9 @@ CO_MAX_NODES = 255
 
 CO_AD_FORWARD, CO_AD_REVERSE = 0, 1
 CO_PREC_FP64, CO_PREC_MIXED = 0, 1
+CO_ORDER_IMPROVE_FIRST, CO_ORDER_CONVERGE_FIRST = 0, 1
+# external statuses (include/pop_format.h, cusr/kernel/lm_core.cuh:46-56)
+STATUS_CONVERGED, STATUS_MAXITER, STATUS_FAIL_NAN, STATUS_K0_SKIP, STATUS_FAIL_CHOLESKY = 0, 1, 2, 3, 4
 
 _ERR_MSG = {
     CO_ERR_BOUNDS: (f"beyond device bounds (K<={CO_MAX_K}, max_stack<={CO_MAX_STACK}, "
@@ -84,7 +87,7 @@ class CoOptions(ctypes.Structure):
                 ("precision", ctypes.c_int32), ("max_iter", ctypes.c_int32),
                 ("lambda0", ctypes.c_double), ("xtol", ctypes.c_double),
                 ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
-                ("reserved", ctypes.c_int32 * 6)]
+                ("lm_order", ctypes.c_int32), ("reserved", ctypes.c_int32 * 5)]
 
 
 assert ctypes.sizeof(PopHeader) == 64
@@ -216,6 +219,9 @@ class InProcessCO:
         self.variant = variant
         self.device_id = int(device_id)
         self._lib = load_library(variant, lib_path)
+        o = CoOptions()
+        self._lib.co_options_default(ctypes.byref(o))
+        self.default_order = int(o.lm_order)   # the library's LM ordering (ad / fd)
         self._handle = _VP()
         self._torn = False
         self._resident = (0, 0)
@@ -264,16 +270,19 @@ class InProcessCO:
 
     def optimize_ex(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                     precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
-                    fp64_guard: bool = True, partitions: int = 0, c_init=None, xs=None,
-                    ym=None) -> dict:
+                    fp64_guard: bool = True, partitions: int = 0, lm_order: int | None = None,
+                    c_init=None, xs=None, ym=None) -> dict:
         """fp64 fit; c_init/xs/ym override the pop's (fp32) arrays when given.
-        partitions: point partitions per expression (0: by N)."""
+        partitions: point partitions per expression (0: by N). lm_order: None
+        keeps the library's default (CO_ORDER_IMPROVE_FIRST for the ad
+        library, CO_ORDER_CONVERGE_FIRST for fd)."""
         self._check()
         M, C = int(pop["M"]), int(pop["total_c"])
         h = _header(pop)
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
                             fp64_guard=1 if fp64_guard else 0, partitions=int(partitions))
+        o.lm_order = self.default_order if lm_order is None else int(lm_order)
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
         ci, pci = _arr(pop["ci"], np.int32)
@@ -335,13 +344,15 @@ class InProcessCO:
 
     def fit_resident(self, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                      precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
-                     fp64_guard: bool = True, outputs: bool = True, partitions: int = 0):
+                     fp64_guard: bool = True, outputs: bool = True, partitions: int = 0,
+                     lm_order: int | None = None):
         """Fit the uploaded population again; outputs=False leaves results on the device."""
         self._check()
         M, C = self._resident
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
                             fp64_guard=1 if fp64_guard else 0, partitions=int(partitions))
+        o.lm_order = self.default_order if lm_order is None else int(lm_order)
         if not outputs:
             rc = self._lib.co_fit_resident(self._handle, ctypes.byref(o), None, None, None, None, None)
             if rc != CO_OK:
@@ -414,7 +425,7 @@ def _teardown_all() -> None:
     _SINGLETONS.clear()
 
 
-def get_inproc_co(device_id: int = 0, variant: str = "ad") -> InProcessCO:
+def get_inproc_co(device_id: int = 0, variant: str = "fd") -> InProcessCO:
     """Process-wide InProcessCO per (device, variant) (co_inproc.py:271-295)."""
     global _ATEXIT
     key = (int(device_id), str(variant))

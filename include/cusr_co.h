@@ -66,8 +66,16 @@ typedef struct CoOptions {
                            co_partitions_for_n). Part of the arithmetic order:
                            the sums of each partition are formed separately and
                            added in partition order. */
-    int32_t reserved[6];
+    int32_t lm_order;   /* CO_ORDER_IMPROVE_FIRST (the AD variant,
+                           cusr/kernel/batch_lm_ad.cu:456-473) or
+                           CO_ORDER_CONVERGE_FIRST (the FD variant: a small step
+                           converges, otherwise a strict decrease is accepted,
+                           cusr/kernel/co_lib.cu:457-473) */
+    int32_t reserved[5];
 } CoOptions;
+
+#define CO_ORDER_IMPROVE_FIRST 0
+#define CO_ORDER_CONVERGE_FIRST 1
 
 /* Point partitions of an expression with N points when CoOptions.partitions
  * is 0: 64-point granule g belongs to partition g mod G, each partition is

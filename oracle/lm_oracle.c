@@ -600,14 +600,27 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
             cn2 = fma(ct[k], ct[k], cn2);
         }
         double dn = sqrt(dn2), cn = sqrt(cn2);
-        if (tri->loss <= cur->loss) {
+        const int small = dn < o->xtol * (cn + o->xtol);
+        int accept, conv;
+        if (o->lm_order == CO_ORDER_CONVERGE_FIRST) {
+            /* FD variant (co_lib.cu:457-473): a small step converges whatever
+             * the loss; otherwise only a strict decrease is accepted */
+            conv = small;
+            accept = small || tri->loss < cur->loss;
+        } else {
+            /* AD variant (batch_lm_ad.cu:456-473): improvement first */
+            accept = tri->loss <= cur->loss;
+            conv = accept && small;
+        }
+        if (accept) {
             for (int k = 0; k < K; k++) c[k] = ct[k];
             PassOut *sw = cur; cur = tri; tri = sw;
-            if (dn < o->xtol * (cn + o->xtol)) st = 1;
-            else {
-                lambda = lambda * 0.1;
-                if (lambda < 1e-12) lambda = 1e-12;
-            }
+        }
+        if (conv) {
+            st = 1;
+        } else if (accept) {
+            lambda = lambda * 0.1;
+            if (lambda < 1e-12) lambda = 1e-12;
         } else {
             lambda = lambda * 10.0;
             if (lambda > 1e12) st = 2;

@@ -171,11 +171,16 @@ def test_bounds_k17():
     assert _code(pop) == ci.CO_ERR_BOUNDS
 
 
-def test_library_exports_every_header_symbol():
+@pytest.mark.parametrize("variant,order", [("ad", 0), ("fd", 1)])
+def test_library_exports_every_header_symbol(variant, order):
+    import ctypes
     import re
     hdr = (GOLDEN.parents[1] / "include" / "cusr_co.h").read_text()
     names = set(re.findall(r"^\s*(?:int|void)\s+(co_\w+)\s*\(", hdr, re.M))
     assert names == set(ci.EXPORTED)
-    lib = ci.load_library()
+    lib = ci.load_library(variant)
     for n in names:
         assert hasattr(lib, n), n
+    o = ci.CoOptions()
+    lib.co_options_default(ctypes.byref(o))          # host-only, no device needed
+    assert o.struct_size == ctypes.sizeof(ci.CoOptions) and o.lm_order == order

@@ -1,0 +1,128 @@
+"""The drop-in boundary on the GPU: the reference fp32 ABI (co_optimize), the
+CLI and its blobs, handle reuse across shrinking/growing populations, edge
+populations, and the FD variant's LM ordering -- each against the CPU oracle.
+
+Reference behaviour followed: cusr/kernel/co_lib.h:45-71 (ABI, ownership),
+cusr/kernel/tests/test_inproc_reuse.py:313,425-469 (reuse, status branches),
+cusr/kernel/batch_lm_ad.cu:226-536 (CLI arguments, blobs, completion line).
+"""
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from cusr_amd.benchmark import popio
+from cusr_amd.kernel import co_inproc as ci
+from oracle import lm_oracle
+from tests.helpers import rel_diff, synth
+
+pytestmark = pytest.mark.gpu
+KDIR = Path(ci.__file__).resolve().parent
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def test_reference_abi_fp32_outputs(co):
+    """co_optimize: fp32 in/out; the fit runs in fp64, results rounded to fp32."""
+    pop, _ = synth("C1", 128, 256)
+    _say("co_optimize fp32 C1 M=128 N=256")
+    g = co.optimize(pop, 20)
+    o = lm_oracle.fit(pop, max_iter=20)
+    assert g["c_final"].dtype == np.float32 and g["loss_final"].dtype == np.float32
+    same = np.mean(g["c_final"] == o["c_final"].astype(np.float32))
+    _say(f"fp32 constants equal to the rounded oracle: {same:.4f}")
+    assert same >= 0.99
+    assert np.mean(g["status"] == o["status"]) >= 0.99
+    assert np.allclose(g["loss_final"], o["loss_final"].astype(np.float32), rtol=1e-6)
+
+
+def test_handle_reuse_shrink_and_grow(co):
+    """Buffers grow by capacity and never shrink; every call starts from its
+    own c_init (test_inproc_reuse.py:313)."""
+    big, _ = synth("C2", 256, 512)
+    small, _ = synth("C1", 32, 128)
+    highk, _ = synth("C3", 16, 256)
+    runs = []
+    for pop, kw in ((big, {}), (small, {}), (highk, {"ad_mode": 1}), (big, {}), (small, {})):
+        _say(f"reuse M={pop['M']} N={pop['N']} {kw}")
+        runs.append(co.optimize_ex(pop, 10, **kw))
+    for a, b in ((runs[0], runs[3]), (runs[1], runs[4])):
+        assert np.array_equal(a["c_final"], b["c_final"])
+        assert np.array_equal(a["status"], b["status"])
+    o = lm_oracle.fit(highk, max_iter=10, ad_mode=1)
+    assert np.mean(rel_diff(runs[2]["loss_final"], o["loss_final"]) <= 1e-9) >= 0.99
+
+
+def test_edge_populations(co):
+    """All-K0 population (K0_SKIP, no iterations) and one-point data."""
+    trees = [([3, 0, 0], [1.0, 0.0, 1.0], [-1, -1, -1], np.zeros(0, np.float32))] * 5
+    xs = np.linspace(-1, 1, 70).reshape(35, 2)
+    pop = popio.build_pop(trees, xs, np.ones((5, 35)))
+    _say("K=0 population")
+    r = co.optimize_ex(pop, 10)
+    assert np.all(r["status"] == ci.STATUS_K0_SKIP) and np.all(r["iters"] == 0)
+    o = lm_oracle.fit(pop, max_iter=10)
+    assert np.array_equal(r["loss_init"], o["loss_init"])
+    one, _ = synth("C1", 8, 1)
+    _say("N=1 population")
+    g = co.optimize_ex(one, 5)
+    o = lm_oracle.fit(one, max_iter=5)
+    assert np.array_equal(g["status"], o["status"])
+    assert np.mean(rel_diff(g["loss_final"], o["loss_final"]) <= 1e-9) == 1.0
+
+
+def test_errors_before_any_copy(co):
+    pop, _ = synth("C1", 8, 16)
+    bad = dict(pop)
+    bad["total_c"] = int(pop["total_c"]) + 1
+    with pytest.raises(ci.COError) as e:
+        co.optimize_ex(bad, 5)
+    assert e.value.code == ci.CO_ERR_SUM_C
+    # the handle still works afterwards
+    r = co.optimize_ex(pop, 5)
+    assert r["status"].shape == (8,)
+
+
+def test_fd_ordering_matches_oracle():
+    """libcusr_co_fd.so: the FD variant's ordering by default (co_lib.cu:457-473)."""
+    fd = ci.get_inproc_co(0, "fd")
+    assert fd.default_order == ci.CO_ORDER_CONVERGE_FIRST
+    pop, _ = synth("C2", 128, 512)
+    _say("fd ordering C2 M=128 N=512")
+    g = fd.optimize_ex(pop, 20, xtol=1e-4)
+    o = lm_oracle.fit(pop, max_iter=20, xtol=1e-4, lm_order=1)
+    d = rel_diff(g["loss_final"], o["loss_final"])
+    _say(f"fd: status agree {np.mean(g['status'] == o['status']):.4f} loss exact {np.mean(d == 0):.4f}")
+    assert np.mean(d <= 1e-9) >= 0.99
+    assert np.mean(g["status"] == o["status"]) >= 0.99
+
+
+@pytest.mark.parametrize("exe,order", [("batch_lm_ad", 0), ("batch_lm", 1)])
+def test_cli_blobs_and_completion_line(tmp_path, exe, order):
+    """CLI arguments, output blobs and the completion line the benchmark
+    parses (cusr/benchmark/backends.py:745,773-774)."""
+    pop, _ = synth("C1", 64, 128)
+    path = tmp_path / "pop.bin"
+    popio.save_pop_bin(pop, path)
+    _say(f"cli {exe}")
+    r = subprocess.run([str(KDIR / exe), str(path), str(tmp_path), "--max-iter", "15"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert re.search(r"总耗时 ([\d.]+) 秒", r.stdout)
+    status = np.fromfile(tmp_path / "status.bin", np.int32)
+    c_final = np.fromfile(tmp_path / "c_final.bin", np.float32)
+    lf = np.fromfile(tmp_path / "loss_final.bin", np.float32)
+    li = np.fromfile(tmp_path / "loss_init.bin", np.float32)
+    assert status.shape == (64,) and c_final.shape == (int(pop["total_c"]),)
+    assert lf.shape == li.shape == (64,)
+    o = lm_oracle.fit(pop, max_iter=15, lm_order=order)
+    assert np.mean(status == o["status"]) >= 0.99
+    assert np.mean(c_final == o["c_final"].astype(np.float32)) >= 0.99
+    # load failure exits 1
+    bad = subprocess.run([str(KDIR / exe), str(tmp_path / "missing.bin")], capture_output=True,
+                         timeout=60)
+    assert bad.returncode == 1

@@ -448,3 +448,26 @@ def test_partitioned_sums_agree():
         a = lm_oracle.pass_sums(small, m, c, partitions=1)
         b = lm_oracle.pass_sums(small, m, c, partitions=4)
         assert a[0] == b[0] and np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2])
+
+
+def test_lm_orders_differ_as_the_reference_variants():
+    """With a huge xtol every first step is 'small'. The FD ordering
+    (co_lib.cu:457-473) then converges after one iteration whatever the loss;
+    the AD ordering (batch_lm_ad.cu:456-473) converges only where the step
+    did not raise the loss."""
+    pop, _ = synth("C1", 64, 128)
+    K = pop["metas"][:, 3]
+    fd = lm_oracle.fit(pop, max_iter=5, xtol=1e3, lm_order=1, fp64_guard=0)
+    ad = lm_oracle.fit(pop, max_iter=5, xtol=1e3, lm_order=0, fp64_guard=0)
+    live = (K > 0) & np.isfinite(fd["loss_init"])
+    # a singular J^T J fails every solve (lambda grows, no step is taken)
+    live &= ~((fd["status"] == 1) & (fd["iters"] == 5) & (fd["loss_final"] == fd["loss_init"]))
+    assert live.sum() > 50
+    assert np.all(fd["status"][live] == 0) and np.all(fd["iters"][live] == 1)
+    went_up = live & (fd["loss_final"] > fd["loss_init"])
+    assert np.all(ad["status"][live & ~went_up] == 0)
+    assert np.all(ad["iters"][went_up] > 1) or not went_up.any()
+    # with the guard, an FD step that raised the loss is taken back
+    fdg = lm_oracle.fit(pop, max_iter=5, xtol=1e3, lm_order=1, fp64_guard=1)
+    assert np.all(fdg["loss_final"][live] <= fdg["loss_init"][live])
+    assert np.all(fdg["status"][went_up] == 1)
