@@ -1,0 +1,130 @@
+"""Constant-optimisation backend for a GP inner loop, with the reference
+demonstrator's contract (cusr/demonstrator/co_backend.py:25-47, 250-285;
+cusr/demonstrator/kernel_bridge.py:140-238):
+
+    fit_batch(skeletons, inits, X, y, *, max_iter, native) -> [COResult]
+
+Every candidate shares one problem's (X, y). `native[j]` is candidate j's
+expression in prefix form, (nt, nv, ci) arrays of pop.bin node types, values
+and constant ranks (the reference extracts the same arrays from its EvoGP
+trees; that extraction belongs to the GP system, not to this library).
+`skeletons[j]` is only consulted for `n_constants` when it has one.
+
+Candidates the device cannot take (more than 16 constants, a value stack
+deeper than 16, more than 255 nodes, more than 8 variables) go to the
+`fallback` backend when one is given; without one they raise, since this
+library has no CPU path of its own. Results stay aligned with the input
+order; final_loss is mean(r^2) = 2 * loss / N in fp64; converged is
+status == CONVERGED (kernel_bridge.py:216).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from cusr_amd.benchmark import popio
+
+
+@dataclass
+class COResult:
+    constants: np.ndarray   # fitted constants, shape (n_consts,)
+    n_iter: int
+    converged: bool
+    final_loss: float       # mean(residual ** 2)
+
+
+def _eligible(nt, n_vars):
+    from cusr_amd.kernel import co_inproc as ci
+
+    nt = np.asarray(nt)
+    K = int(np.sum(nt == popio.NODE_CONST))
+    return (len(nt) <= ci.CO_MAX_NODES and K <= ci.CO_MAX_K and n_vars <= ci.CO_MAX_VARS
+            and popio.stack_depth(nt) <= ci.CO_MAX_STACK and not np.any(nt > popio.NODE_BFUNC))
+
+
+def fit_natives(skeletons, inits, natives, X, y, *, max_iter: int = 50, fallback=None,
+                variant: str = "ad", device_id: int = 0, ad_mode: int = 0,
+                precision: int = 0):
+    """(results aligned with skeletons, stats) -- kernel_bridge.py:140-238."""
+    from cusr_amd.kernel import co_inproc
+
+    X = np.asarray(X, dtype=np.float64)
+    y = np.asarray(y, dtype=np.float64).ravel()
+    n_vars = X.shape[1]
+    M = len(natives)
+    results = [None] * M
+    take, fb, n_overflow, n_kmismatch = [], [], 0, 0
+    for j, nat in enumerate(natives):
+        nt, nv, ci = (np.asarray(a) for a in nat)
+        K = int(np.sum(nt == popio.NODE_CONST))
+        skel = skeletons[j] if skeletons is not None else None
+        if skel is not None and hasattr(skel, "n_constants") and skel.n_constants != K:
+            n_kmismatch += 1
+            fb.append(j)
+        elif not _eligible(nt, n_vars):
+            n_overflow += 1
+            fb.append(j)
+        else:
+            take.append(j)
+    if fb and fallback is None:
+        raise ValueError(f"{len(fb)} candidates are beyond the device limits and no fallback "
+                         "backend was given")
+    if take:
+        trees = []
+        for j in take:
+            nt, nv, ci = (np.asarray(a) for a in natives[j])
+            c0 = np.asarray(inits[j], np.float64)
+            trees.append((nt, nv, ci, c0))
+        pop = popio.build_pop(trees, X.astype(np.float32), np.tile(y, (len(take), 1)))
+        c0_64 = np.concatenate([np.asarray(inits[j], np.float64) for j in take]) \
+            if pop["total_c"] else np.zeros(0)
+        co = co_inproc.get_inproc_co(device_id, variant)
+        r = co.optimize_ex(pop, max_iter, ad_mode=ad_mode, precision=precision,
+                           c_init=c0_64, xs=X, ym=np.tile(y, (len(take), 1)))
+        N = len(y)
+        for slot, j in enumerate(take):
+            _, _, c_off, K = (int(v) for v in pop["metas"][slot])
+            loss = float(r["loss_final"][slot])
+            results[j] = COResult(np.asarray(r["c_final"][c_off:c_off + K], np.float64),
+                                  int(r["iters"][slot]),
+                                  bool(int(r["status"][slot]) == co_inproc.STATUS_CONVERGED),
+                                  2.0 * loss / N if np.isfinite(loss) else float("inf"))
+    if fb:
+        fb_res = fallback.fit_batch([skeletons[j] for j in fb] if skeletons is not None else None,
+                                    [inits[j] for j in fb], X, y, max_iter=max_iter,
+                                    native=[natives[j] for j in fb])
+        for j, res in zip(fb, fb_res):
+            results[j] = res
+    stats = dict(n_total=M, n_kernel=len(take), n_fallback=len(fb), n_overflow=n_overflow,
+                 n_kmismatch=n_kmismatch)
+    return results, stats
+
+
+class KernelLM:
+    """The fitter behind the demonstrator's ConstantOptimizer protocol."""
+
+    name = "cuda_kernel_lm"
+
+    def __init__(self, max_iter: int = 50, fallback=None, variant: str = "ad", device_id: int = 0,
+                 ad_mode: int = 0, precision: int = 0):
+        self.max_iter = int(max_iter)
+        self.fallback = fallback
+        self.variant = variant
+        self.device_id = int(device_id)
+        self.ad_mode = int(ad_mode)
+        self.precision = int(precision)
+        self.last_stats: dict = {}
+        self.cum_stats: dict = {}
+
+    def fit_batch(self, skeletons, inits, X, y, *, max_iter=100, native=None) -> list[COResult]:
+        if native is None:
+            raise ValueError("KernelLM needs the prefix arrays of every candidate via native=")
+        results, stats = fit_natives(skeletons, inits, native, X, y, max_iter=self.max_iter,
+                                     fallback=self.fallback, variant=self.variant,
+                                     device_id=self.device_id, ad_mode=self.ad_mode,
+                                     precision=self.precision)
+        self.last_stats = stats
+        for k, v in stats.items():
+            self.cum_stats[k] = self.cum_stats.get(k, 0) + v
+        return results

@@ -1,0 +1,85 @@
+"""Benchmark and demonstrator backends (reference contracts:
+cusr/benchmark/backends.py:80-89,740-785; cusr/demonstrator/co_backend.py:25-47;
+cusr/demonstrator/kernel_bridge.py:140-238)."""
+import numpy as np
+import pytest
+
+from cusr_amd.benchmark import backends, popio
+from cusr_amd.demonstrator import co_backend
+from oracle import interp, lm_oracle
+from tests.helpers import synth
+
+
+def _candidates(n, seed=3):
+    """Prefix arrays of simple candidates over X with 2 variables."""
+    rng = np.random.default_rng(seed)
+    forms = [([3, 3, 1, 0, 1], [1, 3, 0, 0, 0], [-1, -1, 0, -1, 1]),          # c0*x0 + c1
+             ([2, 3, 1, 0], [14, 3, 0, 1], [-1, -1, 0, -1]),                   # sin(c0*x1)
+             ([3, 3, 1, 2, 0, 1], [1, 3, 0, 34, 1, 0], [-1, -1, 0, -1, -1, 1])]  # c0*sq(x1)+c1
+    nat, inits = [], []
+    for j in range(n):
+        nt, nv, ci = forms[j % len(forms)]
+        K = int(np.sum(np.asarray(nt) == 1))
+        nat.append((np.asarray(nt, np.int32), np.asarray(nv, np.float32), np.asarray(ci, np.int32)))
+        inits.append(rng.normal(size=K))
+    return nat, inits
+
+
+def test_ineligible_without_fallback_raises():
+    nat, inits = _candidates(3)
+    nt = np.asarray([3] * 17 + [1] * 18, np.int32)                  # 18 constants
+    nat.append((nt, np.asarray([1.0] * 17 + [0.0] * 18, np.float32),
+                np.asarray([-1] * 17 + list(range(18)), np.int32)))
+    inits.append(np.zeros(18))
+    X = np.zeros((8, 2))
+    with pytest.raises(ValueError):
+        co_backend.fit_natives(None, inits, nat, X, np.zeros(8))
+
+
+def test_status_map_matches_reference():
+    assert backends.STATUS_MAP == {0: 0, 1: 1, 2: 2, 3: 3, 4: 2}
+
+
+@pytest.mark.gpu
+def test_kernel_pop_and_cli_pop():
+    pop, _ = synth("C1", 96, 128)
+    a = backends.KernelPop(max_iter=20).fit_pop(pop)
+    b = backends.CudaKernelPop(max_iter=20).fit_pop(pop)
+    o = lm_oracle.fit(pop, max_iter=20)
+    assert a.c_final.dtype == np.float64 and a.status.dtype == np.int32
+    assert np.array_equal(a.c_final, o["c_final"])
+    assert np.array_equal(a.n_iter, o["iters"])
+    assert np.array_equal(a.status, backends._map_status(o["status"]))
+    assert np.array_equal(b.status, a.status)
+    assert np.array_equal(b.c_final, a.c_final.astype(np.float32).astype(np.float64))
+    assert np.isfinite(b.wall_core) and b.wall_core >= 0 and np.all(b.n_iter == -1)
+
+
+@pytest.mark.gpu
+def test_kernel_lm_fit_batch_aligned_with_fallback():
+    nat, inits = _candidates(12)
+    rng = np.random.default_rng(9)
+    X = rng.uniform(-2, 2, size=(300, 2))
+    y = 1.5 * X[:, 0] - 0.25 + 0.01 * rng.normal(size=300)
+    big = np.asarray([3] * 17 + [1] * 18, np.int32)
+    nat.insert(5, (big, np.asarray([1.0] * 17 + [0.0] * 18, np.float32),
+                   np.asarray([-1] * 17 + list(range(18)), np.int32)))
+    inits.insert(5, np.zeros(18))
+
+    class Stub:
+        def fit_batch(self, skeletons, inits, X, y, *, max_iter=100, native=None):
+            return [co_backend.COResult(np.asarray(c), -7, False, float("nan")) for c in inits]
+
+    lm = co_backend.KernelLM(max_iter=30, fallback=Stub())
+    res = lm.fit_batch(None, inits, X, y, native=nat)
+    assert len(res) == 13 and res[5].n_iter == -7
+    assert lm.last_stats == dict(n_total=13, n_kernel=12, n_fallback=1, n_overflow=1,
+                                 n_kmismatch=0)
+    for j, r in enumerate(res):
+        if j == 5:
+            continue
+        nt, nv, ci = nat[j]
+        pred = interp.eval_tree_arrays(nt, nv, ci, X, r.constants)
+        assert r.final_loss == pytest.approx(np.mean((pred - y) ** 2), rel=1e-9)
+    # c0*x0 + c1 recovers the line
+    assert np.allclose(res[0].constants, [1.5, -0.25], atol=5e-3) and res[0].converged
