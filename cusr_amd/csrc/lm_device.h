@@ -176,17 +176,19 @@ __device__ __forceinline__ void binary_p(int f, const R *l, const R *rv, bool wa
     case OP_ADD: CUSR_FOR_P { o[p] = l[p] + rv[p]; d1[p] = one; d2[p] = one; } break;
     case OP_SUB: CUSR_FOR_P { o[p] = l[p] - rv[p]; d1[p] = one; d2[p] = -one; } break;
     case OP_MUL: CUSR_FOR_P { o[p] = l[p] * rv[p]; d1[p] = rv[p]; d2[p] = l[p]; } break;
+    // d(l/r)/dr = -(l/r) * (1/r): one division for the value, one for 1/r
     case OP_DIV: case OP_LOOSE_DIV:
-        CUSR_FOR_P { o[p] = l[p] / rv[p]; d1[p] = one / rv[p]; d2[p] = -o[p] / rv[p]; }
+        CUSR_FOR_P { o[p] = l[p] / rv[p]; d1[p] = one / rv[p]; d2[p] = -(o[p] * d1[p]); }
         break;
     case OP_PDIV:
         CUSR_FOR_P {
             const bool prot = F::abs_(rv[p]) < F::eps9;
             const R den = prot ? one : rv[p];
             const R q = l[p] / den;
+            const R inv = one / den;
             o[p] = prot ? one : q;
-            d1[p] = prot ? zero : one / den;
-            d2[p] = prot ? zero : -q / den;
+            d1[p] = prot ? zero : inv;
+            d2[p] = prot ? zero : -(q * inv);
             z1[p] = prot;
             z2[p] = prot;
         }

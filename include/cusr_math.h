@@ -87,6 +87,28 @@ typedef const float *cm_ftab;
 #define CM_SQRTF sqrtf
 #endif
 
+/* Horner step p * z + c with c a table coefficient. On the device the
+ * coefficient sits in scalar registers after its scalar load; the VOP3 fma
+ * takes it from there, where the compiler's two-address fmac form would first
+ * copy it into a vector register pair. Same IEEE fused multiply-add. */
+#if defined(__HIP_DEVICE_COMPILE__)
+static __device__ __forceinline__ double cm_fma_sd(double a, double b, double c) {
+    double r;
+    __asm__("v_fma_f64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(c));
+    return r;
+}
+static __device__ __forceinline__ float cm_fma_sf(float a, float b, float c) {
+    float r;
+    __asm__("v_fma_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(c));
+    return r;
+}
+#define CM_HORNER(p, z, c) cm_fma_sd((p), (z), (c))
+#define CM_HORNERF(p, z, c) cm_fma_sf((p), (z), (c))
+#else
+#define CM_HORNER(p, z, c) CM_FMA((p), (z), (c))
+#define CM_HORNERF(p, z, c) CM_FMAF((p), (z), (c))
+#endif
+
 /* ------------------------------------------------------------ bit helpers */
 
 CM_FN uint64_t cm_bits(double x) { uint64_t u; __builtin_memcpy(&u, &x, 8); return u; }
@@ -139,7 +161,7 @@ CM_FN double cm_exp(double x) {
     double r = CM_FMA(-kf, t[1], x);
     r = CM_FMA(-kf, t[2], r);
     double p = t[3];
-    for (int i = 4; i < 17; i++) p = CM_FMA(p, r, t[i]);
+    for (int i = 4; i < 17; i++) p = CM_HORNER(p, r, t[i]);
     int k = (int)kf;
     if (k >= -1020 && k <= 1022) return p * cm_pow2i(k);
     if (k > 1022) return (p * cm_pow2i(k - 2)) * 4.0;
@@ -162,7 +184,7 @@ CM_FN float cm_expf(float x) {
     float r = CM_FMAF(-kf, t[1], x);
     r = CM_FMAF(-kf, t[2], r);
     float p = t[3];
-    for (int i = 4; i < 11; i++) p = CM_FMAF(p, r, t[i]);
+    for (int i = 4; i < 11; i++) p = CM_HORNERF(p, r, t[i]);
     int k = (int)kf;
     if (k >= -124 && k <= 126) return p * cm_pow2if(k);
     if (k > 126) return (p * cm_pow2if(k - 2)) * 4.0f;
@@ -197,7 +219,7 @@ CM_FN double cm_log(double x) {
     double z = s * s;
     cm_dtab t = CM_TAB(cm_dtab, cm_log_tab);
     double R = t[0];
-    for (int i = 1; i < 11; i++) R = CM_FMA(R, z, t[i]);
+    for (int i = 1; i < 11; i++) R = CM_HORNER(R, z, t[i]);
     R = R * z;
     double hfsq = 0.5 * (f * f);
     double dk = (double)e;
@@ -229,7 +251,7 @@ CM_FN float cm_logf(float x) {
     float z = s * s;
     cm_ftab t = CM_TAB(cm_ftab, cm_logf_tab);
     float R = t[0];
-    for (int i = 1; i < 6; i++) R = CM_FMAF(R, z, t[i]);
+    for (int i = 1; i < 6; i++) R = CM_HORNERF(R, z, t[i]);
     R = R * z;
     float hfsq = 0.5f * (f * f);
     float dk = (float)e;
@@ -253,37 +275,41 @@ CM_ACCESSOR(cm_dtab, cm_trig_tab)
 CM_FN double cm_sin_kernel(double r, cm_dtab t) {
     double z = r * r;
     double p = t[0];
-    for (int i = 1; i < 8; i++) p = CM_FMA(p, z, t[i]);
+    for (int i = 1; i < 8; i++) p = CM_HORNER(p, z, t[i]);
     return CM_FMA(r * z, p, r);
 }
 
 CM_FN double cm_cos_kernel(double r, cm_dtab t) {
     double z = r * r;
     double p = t[8];
-    for (int i = 9; i < 16; i++) p = CM_FMA(p, z, t[i]);
+    for (int i = 9; i < 16; i++) p = CM_HORNER(p, z, t[i]);
     double hz = 0.5 * z;
     double w = 1.0 - hz;
     return w + (((1.0 - w) - hz) + z * (z * p));
 }
 
-/* sin and cos of x from one argument reduction */
+/* sin and cos of x from one argument reduction. Branch-free: NaN and +-inf
+ * give NaN, |x| >= 2^50 gives sin 0 and cos 1, both through the reduction of
+ * 0 and a final select; the quadrant k mod 4 swaps and negates. */
 CM_FN void cm_sincos(double x, double *s, double *c) {
-    if (cm_isnan(x) || cm_fabs(x) == CM_INF) { *s = CM_NAN; *c = CM_NAN; return; }
-    if (cm_fabs(x) >= 1125899906842624.0) { *s = 0.0; *c = 1.0; return; } /* 2^50 */
+    const double ax = cm_fabs(x);
+    const int bad = !(ax < CM_INF);
+    const int huge = !bad && ax >= 1125899906842624.0; /* 2^50 */
+    const double xr = (bad || huge) ? 0.0 : x;
     cm_dtab t = CM_TAB(cm_dtab, cm_trig_tab);
-    double kf = cm_rint_small(x * t[16]);
-    double r = CM_FMA(-kf, t[17], x);
+    double kf = cm_rint_small(xr * t[16]);
+    double r = CM_FMA(-kf, t[17], xr);
     r = CM_FMA(-kf, t[18], r);
     r = CM_FMA(-kf, t[19], r);
     double q4 = kf - 4.0 * cm_rint_small(kf * 0.25 - 0.375); /* kf mod 4, in 0..3 */
     int q = (int)q4;
     double sr = cm_sin_kernel(r, t), cr = cm_cos_kernel(r, t);
-    switch (q & 3) {
-    case 0: *s = sr; *c = cr; break;
-    case 1: *s = cr; *c = -sr; break;
-    case 2: *s = -sr; *c = -cr; break;
-    default: *s = -cr; *c = sr; break;
-    }
+    double so = (q & 1) ? cr : sr;
+    double co = (q & 1) ? sr : cr;
+    so = (q & 2) ? -so : so;
+    co = ((q + 1) & 2) ? -co : co;
+    *s = bad ? CM_NAN : (huge ? 0.0 : so);
+    *c = bad ? CM_NAN : (huge ? 1.0 : co);
 }
 
 CM_FN double cm_sin(double x) { double s, c; cm_sincos(x, &s, &c); return s; }
@@ -303,36 +329,38 @@ CM_ACCESSOR(cm_ftab, cm_trigf_tab)
 CM_FN float cm_sin_kernelf(float r, cm_ftab t) {
     float z = r * r;
     float p = t[0];
-    for (int i = 1; i < 5; i++) p = CM_FMAF(p, z, t[i]);
+    for (int i = 1; i < 5; i++) p = CM_HORNERF(p, z, t[i]);
     return CM_FMAF(r * z, p, r);
 }
 
 CM_FN float cm_cos_kernelf(float r, cm_ftab t) {
     float z = r * r;
     float p = t[5];
-    for (int i = 6; i < 10; i++) p = CM_FMAF(p, z, t[i]);
+    for (int i = 6; i < 10; i++) p = CM_HORNERF(p, z, t[i]);
     float hz = 0.5f * z;
     float w = 1.0f - hz;
     return w + (((1.0f - w) - hz) + z * (z * p));
 }
 
 CM_FN void cm_sincosf(float x, float *s, float *c) {
-    if (x != x || cm_fabsf(x) == CM_INFF) { *s = CM_NANF; *c = CM_NANF; return; }
-    if (cm_fabsf(x) >= 2097152.0f) { *s = 0.0f; *c = 1.0f; return; } /* 2^21 */
+    const float ax = cm_fabsf(x);
+    const int bad = !(ax < CM_INFF);
+    const int huge = !bad && ax >= 2097152.0f; /* 2^21 */
+    const float xr = (bad || huge) ? 0.0f : x;
     cm_ftab t = CM_TAB(cm_ftab, cm_trigf_tab);
-    float kf = cm_rint_smallf(x * t[10]);
-    float r = CM_FMAF(-kf, t[11], x);
+    float kf = cm_rint_smallf(xr * t[10]);
+    float r = CM_FMAF(-kf, t[11], xr);
     r = CM_FMAF(-kf, t[12], r);
     r = CM_FMAF(-kf, t[13], r);
     float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
     int q = (int)q4;
     float sr = cm_sin_kernelf(r, t), cr = cm_cos_kernelf(r, t);
-    switch (q & 3) {
-    case 0: *s = sr; *c = cr; break;
-    case 1: *s = cr; *c = -sr; break;
-    case 2: *s = -sr; *c = -cr; break;
-    default: *s = -cr; *c = sr; break;
-    }
+    float so = (q & 1) ? cr : sr;
+    float co = (q & 1) ? sr : cr;
+    so = (q & 2) ? -so : so;
+    co = ((q + 1) & 2) ? -co : co;
+    *s = bad ? CM_NANF : (huge ? 0.0f : so);
+    *c = bad ? CM_NANF : (huge ? 1.0f : co);
 }
 
 CM_FN float cm_sinf(float x) { float s, c; cm_sincosf(x, &s, &c); return s; }
@@ -356,7 +384,7 @@ CM_FN double cm_sinh(double x) {
         cm_dtab t = CM_TAB(cm_dtab, cm_sinh_tab);
         double z = a * a;
         double p = t[0];
-        for (int i = 1; i < 9; i++) p = CM_FMA(p, z, t[i]);
+        for (int i = 1; i < 9; i++) p = CM_HORNER(p, z, t[i]);
         r = CM_FMA(a * z, p, a);
     } else if (a < 709.0) {
         double e = cm_exp(a);
@@ -406,7 +434,7 @@ CM_FN float cm_sinhf(float x) {
         cm_ftab t = CM_TAB(cm_ftab, cm_sinhf_tab);
         float z = a * a;
         float p = t[0];
-        for (int i = 1; i < 5; i++) p = CM_FMAF(p, z, t[i]);
+        for (int i = 1; i < 5; i++) p = CM_HORNERF(p, z, t[i]);
         r = CM_FMAF(a * z, p, a);
     } else if (a < 88.0f) {
         float e = cm_expf(a);

@@ -182,10 +182,11 @@ static double op_b64(int f, double l, double rv, int want_d2, double *d1, double
     case OP_ADD: o = l + rv; *d1 = 1.0; *d2 = 1.0; break;
     case OP_SUB: o = l - rv; *d1 = 1.0; *d2 = -1.0; break;
     case OP_MUL: o = l * rv; *d1 = rv; *d2 = l; break;
-    case OP_DIV: case OP_LOOSE_DIV: o = l / rv; *d1 = 1.0 / rv; *d2 = -o / rv; break;
+    /* d(l/r)/dr = -(l/r) * (1/r): one division for the value, one for 1/r */
+    case OP_DIV: case OP_LOOSE_DIV: o = l / rv; *d1 = 1.0 / rv; *d2 = -(o * *d1); break;
     case OP_PDIV:
         if (fabs(rv) < 1e-9) { o = 1.0; *d1 = 0.0; *d2 = 0.0; *mode = 1; }
-        else { o = l / rv; *d1 = 1.0 / rv; *d2 = -o / rv; }
+        else { o = l / rv; *d1 = 1.0 / rv; *d2 = -(o * *d1); }
         break;
     case OP_POW:
         o = cm_pow(l, rv);
@@ -258,10 +259,10 @@ static float op_b32(int f, float l, float rv, int want_d2, float *d1, float *d2,
     case OP_ADD: o = l + rv; *d1 = 1.0f; *d2 = 1.0f; break;
     case OP_SUB: o = l - rv; *d1 = 1.0f; *d2 = -1.0f; break;
     case OP_MUL: o = l * rv; *d1 = rv; *d2 = l; break;
-    case OP_DIV: case OP_LOOSE_DIV: o = l / rv; *d1 = 1.0f / rv; *d2 = -o / rv; break;
+    case OP_DIV: case OP_LOOSE_DIV: o = l / rv; *d1 = 1.0f / rv; *d2 = -(o * *d1); break;
     case OP_PDIV:
         if (fabsf(rv) < 1e-9f) { o = 1.0f; *d1 = 0.0f; *d2 = 0.0f; *mode = 1; }
-        else { o = l / rv; *d1 = 1.0f / rv; *d2 = -o / rv; }
+        else { o = l / rv; *d1 = 1.0f / rv; *d2 = -(o * *d1); }
         break;
     case OP_POW:
         o = cm_powf(l, rv);
