@@ -139,7 +139,8 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
     case OP_LOOSE_SQRT:
         CUSR_FOR_P {
             r[p] = F::sqrt_(F::abs_(a[p]));
-            d[p] = (a[p] > zero) ? one / (two * r[p]) : ((a[p] < zero) ? -one / (two * r[p]) : zero);
+            const R inv = one / (two * r[p]);      // -(1/x) == (-1)/x exactly
+            d[p] = (a[p] > zero) ? inv : ((a[p] < zero) ? -inv : zero);
         }
         break;
     case OP_CEXP:
@@ -156,7 +157,8 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
         CUSR_FOR_P {
             const R t = F::abs_(a[p]) + F::eps9;
             r[p] = F::log_(t);
-            d[p] = (a[p] > zero) ? one / t : ((a[p] < zero) ? -one / t : zero);
+            const R inv = one / t;
+            d[p] = (a[p] > zero) ? inv : ((a[p] < zero) ? -inv : zero);
         }
         break;
     case OP_IDENT: CUSR_FOR_P { r[p] = a[p]; d[p] = one; } break;

@@ -153,19 +153,24 @@ CM_TABLE double cm_exp_tab[17] = {
 CM_ACCESSOR(cm_dtab, cm_exp_tab)
 
 CM_FN double cm_exp(double x) {
-    if (cm_isnan(x)) return x;
-    if (x > 709.782712893384) return CM_INF;
-    if (x < -745.1332191019412) return 0.0;
+    /* branch-free: out-of-range and NaN arguments reduce 0 and are selected
+     * at the end; the scaling by 2^k is split in two outside the normal range */
+    const int nan = cm_isnan(x);
+    const int hi = x > 709.782712893384;
+    const int lo = x < -745.1332191019412;
+    const double xr = (nan || hi || lo) ? 0.0 : x;
     cm_dtab t = CM_TAB(cm_dtab, cm_exp_tab);
-    double kf = cm_rint_small(x * t[0]);
-    double r = CM_FMA(-kf, t[1], x);
+    double kf = cm_rint_small(xr * t[0]);
+    double r = CM_FMA(-kf, t[1], xr);
     r = CM_FMA(-kf, t[2], r);
     double p = t[3];
     for (int i = 4; i < 17; i++) p = CM_HORNER(p, r, t[i]);
     int k = (int)kf;
-    if (k >= -1020 && k <= 1022) return p * cm_pow2i(k);
-    if (k > 1022) return (p * cm_pow2i(k - 2)) * 4.0;
-    return (p * cm_pow2i(k + 1000)) * cm_pow2i(-1000);
+    const int big = k > 1022, small = k < -1020;
+    const int ka = big ? k - 2 : (small ? k + 1000 : k);
+    double res = p * cm_pow2i(ka);
+    res = big ? res * 4.0 : (small ? res * cm_pow2i(-1000) : res);
+    return nan ? x : (hi ? CM_INF : (lo ? 0.0 : res));
 }
 
 /* 1/ln2, ln2 head (16 bits), ln2 tail, then 1/7!, ..., 1/2!, 1, 1 */
@@ -176,19 +181,22 @@ CM_TABLE float cm_expf_tab[11] = {
 CM_ACCESSOR(cm_ftab, cm_expf_tab)
 
 CM_FN float cm_expf(float x) {
-    if (x != x) return x;
-    if (x > 88.72283f) return CM_INFF;
-    if (x < -103.97208f) return 0.0f;
+    const int nan = x != x;
+    const int hi = x > 88.72283f;
+    const int lo = x < -103.97208f;
+    const float xr = (nan || hi || lo) ? 0.0f : x;
     cm_ftab t = CM_TAB(cm_ftab, cm_expf_tab);
-    float kf = cm_rint_smallf(x * t[0]);
-    float r = CM_FMAF(-kf, t[1], x);
+    float kf = cm_rint_smallf(xr * t[0]);
+    float r = CM_FMAF(-kf, t[1], xr);
     r = CM_FMAF(-kf, t[2], r);
     float p = t[3];
     for (int i = 4; i < 11; i++) p = CM_HORNERF(p, r, t[i]);
     int k = (int)kf;
-    if (k >= -124 && k <= 126) return p * cm_pow2if(k);
-    if (k > 126) return (p * cm_pow2if(k - 2)) * 4.0f;
-    return (p * cm_pow2if(k + 100)) * cm_pow2if(-100);
+    const int big = k > 126, small = k < -124;
+    const int ka = big ? k - 2 : (small ? k + 100 : k);
+    float res = p * cm_pow2if(ka);
+    res = big ? res * 4.0f : (small ? res * cm_pow2if(-100) : res);
+    return nan ? x : (hi ? CM_INFF : (lo ? 0.0f : res));
 }
 
 /* ------------------------------------------------------------------- log */
@@ -201,19 +209,16 @@ CM_TABLE double cm_log_tab[13] = {
 CM_ACCESSOR(cm_dtab, cm_log_tab)
 
 CM_FN double cm_log(double x) {
-    if (cm_isnan(x)) return x;
-    if (x < 0.0) return CM_NAN;
-    if (x == 0.0) return -CM_INF;
-    if (x == CM_INF) return x;
-    uint64_t u = cm_bits(x);
-    int e = (int)((u >> 52) & 0x7ff);
-    if (e == 0) { /* subnormal */
-        u = cm_bits(x * 18014398509481984.0); /* 2^54 */
-        e = (int)((u >> 52) & 0x7ff) - 54;
-    }
-    e -= 1023;
+    /* branch-free: subnormals are scaled by 2^54 through a select; NaN,
+     * negative, zero and +inf arguments are selected at the end */
+    const int sub = x > 0.0 && x < 2.2250738585072014e-308;
+    const double xs = sub ? x * 18014398509481984.0 : x; /* 2^54 */
+    uint64_t u = cm_bits(xs);
+    int e = (int)((u >> 52) & 0x7ff) - (sub ? 54 : 0) - 1023;
     double m = cm_dbl((u & 0x000fffffffffffffULL) | 0x3ff0000000000000ULL);
-    if (m > 1.4142135623730951) { m = m * 0.5; e += 1; }
+    const int up = m > 1.4142135623730951;
+    m = up ? m * 0.5 : m;
+    e = up ? e + 1 : e;
     double f = m - 1.0;
     double s = f / (2.0 + f);
     double z = s * s;
@@ -223,7 +228,8 @@ CM_FN double cm_log(double x) {
     R = R * z;
     double hfsq = 0.5 * (f * f);
     double dk = (double)e;
-    return dk * t[11] - ((hfsq - (s * (hfsq + R) + dk * t[12])) - f);
+    double res = dk * t[11] - ((hfsq - (s * (hfsq + R) + dk * t[12])) - f);
+    return cm_isnan(x) ? x : (x < 0.0 ? CM_NAN : (x == 0.0 ? -CM_INF : (x == CM_INF ? x : res)));
 }
 
 /* 2/13, ..., 2/3, then ln2 head and tail */
@@ -233,19 +239,14 @@ CM_TABLE float cm_logf_tab[8] = {
 CM_ACCESSOR(cm_ftab, cm_logf_tab)
 
 CM_FN float cm_logf(float x) {
-    if (x != x) return x;
-    if (x < 0.0f) return CM_NANF;
-    if (x == 0.0f) return -CM_INFF;
-    if (x == CM_INFF) return x;
-    uint32_t u = cm_bitsf(x);
-    int e = (int)((u >> 23) & 0xff);
-    if (e == 0) {
-        u = cm_bitsf(x * 33554432.0f); /* 2^25 */
-        e = (int)((u >> 23) & 0xff) - 25;
-    }
-    e -= 127;
+    const int sub = x > 0.0f && x < 1.17549435e-38f;
+    const float xs = sub ? x * 33554432.0f : x; /* 2^25 */
+    uint32_t u = cm_bitsf(xs);
+    int e = (int)((u >> 23) & 0xff) - (sub ? 25 : 0) - 127;
     float m = cm_flt((u & 0x007fffffu) | 0x3f800000u);
-    if (m > 1.4142135381698608f) { m = m * 0.5f; e += 1; }
+    const int up = m > 1.4142135381698608f;
+    m = up ? m * 0.5f : m;
+    e = up ? e + 1 : e;
     float f = m - 1.0f;
     float s = f / (2.0f + f);
     float z = s * s;
@@ -255,7 +256,8 @@ CM_FN float cm_logf(float x) {
     R = R * z;
     float hfsq = 0.5f * (f * f);
     float dk = (float)e;
-    return dk * t[6] - ((hfsq - (s * (hfsq + R) + dk * t[7])) - f);
+    float res = dk * t[6] - ((hfsq - (s * (hfsq + R) + dk * t[7])) - f);
+    return (x != x) ? x : (x < 0.0f ? CM_NANF : (x == 0.0f ? -CM_INFF : (x == CM_INFF ? x : res)));
 }
 
 /* --------------------------------------------------------------- sin/cos */
