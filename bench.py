@@ -223,6 +223,8 @@ def main():
     ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--rounds", type=int, default=3, help="C5 rounds (the spec runs 20)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ad-mode", type=int, default=None, choices=[0, 1],
+                    help="override the configuration's AD mode (0 forward, 1 reverse)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip the end-to-end fit from host buffers (profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -237,6 +239,9 @@ def main():
     from cusr_amd.kernel import co_inproc
 
     cfg = gen_synth.CONFIGS[args.config]
+    if args.ad_mode is not None:
+        cfg = gen_synth.scaled(cfg)
+        cfg.ad_mode = args.ad_mode
     co = co_inproc.get_inproc_co(0, "ad")
 
     def gen(round_index=0):

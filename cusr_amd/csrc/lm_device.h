@@ -429,7 +429,20 @@ struct PassArgs {
     int pwaves;         // wavefronts of the workgroup; wave w sums partitions w, w+pwaves, ...
     int wave;           // this wavefront
     double *part;       // LDS [parts][sums_width(K)] partition sums (parts > 1)
+    double *jt;         // LDS [64][17] augmented Jacobian rows of one slice (matrix sums)
 };
+
+// Matrix sums (forward AD, K >= CO_SUMS_MATRIX_MIN_K): v_mfma_f64_16x16x4 takes A[i][k]
+// from lane i + 16k and B[k][j] from lane j + 16k, and returns D[i][j] in
+// lane j + 16 (i mod 4), register i / 4; each output is the chain
+// c = fma(a_k, b_k, c) over k = 0..3 (measured on gfx950). With A = B^T =
+// 4 rows of [J | r], 16 instructions fold one 64-point slice into the
+// 16 x 16 accumulator in ascending point order.
+typedef double cusr_double4 __attribute__((ext_vector_type(4)));
+constexpr int kJtStride = 17;                       // doubles per row (bank spread)
+constexpr size_t kJtBytes = (size_t)kLanes * kJtStride * sizeof(double);
+template <int K, int AD>
+constexpr bool matrix_sums() { return AD == CO_AD_FORWARD && K >= CO_SUMS_MATRIX_MIN_K; }
 
 constexpr int sums_width(int K) { return 1 + K + K * (K + 1) / 2; }
 
@@ -462,12 +475,16 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
                           double *out, int lane) {
     constexpr int W = (JAC == 0) ? 1 : sums_width(K);
     constexpr int KT = (K > 0) ? K : 1;
+    constexpr bool MX = (JAC == 1) && matrix_sums<K, CO_AD_FORWARD>();
+    // per-lane accumulators: all sums, or (matrix sums, K = 16) r^2 and J^T r
+    constexpr int WL = MX ? ((K < 16) ? 1 : 1 + K) : W;
     const int granules = (a.N + kLanes - 1) / kLanes;
     const int last = a.N - 1;
     for (int part = a.wave; part < a.parts; part += a.pwaves) {
-    double acc[W];
+    double acc[WL];
 #pragma unroll
-    for (int q = 0; q < W; ++q) acc[q] = 0.0;
+    for (int q = 0; q < WL; ++q) acc[q] = 0.0;
+    cusr_double4 g4 = {0.0, 0.0, 0.0, 0.0};
     // granules part, part + G, part + 2G, ... of this partition, P per batch
     const int ng = (part < granules) ? (granules - part + a.parts - 1) / a.parts : 0;
     const int batches = (ng + P - 1) / P;
@@ -498,6 +515,29 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
         for (int j = 0; j < P * KT; ++j) T[j] = (JAC == 1) ? R(1) : R(0);
         forward_pass<K, R, P, JAC>(a.prog, a.n, w, cs, lane, accv, T);
         if constexpr (JAC == 2) reverse_pass<K, R, P>(a.prog, a.n, w, lane, T);
+        if constexpr (MX) {
+            CUSR_FOR_P {
+                const double r = valid[p] ? (double)accv[p] - yv[p] : 0.0;
+                double *row = a.jt + lane * kJtStride;
+#pragma unroll
+                for (int j = 0; j < K; ++j) row[j] = valid[p] ? (double)T[p * KT + j] : 0.0;
+                if constexpr (K < 16) {
+                    row[K] = r;
+                } else if (valid[p]) {
+                    acc[0] = fma(r, r, acc[0]);
+#pragma unroll
+                    for (int j = 0; j < K; ++j) acc[1 + j] = fma((double)T[p * KT + j], r, acc[1 + j]);
+                }
+                wave_sync_lds();
+#pragma unroll
+                for (int m = 0; m < 16; ++m) {
+                    const double v = a.jt[(4 * m + (lane >> 4)) * kJtStride + (lane & 15)];
+                    g4 = __builtin_amdgcn_mfma_f64_16x16x4f64(v, v, g4, 0, 0, 0);
+                }
+                wave_sync_lds();
+            }
+            continue;
+        }
         CUSR_FOR_P {
             if (valid[p]) {
                 const double r = (double)accv[p] - yv[p];
@@ -516,11 +556,36 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
             }
         }
     }
-    wave_allreduce<W>(acc);
     double *dst = (a.parts == 1) ? out : a.part + part * W;
-    if (lane == 0) {
+    if constexpr (MX) {
+        // the accumulator to LDS as G[16][16], then the sums vector by lane 0
+        double *gt = a.jt;
 #pragma unroll
-        for (int q = 0; q < W; ++q) dst[q] = acc[q];
+        for (int r4 = 0; r4 < 4; ++r4) gt[(4 * r4 + (lane >> 4)) * 16 + (lane & 15)] = g4[r4];
+        if constexpr (K == 16) wave_allreduce<WL>(acc);
+        wave_sync_lds();
+        if (lane == 0) {
+            if constexpr (K < 16) {
+                dst[0] = gt[K * 16 + K];
+#pragma unroll
+                for (int j = 0; j < K; ++j) dst[1 + j] = gt[j * 16 + K];
+            } else {
+#pragma unroll
+                for (int q = 0; q < WL; ++q) dst[q] = acc[q];
+            }
+            int q = 1 + K;
+#pragma unroll
+            for (int j1 = 0; j1 < K; ++j1)
+#pragma unroll
+                for (int j2 = j1; j2 < K; ++j2, ++q) dst[q] = gt[j1 * 16 + j2];
+        }
+        wave_sync_lds();
+    } else {
+        wave_allreduce<WL>(acc);
+        if (lane == 0) {
+#pragma unroll
+            for (int q = 0; q < W; ++q) dst[q] = acc[q];
+        }
     }
     }
     if (a.parts == 1) {
@@ -596,6 +661,65 @@ __device__ __forceinline__ bool damped_solve(const double *s, double lambda, dou
     return true;
 }
 
+// The same solve with L in LDS (the matrix-sum kernels,
+// where K(K+1)/2 doubles per lane of the register version would set the
+// kernel's register count). Every element gets exactly the arithmetic of
+// damped_solve: column j's pivot is computed by every lane, the entries below
+// it by lane i; the substitutions run on every lane with L read by broadcast.
+template <int K>
+__device__ __forceinline__ bool damped_solve_lds(const double *s, double lambda, double (&delta)[K],
+                                                 double *L, int lane) {
+    double *b = L + K * K;   // right-hand side, then the solution (LDS, K doubles)
+    // L[i][j] = upper-triangle element (j, i) of J^T J for j <= i; diagonal damped
+    if (lane < K) {
+        const int i = lane;
+        for (int j = 0; j <= i; ++j) {
+            double v = s[1 + K + j * K - (j * (j - 1)) / 2 + (i - j)];
+            if (j == i) v = v * (1.0 + lambda);
+            L[i * K + j] = v;
+        }
+        b[i] = -s[1 + i];
+    }
+    wave_sync_lds();
+    bool ok = true;
+#pragma unroll 1
+    for (int j = 0; j < K; ++j) {
+        double sj = L[j * K + j];
+        for (int k = 0; k < j; ++k) sj = fma(-L[j * K + k], L[j * K + k], sj);
+        if (sj <= 0.0) ok = false;
+        const double dj = ::sqrt(sj);
+        if (lane > j && lane < K) {
+            const int i = lane;
+            double t = L[i * K + j];
+            for (int k = 0; k < j; ++k) t = fma(-L[i * K + k], L[j * K + k], t);
+            L[i * K + j] = t / dj;
+        }
+        wave_sync_lds();
+        if (lane == j) L[j * K + j] = dj;
+        wave_sync_lds();
+    }
+    if (!ok) return false;
+#pragma unroll 1
+    for (int i = 0; i < K; ++i) {
+        double t = b[i];
+        for (int k = 0; k < i; ++k) t = fma(-L[i * K + k], b[k], t);
+        wave_sync_lds();
+        if (lane == 0) b[i] = t / L[i * K + i];
+        wave_sync_lds();
+    }
+#pragma unroll 1
+    for (int i = K - 1; i >= 0; --i) {
+        double t = b[i];
+        for (int k = i + 1; k < K; ++k) t = fma(-L[k * K + i], b[k], t);
+        wave_sync_lds();
+        if (lane == 0) b[i] = t / L[i * K + i];
+        wave_sync_lds();
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) delta[i] = b[i];
+    return true;
+}
+
 // ------------------------------------------------------------- the fit
 
 struct FitArgs {
@@ -627,6 +751,14 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     constexpr int JAC = (K == 0) ? 0 : (AD == CO_AD_REVERSE ? 2 : 1);
     char *my_lds = lds_dyn + (size_t)wave * fa.wave_bytes;
     const bool lead = wave == 0;     // the wavefront that writes shared state
+    double *jt = (double *)my_lds;   // matrix sums: [64][17] slice tile first
+    double *lds_l = jt + kLanes * kJtStride;   // then the K x K Cholesky factor and rhs
+    if constexpr (matrix_sums<K, AD>()) {
+        // columns K+1.. of every row stay zero for the whole fit
+#pragma unroll
+        for (int j = 0; j < kJtStride; ++j) jt[lane * kJtStride + j] = 0.0;
+        my_lds += kJtBytes + (size_t)K * (K + 1) * sizeof(double);
+    }
     WaveLds<R, P> wl;
     wl.x = (R *)my_lds;
     wl.slot = wl.x + (size_t)fa.D * P * kLanes;
@@ -642,6 +774,7 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     pa.pwaves = fa.pwaves;
     pa.wave = wave;
     pa.part = (double *)(lds_dyn + (size_t)fa.pwaves * fa.wave_bytes);
+    pa.jt = jt;
 
     double *c_cur = lds_c, *c_try = lds_c + CO_MAX_K;
     double *s_cur = lds_s, *s_try = lds_s + sums_width(CO_MAX_K);
@@ -658,7 +791,12 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
         while (uni(st) == ST_RUN && it < fa.max_iter) {
             ++it;
             double delta[K];
-            if (!damped_solve<K>(s_cur, lambda, delta)) {
+            bool solved;
+            if constexpr (matrix_sums<K, AD>())
+                solved = damped_solve_lds<K>(s_cur, lambda, delta, lds_l, lane);
+            else
+                solved = damped_solve<K>(s_cur, lambda, delta);
+            if (!solved) {
                 lambda = lambda * 10.0;
                 if (lambda > 1e12) st = ST_CHOL;
                 continue;
@@ -776,7 +914,8 @@ template <typename R, int K, int AD>
 constexpr size_t fit_lds_bytes_t(int D, int slots, int tape) {
     const size_t a = (size_t)(D + slots + tape) * points_per_pass<R, K, AD>() * kLanes * sizeof(R);
     const size_t b = (size_t)(D + slots) * kLanes * sizeof(double);
-    return a > b ? a : b;
+    return (matrix_sums<K, AD>() ? kJtBytes + (size_t)K * (K + 1) * sizeof(double) : 0) +
+           (a > b ? a : b);
 }
 
 hipError_t launch_fit_f64_fwd(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);

@@ -87,6 +87,19 @@ static inline int co_partitions_for_n(int N) {
 }
 #define CO_MAX_PARTITIONS 4
 
+/* Forward-AD fits of expressions with K >= CO_SUMS_MATRIX_MIN_K form their
+ * sums with the fp64 matrix instruction (v_mfma_f64_16x16x4): the augmented
+ * Jacobian rows [J | r] of a partition's points are multiplied into one
+ * 16 x 16 accumulator, which adds the products of each entry with one fused
+ * multiply-add per point in ascending point order (no per-lane split, no
+ * butterfly). For K = 16 the r column does not fit: r^2 and J^T r then keep
+ * the per-lane order. Part of the arithmetic order, so the CPU oracle
+ * follows the same rule. (Below the threshold, and in reverse mode, whose
+ * LDS tape already limits occupancy, the per-lane sums are faster.) */
+#ifndef CO_SUMS_MATRIX_MIN_K
+#define CO_SUMS_MATRIX_MIN_K 13
+#endif
+
 /* --- reference ABI (cusr/kernel/co_lib.h:45-71) ------------------------ */
 
 /* Select device_id, create its context once and return an opaque handle. */

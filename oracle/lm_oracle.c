@@ -447,22 +447,31 @@ typedef struct {
 
 /* Sums over points in the canonical lane order (see the file header). */
 /* One pass in the device's order (cusr_amd/csrc/lm_device.h data_pass):
- * 64-point granule g belongs to partition g mod G; point i of a partition
- * goes to lane i mod 64, which sums its points in ascending order from 0.0
- * with fma; each partition combines its lanes with strides 32..1; the
- * partitions are then added in order 0, 1, ..., G-1. */
+ * 64-point granule g belongs to partition g mod G; the partitions' sums are
+ * added in order 0, 1, ..., G-1 at the end. Within a partition:
+ *   - otherwise (smaller K, reverse AD, value-only passes): point i goes to
+ *     lane i mod 64, which sums its points in ascending order from 0.0 with
+ *     fma; the lanes combine with strides 32..1;
+ *   - forward AD with K >= CO_SUMS_MATRIX_MIN_K: every entry of [J | r]^T [J | r]
+ *     is one fma chain over the partition's points in ascending order (the
+ *     matrix instruction's order); for K = 16, r^2 and J^T r keep the lane
+ *     order above. */
 static void orc_pass(const Tree *t, int N, int D, const double *xs, const double *y,
                      const double *c, int prec, int jac, int G, PassOut *out) {
     int K = t->K;
     int nq = K * (K + 1) / 2;
     int width = 1 + K + nq;
-    double *acc = (double *)calloc((size_t)G * ORC_LANES * width, sizeof(double));
+    const int mx = jac == 1 && K >= CO_SUMS_MATRIX_MIN_K;   /* forward AD only */
+    const int ncol = K < 16 ? K + 1 : 16;   /* columns of the matrix product */
+    const int lane_w = mx ? (K < 16 ? 0 : 1 + K) : width;
+    double *acc = (double *)calloc((size_t)G * ORC_LANES * (lane_w ? lane_w : 1), sizeof(double));
+    double *gm = mx ? (double *)calloc((size_t)G * 256, sizeof(double)) : NULL;
     double g64[ORC_MAXK];
     float g32[ORC_MAXK];
-    double x[64];
+    double x[64], aug[17];
     for (int i = 0; i < N; i++) {
         int part = (i / ORC_LANES) % G;
-        double *a = acc + ((size_t)part * ORC_LANES + (size_t)(i % ORC_LANES)) * width;
+        double *a = acc + ((size_t)part * ORC_LANES + (size_t)(i % ORC_LANES)) * (lane_w ? lane_w : 1);
         for (int k = 0; k < D; k++) x[k] = xs[(size_t)i * D + k];
         double f;
         if (prec == CO_PREC_FP64) {
@@ -473,6 +482,19 @@ static void orc_pass(const Tree *t, int N, int D, const double *xs, const double
                 for (int k = 0; k < K; k++) g64[k] = (double)g32[k];
         }
         double r = f - y[i];
+        if (mx) {
+            for (int k = 0; k < K; k++) aug[k] = g64[k];
+            if (K < 16) aug[K] = r;
+            double *gp = gm + (size_t)part * 256;
+            for (int i1 = 0; i1 < ncol; i1++)
+                for (int i2 = 0; i2 < ncol; i2++)
+                    gp[i1 * 16 + i2] = fma(aug[i1], aug[i2], gp[i1 * 16 + i2]);
+            if (K == 16) {
+                a[0] = fma(r, r, a[0]);
+                for (int j = 0; j < K; j++) a[1 + j] = fma(g64[j], r, a[1 + j]);
+            }
+            continue;
+        }
         a[0] = fma(r, r, a[0]);
         if (jac) {
             for (int j = 0; j < K; j++) a[1 + j] = fma(g64[j], r, a[1 + j]);
@@ -481,29 +503,47 @@ static void orc_pass(const Tree *t, int N, int D, const double *xs, const double
                 for (int j2 = j1; j2 < K; j2++, q++) a[q] = fma(g64[j1], g64[j2], a[q]);
         }
     }
+    /* per partition: lane butterfly (lane sums), then the sums vector */
+    double *sums = (double *)calloc((size_t)G * width, sizeof(double));
     for (int part = 0; part < G; part++) {
-        double *pacc = acc + (size_t)part * ORC_LANES * width;
-        for (int s = ORC_LANES / 2; s >= 1; s >>= 1) {
-            /* every lane becomes p[l] + p[l^s]; lanes l and l^s hold the same value */
-            for (int l = 0; l < ORC_LANES; l++) {
-                if (l & s) continue;
-                double *pa = pacc + (size_t)l * width, *pb = pacc + (size_t)(l ^ s) * width;
-                for (int w = 0; w < width; w++) { double v = pa[w] + pb[w]; pa[w] = v; pb[w] = v; }
+        double *ps = sums + (size_t)part * width;
+        if (lane_w) {
+            double *pacc = acc + (size_t)part * ORC_LANES * lane_w;
+            for (int s = ORC_LANES / 2; s >= 1; s >>= 1) {
+                /* every lane becomes p[l] + p[l^s]; lanes l and l^s hold the same value */
+                for (int l = 0; l < ORC_LANES; l++) {
+                    if (l & s) continue;
+                    double *pa = pacc + (size_t)l * lane_w, *pb = pacc + (size_t)(l ^ s) * lane_w;
+                    for (int w = 0; w < lane_w; w++) { double v = pa[w] + pb[w]; pa[w] = v; pb[w] = v; }
+                }
             }
+            for (int w = 0; w < lane_w; w++) ps[w] = pacc[w];
+        }
+        if (mx) {
+            const double *gp = gm + (size_t)part * 256;
+            if (K < 16) {
+                ps[0] = gp[K * 16 + K];
+                for (int j = 0; j < K; j++) ps[1 + j] = gp[j * 16 + K];
+            }
+            int q = 1 + K;
+            for (int j1 = 0; j1 < K; j1++)
+                for (int j2 = j1; j2 < K; j2++, q++) ps[q] = gp[j1 * 16 + j2];
         }
     }
-    /* partition sums (lane 0 of each) added in partition order */
+    /* partition sums added in partition order */
     for (int part = 1; part < G; part++) {
-        const double *pp = acc + (size_t)part * ORC_LANES * width;
-        for (int w = 0; w < width; w++) acc[w] = acc[w] + pp[w];
+        const double *pp = sums + (size_t)part * width;
+        for (int w = 0; w < width; w++) sums[w] = sums[w] + pp[w];
     }
-    out->loss = 0.5 * acc[0];
+    out->loss = 0.5 * sums[0];
     if (jac) {
-        for (int j = 0; j < K; j++) out->jtr[j] = acc[1 + j];
+        for (int j = 0; j < K; j++) out->jtr[j] = sums[1 + j];
         int q = 1 + K;
         for (int j1 = 0; j1 < K; j1++)
-            for (int j2 = j1; j2 < K; j2++, q++) out->jtj[j1 * K + j2] = acc[q];
+            for (int j2 = j1; j2 < K; j2++, q++) out->jtj[j1 * K + j2] = sums[q];
     }
+    free(sums);
+    free(gm);
     free(acc);
 }
 

@@ -158,3 +158,17 @@ def test_large_n_auto_partitions(co):
     _say(f"large N: status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
     assert np.mean(d <= 1e-9) >= 0.95
     assert st >= 0.95
+
+
+@pytest.mark.parametrize("ad_mode,parts", [(1, 0), (0, 0), (1, 2)])
+def test_high_k_matrix_sums(co, ad_mode, parts):
+    """K >= CO_SUMS_MATRIX_MIN_K: sums from the fp64 matrix instruction (one fma
+    chain per entry over the points in order) and the LDS Cholesky; K up to 16
+    (C3 shapes: depth <= 8, <= 63 nodes)."""
+    pop, _ = synth("C3", 128, 700)
+    assert pop["K_max"] >= 13
+    g, o = _fit_both(co, pop, 15, ad_mode=ad_mode, partitions=parts)
+    st, d = _report(g, o)
+    _say(f"high K: status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
+    assert np.mean(d <= 1e-9) >= 0.99
+    assert st >= 0.99
