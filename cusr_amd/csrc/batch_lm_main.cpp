@@ -3,6 +3,8 @@
 //
 //   batch_lm_ad <pop.bin> [out_dir] [--max-iter N] [--quiet] [--rev] [--mixed]
 //
+// Reads pop.bin v1 and the v2 extension (float64 payloads, shared target;
+// include/pop_format.h).
 // writes out_dir/{status.bin, c_final.bin, loss_init.bin, loss_final.bin}
 // (int32 / float32 blobs, batch_lm_ad.cu:526-536) and prints the completion
 // line the reference benchmark parses (cusr/benchmark/backends.py:745):
@@ -24,9 +26,13 @@ namespace {
 struct Pop {
     PopHeader h;
     std::vector<int32_t> nt, ci;
-    std::vector<float> nv, c_init, xs, ym;
+    std::vector<float> nv;
+    std::vector<double> c_init, xs, ym;   // promoted from float32 for v1 files
     std::vector<TreeMeta> metas;
 };
+
+// float32 (v1) or float64 (v2 with POP_FLAG_F64) payload array, as double
+bool read_payload(FILE *f, std::vector<double> &dst, size_t count, bool f64, const char *what);
 
 bool read_exact(FILE *f, void *dst, size_t bytes, const char *what) {
     if (bytes == 0) return true;
@@ -48,10 +54,17 @@ bool load_pop(const char *path, Pop &p) {
         fprintf(stderr, "load_pop_bin: bad magic 0x%08x\n", (unsigned)p.h.magic);
         ok = false;
     }
-    if (ok && p.h.version != POP_VERSION) {
-        fprintf(stderr, "load_pop_bin: version %d != %d\n", p.h.version, POP_VERSION);
+    if (ok && p.h.version != POP_VERSION && p.h.version != POP_VERSION_2) {
+        fprintf(stderr, "load_pop_bin: version %d is neither %d nor %d\n", p.h.version,
+                POP_VERSION, POP_VERSION_2);
         ok = false;
     }
+    const int flags = ok ? pop_flags(&p.h) : 0;
+    if (ok && (flags & ~(POP_FLAG_F64 | POP_FLAG_SHARED_Y))) {
+        fprintf(stderr, "load_pop_bin: unknown flags 0x%x\n", (unsigned)flags);
+        ok = false;
+    }
+    if (ok && p.h.version == POP_VERSION) p.h.reserved[0] = 0;
     if (ok && (p.h.M_prob < 0 || p.h.total_nodes < 0 || p.h.total_c < 0 || p.h.N < 0 ||
                p.h.n_vars < 0)) {
         fprintf(stderr, "load_pop_bin: negative size in header\n");
@@ -60,17 +73,27 @@ bool load_pop(const char *path, Pop &p) {
     if (ok) {
         const size_t T = p.h.total_nodes, M = p.h.M_prob, C = p.h.total_c;
         const size_t N = p.h.N, D = p.h.n_vars;
+        const bool f64 = flags & POP_FLAG_F64;
+        const size_t rows = (flags & POP_FLAG_SHARED_Y) ? 1 : M;
         p.nt.resize(T); p.nv.resize(T); p.ci.resize(T); p.metas.resize(M);
-        p.c_init.resize(C); p.xs.resize(N * D); p.ym.resize(M * N);
         ok = read_exact(f, p.nt.data(), 4 * T, "nt") && read_exact(f, p.nv.data(), 4 * T, "nv") &&
              read_exact(f, p.ci.data(), 4 * T, "ci") &&
              read_exact(f, p.metas.data(), 16 * M, "metas") &&
-             read_exact(f, p.c_init.data(), 4 * C, "c_init") &&
-             read_exact(f, p.xs.data(), 4 * N * D, "xs") &&
-             read_exact(f, p.ym.data(), 4 * M * N, "ym");
+             read_payload(f, p.c_init, C, f64, "c_init") &&
+             read_payload(f, p.xs, N * D, f64, "xs") &&
+             read_payload(f, p.ym, rows * N, f64, "ym");
     }
     fclose(f);
     return ok;
+}
+
+bool read_payload(FILE *f, std::vector<double> &dst, size_t count, bool f64, const char *what) {
+    dst.resize(count);
+    if (f64) return read_exact(f, dst.data(), 8 * count, what);
+    std::vector<float> tmp(count);
+    if (!read_exact(f, tmp.data(), 4 * count, what)) return false;
+    for (size_t i = 0; i < count; i++) dst[i] = tmp[i];
+    return true;
 }
 
 bool write_blob(const std::string &path, const void *buf, size_t bytes) {
@@ -142,8 +165,6 @@ int main(int argc, char **argv) {
         return 1;
     }
     const size_t M = h.M_prob, C = h.total_c;
-    std::vector<double> c0(p.c_init.begin(), p.c_init.end());
-    std::vector<double> xs(p.xs.begin(), p.xs.end()), ym(p.ym.begin(), p.ym.end());
     std::vector<double> cf(C > 0 ? C : 1), li(M > 0 ? M : 1), lf(M > 0 ? M : 1);
     std::vector<int32_t> status(M > 0 ? M : 1), iters(M > 0 ? M : 1);
     CoOptions opt;
@@ -152,7 +173,7 @@ int main(int argc, char **argv) {
     opt.ad_mode = rev ? CO_AD_REVERSE : CO_AD_FORWARD;
     opt.precision = mixed ? CO_PREC_MIXED : CO_PREC_FP64;
     int rc = co_optimize_ex(handle, &opt, &h, p.nt.data(), p.nv.data(), p.ci.data(),
-                            p.metas.data(), c0.data(), xs.data(), ym.data(), cf.data(),
+                            p.metas.data(), p.c_init.data(), p.xs.data(), p.ym.data(), cf.data(),
                             status.data(), li.data(), lf.data(), iters.data());
     co_teardown(handle);
     if (rc != CO_OK) {

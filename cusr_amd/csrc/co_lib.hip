@@ -81,6 +81,7 @@ struct Ctx {
     bool bin_launched[CO_MAX_K + 1] = {};
     Plan plan = {};
     bool resident = false;
+    bool shared_y = false;   // the resident y is one row for every expression
     double last_kernel_ms = -1.0;
     double last_bin_ms[CO_MAX_K + 1] = {};
     size_t max_dyn_lds = 0;  // dynamic LDS one workgroup may use on this device
@@ -171,7 +172,8 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
         return CO_OK;
     }
     const int N = h->N, D = h->n_vars, C = h->total_c;
-    const size_t nX = (size_t)N * D, nY = (size_t)M * N;
+    const bool shared_y = (pop_flags(h) & POP_FLAG_SHARED_Y) != 0;
+    const size_t nX = (size_t)N * D, nY = shared_y ? (size_t)N : (size_t)M * N;
     const size_t esz = in32 ? 4 : 8;
     CO_GROW(ctx->prog, sizeof(uint64_t) * h->total_nodes);
     CO_GROW(ctx->desc, sizeof(ExprDesc) * M);
@@ -222,6 +224,7 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
         if (C) CO_HIP(hipMemcpyAsync(ctx->C0.p, c, 8 * (size_t)C, hipMemcpyHostToDevice, s));
     }
     CO_HIP(hipStreamSynchronize(s));
+    ctx->shared_y = shared_y;
     ctx->resident = true;
     return CO_OK;
 }
@@ -262,6 +265,7 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     fa.D = plan.D;
     fa.max_iter = opt.max_iter;
     fa.guard = opt.fp64_guard ? 1 : 0;
+    fa.shared_y = ctx->shared_y ? 1 : 0;
     fa.lm_order = opt.lm_order;
     fa.lambda0 = opt.lambda0;
     fa.xtol = opt.xtol;

@@ -726,7 +726,7 @@ struct FitArgs {
     const uint64_t *prog;
     const ExprDesc *desc;   // by launch position (offset to the bin's start)
     const double *X;        // [D][N]
-    const double *Y;        // [M][N]
+    const double *Y;        // [M][N], or [N] when shared_y
     const double *C0;       // [total_c]
     double *C;              // [total_c] out
     int32_t *status;        // [M] out
@@ -734,6 +734,7 @@ struct FitArgs {
     double *loss_final;     // [M] out
     int32_t *iters;         // [M] out
     int N, D, max_iter, guard, lm_order;
+    int shared_y;           // 1: Y is one row [N] shared by every expression
     double lambda0, xtol;
     int slots, tape;        // per-wave LDS rows of this launch ([row][P][64] each)
     int parts;              // point partitions per expression (1, 2 or 4)
@@ -767,7 +768,7 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     pa.prog = (ProgPtr)(fa.prog + e.prog_off);
     pa.n = e.n;
     pa.X = fa.X;
-    pa.y = fa.Y + (size_t)e.y_row * fa.N;
+    pa.y = fa.Y + (fa.shared_y ? (size_t)0 : (size_t)e.y_row * fa.N);
     pa.N = fa.N;
     pa.D = fa.D;
     pa.parts = fa.parts;

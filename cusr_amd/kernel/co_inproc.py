@@ -43,6 +43,7 @@ CO_MAX_NODES = 255
 CO_AD_FORWARD, CO_AD_REVERSE = 0, 1
 CO_PREC_FP64, CO_PREC_MIXED = 0, 1
 CO_ORDER_IMPROVE_FIRST, CO_ORDER_CONVERGE_FIRST = 0, 1
+POP_FLAG_F64, POP_FLAG_SHARED_Y = 1, 2
 # external statuses (include/pop_format.h, cusr/kernel/lm_core.cuh:46-56)
 STATUS_CONVERGED, STATUS_MAXITER, STATUS_FAIL_NAN, STATUS_K0_SKIP, STATUS_FAIL_CHOLESKY = 0, 1, 2, 3, 4
 
@@ -124,7 +125,28 @@ def _header(pop: dict) -> PopHeader:
     h.n_vars = int(pop["n_vars"])
     h.K_max = int(pop["K_max"])
     h.max_stack = int(pop["max_stack"])
+    if pop.get("shared_y"):
+        # pop.bin v2: ym is one row [N] shared by every expression
+        h.version = 2
+        h.reserved[0] = POP_FLAG_SHARED_Y
     return h
+
+
+def _sized(a, dtype, count: int, name: str):
+    """_arr with the element count the header implies; a short host array
+    would be read past its end by the library's copy."""
+    a, p = _arr(a, dtype)
+    if a.size != count:
+        raise ValueError(f"{name} has {a.size} elements, the header implies {count}")
+    return a, p
+
+
+def _counts(pop: dict):
+    """(c_init, xs, ym) element counts of a pop dict (ym is one row when the
+    target is shared)."""
+    M, N = int(pop["M"]), int(pop["N"])
+    rows = 1 if pop.get("shared_y") else M
+    return int(pop["total_c"]), N * int(pop["n_vars"]), rows * N
 
 
 def _metas(pop: dict):
@@ -252,9 +274,10 @@ class InProcessCO:
         nv, pnv = _arr(pop["nv"], np.float32)
         ci, pci = _arr(pop["ci"], np.int32)
         me, pme = _metas(pop)
-        c0, pc0 = _arr(pop["c_init"], np.float32)
-        xs, pxs = _arr(pop["xs"], np.float32)
-        ym, pym = _arr(pop["ym"], np.float32)
+        nc, nx, ny = _counts(pop)
+        c0, pc0 = _sized(pop["c_init"], np.float32, nc, "c_init")
+        xs, pxs = _sized(pop["xs"], np.float32, nx, "xs")
+        ym, pym = _sized(pop["ym"], np.float32, ny, "ym")
         c_final = np.zeros(max(C, 1), np.float32)
         status = np.zeros(max(M, 1), np.int32)
         loss_init = np.zeros(max(M, 1), np.float32)
@@ -287,9 +310,10 @@ class InProcessCO:
         nv, pnv = _arr(pop["nv"], np.float32)
         ci, pci = _arr(pop["ci"], np.int32)
         me, pme = _metas(pop)
-        c0, pc0 = _arr(pop["c_init"] if c_init is None else c_init, np.float64)
-        x, px = _arr(pop["xs"] if xs is None else xs, np.float64)
-        y, py = _arr(pop["ym"] if ym is None else ym, np.float64)
+        nc, nx, ny = _counts(pop)
+        c0, pc0 = _sized(pop["c_init"] if c_init is None else c_init, np.float64, nc, "c_init")
+        x, px = _sized(pop["xs"] if xs is None else xs, np.float64, nx, "xs")
+        y, py = _sized(pop["ym"] if ym is None else ym, np.float64, ny, "ym")
         out = {"c_final": np.zeros(max(C, 1)), "status": np.zeros(max(M, 1), np.int32),
                "loss_init": np.zeros(max(M, 1)), "loss_final": np.zeros(max(M, 1)),
                "iters": np.zeros(max(M, 1), np.int32)}
@@ -316,7 +340,7 @@ class InProcessCO:
         cc, pcc = _arr(pop["c_init"] if c is None else c, np.float64)
         if cc.size == 0:
             cc, pcc = _arr(np.zeros(1), np.float64)
-        x, px = _arr(pop["xs"] if xs is None else xs, np.float64)
+        x, px = _sized(pop["xs"] if xs is None else xs, np.float64, _counts(pop)[1], "xs")
         y = np.zeros((max(M, 1), max(N, 1)))
         rc = self._lib.co_eval_ex(self._handle, ctypes.byref(h), pnt, pnv, pci, pme, pcc, px,
                                   int(precision), y.ctypes.data_as(_VP))
@@ -332,11 +356,12 @@ class InProcessCO:
         nv, pnv = _arr(pop["nv"], np.float32)
         ci, pci = _arr(pop["ci"], np.int32)
         me, pme = _metas(pop)
-        c0, pc0 = _arr(pop["c_init"] if c_init is None else c_init, np.float64)
+        nc, nx, ny = _counts(pop)
+        c0, pc0 = _sized(pop["c_init"] if c_init is None else c_init, np.float64, nc, "c_init")
         if c0.size == 0:
             c0, pc0 = _arr(np.zeros(1), np.float64)
-        x, px = _arr(pop["xs"] if xs is None else xs, np.float64)
-        y, py = _arr(pop["ym"] if ym is None else ym, np.float64)
+        x, px = _sized(pop["xs"] if xs is None else xs, np.float64, nx, "xs")
+        y, py = _sized(pop["ym"] if ym is None else ym, np.float64, ny, "ym")
         rc = self._lib.co_upload_ex(self._handle, ctypes.byref(h), pnt, pnv, pci, pme, pc0, px, py)
         if rc != CO_OK:
             raise COError(rc, "co_upload_ex")

@@ -23,6 +23,19 @@
 #define POP_MAGIC   0x4D4C344D /* "M4LM" read as a little-endian uint32 */
 #define POP_VERSION 1
 
+/* pop.bin v2 (extension; v1 files are unchanged and still read): version 2
+ * and reserved[0] holds flags.
+ *   POP_FLAG_F64       c_init, xs and ym are stored as float64
+ *   POP_FLAG_SHARED_Y  ym holds one row [N] that every expression fits (the
+ *                      GP case, where the reference tiles one target M
+ *                      times, cusr/demonstrator/kernel_bridge.py:202)
+ * The library honours POP_FLAG_SHARED_Y in every entry point that takes ym
+ * (ym then points at N values); the array precision of an entry point is set
+ * by the entry point itself (co_optimize fp32, co_optimize_ex fp64). */
+#define POP_VERSION_2 2
+#define POP_FLAG_F64 1
+#define POP_FLAG_SHARED_Y 2
+
 typedef struct PopHeader {
     int32_t magic;       /* POP_MAGIC */
     int32_t version;     /* POP_VERSION */
@@ -42,6 +55,11 @@ typedef struct TreeMeta {
     int32_t c_offset;
     int32_t K;
 } TreeMeta;
+
+/* Flags of a header: reserved[0] of a v2 header; a v1 header has none. */
+static inline int32_t pop_flags(const PopHeader *h) {
+    return h->version == POP_VERSION_2 ? h->reserved[0] : 0;
+}
 
 #ifdef __cplusplus
 static_assert(sizeof(PopHeader) == 64, "PopHeader must be 64 bytes");

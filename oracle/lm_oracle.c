@@ -709,7 +709,8 @@ int orc_fit(const CoOptions *o, const PopHeader *h, const int32_t *nt, const flo
                   mt->n_nodes, mt->K};
         double li, lf;
         int32_t st, itn;
-        orc_fit_one(o, &t, h->N, h->n_vars, xs, ym + (size_t)m * h->N, c_init + mt->c_offset,
+        const double *yrow = (pop_flags(h) & POP_FLAG_SHARED_Y) ? ym : ym + (size_t)m * h->N;
+        orc_fit_one(o, &t, h->N, h->n_vars, xs, yrow, c_init + mt->c_offset,
                     c_final + mt->c_offset, &st, &li, &lf, &itn);
         status[m] = st;
         if (loss_init) loss_init[m] = li;

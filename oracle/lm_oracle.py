@@ -53,6 +53,8 @@ def _header(pop) -> PopHeader:
     h.M_prob, h.total_nodes, h.total_c = int(pop["M"]), int(pop["total_nodes"]), int(pop["total_c"])
     h.N, h.n_vars, h.K_max, h.max_stack = (int(pop["N"]), int(pop["n_vars"]),
                                           int(pop["K_max"]), int(pop["max_stack"]))
+    if pop.get("shared_y"):
+        h.version, h.reserved[0] = 2, 2     # pop.bin v2, POP_FLAG_SHARED_Y
     return h
 
 
@@ -159,7 +161,8 @@ def pass_sums(pop, m, c, xs=None, y=None, precision=CO_PREC_FP64, ad_mode=CO_AD_
     K = int(pop["metas"][m][3])
     cc, pcc = _p(c, np.float64)
     x, px = _p(pop["xs"] if xs is None else xs, np.float64)
-    yy, pyy = _p(pop["ym"][m] if y is None else y, np.float64)
+    yrow = pop["ym"][0] if pop.get("shared_y") else pop["ym"][m]
+    yy, pyy = _p(yrow if y is None else y, np.float64)
     loss = ctypes.c_double()
     jtj = np.zeros((max(K, 1), max(K, 1)))
     jtr = np.zeros(max(K, 1))

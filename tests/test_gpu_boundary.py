@@ -79,6 +79,8 @@ def test_errors_before_any_copy(co):
     pop, _ = synth("C1", 8, 16)
     bad = dict(pop)
     bad["total_c"] = int(pop["total_c"]) + 1
+    # host arrays sized to the header, so the library's own check is reached
+    bad["c_init"] = np.append(pop["c_init"], np.float32(0))
     with pytest.raises(ci.COError) as e:
         co.optimize_ex(bad, 5)
     assert e.value.code == ci.CO_ERR_SUM_C
@@ -126,3 +128,55 @@ def test_cli_blobs_and_completion_line(tmp_path, exe, order):
     bad = subprocess.run([str(KDIR / exe), str(tmp_path / "missing.bin")], capture_output=True,
                          timeout=60)
     assert bad.returncode == 1
+
+
+def _shared_target(M=96, N=256, seed=9):
+    pop, _ = synth("C1", M, N)
+    y = np.random.default_rng(seed).normal(size=N).astype(np.float32)
+    tiled = dict(pop)
+    tiled["ym"] = np.broadcast_to(y, (M, N)).copy()
+    return tiled
+
+
+@pytest.mark.parametrize("ad_mode", [0, 1])
+def test_shared_target_equals_tiled(co, ad_mode):
+    """pop.bin v2 shared target: one y row on the device gives the fit of the
+    target repeated per expression, bit for bit, and the oracle's."""
+    tiled = _shared_target()
+    shared = popio.share_y(tiled)
+    _say(f"shared target ad_mode={ad_mode}")
+    a = co.optimize_ex(tiled, 30, ad_mode=ad_mode)
+    b = co.optimize_ex(shared, 30, ad_mode=ad_mode)
+    for k in ("c_final", "status", "loss_init", "loss_final", "iters"):
+        assert np.array_equal(a[k], b[k], equal_nan=True), k
+    o = lm_oracle.fit(shared, max_iter=30, ad_mode=ad_mode)
+    assert np.mean(rel_diff(b["loss_final"], o["loss_final"]) <= 1e-9) >= 0.99
+    assert np.mean(b["status"] == o["status"]) >= 0.99
+    # fp32 reference ABI and the resident path read the shared row as well
+    r = co.optimize(shared, 30)
+    assert np.array_equal(r["status"], a["status"])
+    co.upload(shared)
+    res = co.fit_resident(30, ad_mode=ad_mode)
+    assert np.array_equal(res["c_final"], a["c_final"], equal_nan=True)
+    # a ym whose size disagrees with the flag is refused before any copy
+    with pytest.raises(ValueError, match="ym has"):
+        co.optimize_ex(dict(tiled, ym=shared["ym"]), 30)
+
+
+def test_cli_reads_v2_f64_shared(tmp_path):
+    """The CLI reads a v2 file with float64 payloads and a shared target and
+    fits what the library fits from the same fp64 arrays."""
+    shared = dict(popio.share_y(_shared_target(M=64, N=128)))
+    for k in ("c_init", "xs", "ym"):
+        shared[k] = np.asarray(shared[k], np.float64) * (1 + 2.0 ** -30)
+    path = tmp_path / "pop.bin"
+    popio.save_pop_bin(shared, path, f64=True)
+    _say("cli batch_lm_ad v2")
+    r = subprocess.run([str(KDIR / "batch_lm_ad"), str(path), str(tmp_path), "--max-iter", "20"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    status = np.fromfile(tmp_path / "status.bin", np.int32)
+    c_final = np.fromfile(tmp_path / "c_final.bin", np.float32)
+    o = lm_oracle.fit(shared, max_iter=20)
+    assert np.mean(status == o["status"]) >= 0.99
+    assert np.mean(c_final == o["c_final"].astype(np.float32)) >= 0.99
