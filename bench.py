@@ -1,7 +1,7 @@
 """Benchmark of the batched LM fitter.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-cpu]
-                    [--rounds R] [--copy-calibration]
+                    [--rounds R] [--tiled] [--copy-calibration]
 
 Default (the headline metric): one step = one full LM fit (all iterations,
 on-device accept/reject) of the synthetic C2 population: 16,384 seeded
@@ -12,7 +12,8 @@ constants. Prints one JSON line. --config C1/C3/C4 measure the other resident
 configurations the same way; --config C5 runs the GP inner-solver shape: R
 rounds of fresh 65,536-expression populations (generated untimed), each timed
 end to end from host buffers (upload, 10 mixed-precision iterations,
-read-back), the per-round latency being the step.
+read-back), the per-round latency being the step; the round's one target goes
+over as a shared row (pop.bin v2), or tiled per expression with --tiled.
 
 roofline: the dominant launch is the fit kernel of the K bin that runs
 longest; its algorithmic HBM bytes (cusr_amd/benchmark/accounting.py: per LM
@@ -190,10 +191,16 @@ def run_resident(args, cfg, co, pop):
 
 
 def run_rounds(args, cfg, co, gen):
-    """C5: fresh populations per round, each timed from host buffers."""
+    """C5: fresh populations per round, each timed from host buffers. The
+    round's one target goes over as the shared row of pop.bin v2 unless
+    --tiled sends it once per expression, as the reference does."""
+    from cusr_amd.benchmark import popio
+
     lat, fits, rounds, last = [], 0, [], None
     for r in range(args.rounds):
         pop = gen(r)
+        if not args.tiled:
+            pop = popio.share_y(pop)
         if r == 0:
             co.optimize_ex(pop, 0, precision=cfg.precision)     # first-use costs, untimed
         t0 = time.perf_counter()
@@ -211,7 +218,8 @@ def run_rounds(args, cfg, co, gen):
     pop, res, bins = last
     roof = roofline(pop, cfg, res["iters"], bins, lambda k: f"lm_fit_kernel<{k}, float, 0>")
     fit = {"rounds": rounds, "mean_round_ms": float(np.mean(lat)),
-           "p50_round_ms": float(np.median(lat))}
+           "p50_round_ms": float(np.median(lat)),
+           "target": "tiled [M][N]" if args.tiled else "shared row [N] (pop.bin v2)"}
     return value, float(np.mean(lat)), roof, fit, pop
 
 
@@ -227,6 +235,8 @@ def main():
                     help="override the configuration's AD mode (0 forward, 1 reverse)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip the end-to-end fit from host buffers (profiling runs)")
+    ap.add_argument("--tiled", action="store_true",
+                    help="C5: send the target tiled per expression, as the reference does")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one copy kernel of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()

@@ -82,10 +82,13 @@ struct Ctx {
     Plan plan = {};
     bool resident = false;
     bool shared_y = false;   // the resident y is one row for every expression
+    bool on_data = false;    // the resident population fits the uploaded data set
+    int data_N = -1, data_D = 0;  // shape of the uploaded data set (-1: none)
     double last_kernel_ms = -1.0;
     double last_bin_ms[CO_MAX_K + 1] = {};
     size_t max_dyn_lds = 0;  // dynamic LDS one workgroup may use on this device
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
+    DevBuf data_X, data_Y;   // co_data_upload: X [D][N] column-major, y [N]
     std::vector<uint64_t> h_prog;
     std::vector<ExprDesc> h_desc;
     std::vector<double> h_c, h_li, h_lf;
@@ -156,9 +159,11 @@ size_t fit_lds_bytes(bool mixed, bool rev, int K, int D, int slots, int tape) {
 
 // Check, decode and upload one population into the context (fp32 or fp64
 // host inputs); the population stays resident until the next upload.
+// With on_data, xs and ym are unused: the population fits the data set of
+// co_data_upload, whose shape must match the header's.
 int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const float *nv,
                       const int32_t *ci, const TreeMeta *metas, const void *c, const void *xs,
-                      const void *ym, bool in32) {
+                      const void *ym, bool in32, bool on_data = false) {
     CO_HIP(hipSetDevice(ctx->device));
     ctx->resident = false;
     const int M = h->M_prob;
@@ -167,13 +172,18 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
     int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
                                ctx->h_desc.data(), nullptr, nullptr, &ctx->plan);
     if (rc != CO_OK) return rc;
+    if (on_data && (ctx->data_N < 0 || h->N != ctx->data_N || h->n_vars != ctx->data_D))
+        return CO_ERR_DATA;
+    ctx->on_data = on_data;
     if (M == 0) {
         ctx->resident = true;
         return CO_OK;
     }
     const int N = h->N, D = h->n_vars, C = h->total_c;
-    const bool shared_y = (pop_flags(h) & POP_FLAG_SHARED_Y) != 0;
-    const size_t nX = (size_t)N * D, nY = shared_y ? (size_t)N : (size_t)M * N;
+    const bool shared_y = on_data || (pop_flags(h) & POP_FLAG_SHARED_Y) != 0;
+    // the data set's X and y stay in their own buffers
+    const size_t nX = on_data ? 0 : (size_t)N * D;
+    const size_t nY = on_data ? 0 : shared_y ? (size_t)N : (size_t)M * N;
     const size_t esz = in32 ? 4 : 8;
     CO_GROW(ctx->prog, sizeof(uint64_t) * h->total_nodes);
     CO_GROW(ctx->desc, sizeof(ExprDesc) * M);
@@ -253,8 +263,8 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     FitArgs fa;
     fa.prog = ptr<uint64_t>(ctx->prog);
     fa.desc = ptr<ExprDesc>(ctx->desc);
-    fa.X = ptr<double>(ctx->X);
-    fa.Y = ptr<double>(ctx->Y);
+    fa.X = ptr<double>(ctx->on_data ? ctx->data_X : ctx->X);
+    fa.Y = ptr<double>(ctx->on_data ? ctx->data_Y : ctx->Y);
     fa.C0 = ptr<double>(ctx->C0);
     fa.C = ptr<double>(ctx->C);
     fa.status = ptr<int32_t>(ctx->status);
@@ -342,14 +352,14 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
 int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t *nt,
                const float *nv, const int32_t *ci, const TreeMeta *metas, const void *c,
                const void *xs, const void *ym, bool in32, double *c_out, int32_t *status_out,
-               double *li_out, double *lf_out, int32_t *iters_out) {
+               double *li_out, double *lf_out, int32_t *iters_out, bool on_data = false) {
     const double t0 = now_ms();
     if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
     if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
     if (opt.max_iter < 0) return CO_ERR_NULLARG;
     if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
         return CO_ERR_NULLARG;
-    int rc = upload_population(ctx, h, nt, nv, ci, metas, c, xs, ym, in32);
+    int rc = upload_population(ctx, h, nt, nv, ci, metas, c, xs, ym, in32, on_data);
     if (rc != CO_OK) return rc;
     const double t1 = now_ms();
     rc = run_fit(ctx, opt, c_out, status_out, li_out, lf_out, iters_out);
@@ -446,6 +456,45 @@ extern "C" int co_optimize_ex(void *handle, const CoOptions *opt, const PopHeade
     if (opt->struct_size != (int32_t)sizeof(CoOptions)) return CO_ERR_NULLARG;
     return fit_common((Ctx *)handle, *opt, h, nt, nv, ci, metas, c, xs, ym, false, c_final_out,
                       status_out, loss_init_out, loss_final_out, iters_out);
+}
+
+extern "C" int co_data_upload(void *handle, int N, int n_vars, const double *xs,
+                              const double *y) {
+    if (!handle || N < 0 || n_vars < 0 || n_vars > CO_MAX_VARS) return CO_ERR_NULLARG;
+    if (N > 0 && (!y || (n_vars > 0 && !xs))) return CO_ERR_NULLARG;
+    Ctx *ctx = (Ctx *)handle;
+    CO_HIP(hipSetDevice(ctx->device));
+    ctx->data_N = -1;   // no data set until this upload completes
+    if (ctx->on_data) ctx->resident = false;
+    const size_t nX = (size_t)N * n_vars;
+    CO_GROW(ctx->data_X, sizeof(double) * nX);
+    CO_GROW(ctx->data_Y, sizeof(double) * N);
+    CO_GROW(ctx->stage, sizeof(double) * nX);
+    hipStream_t s = ctx->stream;
+    if (nX) {
+        CO_HIP(hipMemcpyAsync(ctx->stage.p, xs, 8 * nX, hipMemcpyHostToDevice, s));
+        transpose_x_kernel<double><<<blocks_for(nX, 256), 256, 0, s>>>(
+            ptr<double>(ctx->stage), ptr<double>(ctx->data_X), N, n_vars);
+        CO_HIP(hipGetLastError());
+    }
+    if (N) CO_HIP(hipMemcpyAsync(ctx->data_Y.p, y, 8 * (size_t)N, hipMemcpyHostToDevice, s));
+    CO_HIP(hipStreamSynchronize(s));
+    ctx->data_N = N;
+    ctx->data_D = n_vars;
+    return CO_OK;
+}
+
+extern "C" int co_optimize_data(void *handle, const CoOptions *opt, const PopHeader *h,
+                                const int32_t *nt, const float *nv, const int32_t *ci,
+                                const TreeMeta *metas, const double *c, double *c_final_out,
+                                int32_t *status_out, double *loss_init_out,
+                                double *loss_final_out, int32_t *iters_out) {
+    if (!handle || !opt || !h || !nt || !nv || !ci || !metas || !c || !c_final_out ||
+        !status_out)
+        return CO_ERR_NULLARG;
+    if (opt->struct_size != (int32_t)sizeof(CoOptions)) return CO_ERR_NULLARG;
+    return fit_common((Ctx *)handle, *opt, h, nt, nv, ci, metas, c, nullptr, nullptr, false,
+                      c_final_out, status_out, loss_init_out, loss_final_out, iters_out, true);
 }
 
 extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, const float *nv,
@@ -562,7 +611,8 @@ extern "C" void co_teardown(void *handle) {
     Ctx *ctx = (Ctx *)handle;
     (void)hipSetDevice(ctx->device);
     DevBuf *bufs[] = {&ctx->prog, &ctx->desc, &ctx->X, &ctx->Y, &ctx->C0, &ctx->C,
-                      &ctx->status, &ctx->li, &ctx->lf, &ctx->iters, &ctx->stage};
+                      &ctx->status, &ctx->li, &ctx->lf, &ctx->iters, &ctx->stage,
+                      &ctx->data_X, &ctx->data_Y};
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

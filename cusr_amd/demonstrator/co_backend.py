@@ -8,9 +8,10 @@ Every candidate shares one problem's (X, y). `native[j]` is candidate j's
 expression in prefix form, (nt, nv, ci) arrays of pop.bin node types, values
 and constant ranks (the reference extracts the same arrays from its EvoGP
 trees; that extraction belongs to the GP system, not to this library).
-`skeletons[j]` is only consulted for `n_constants` when it has one. The
-target goes to the device once, as the shared row of pop.bin v2, where the
-reference tiles it per candidate (kernel_bridge.py:202).
+`skeletons[j]` is only consulted for `n_constants` when it has one. (X, y)
+goes to the device once and stays there while later calls pass the same
+values; the reference re-sends X with y tiled per candidate on every call
+(kernel_bridge.py:200-206).
 
 Candidates the device cannot take (more than 16 constants, a value stack
 deeper than 16, more than 255 nodes, more than 8 variables) go to the
@@ -78,16 +79,18 @@ def fit_natives(skeletons, inits, natives, X, y, *, max_iter: int = 50, fallback
             nt, nv, ci = (np.asarray(a) for a in natives[j])
             c0 = np.asarray(inits[j], np.float64)
             trees.append((nt, nv, ci, c0))
-        # one shared target row (pop.bin v2) instead of y tiled per candidate
-        y32 = y.astype(np.float32)
-        pop = popio.build_pop(trees, X.astype(np.float32),
-                              np.broadcast_to(y32, (len(take), len(y32))))
-        pop["ym"], pop["shared_y"] = y32[None, :], True
+        # programs only: (X, y) stays on the device across calls while it is
+        # unchanged (co_data_upload), instead of X and y tiled per candidate
+        pop = popio.build_pop(trees, np.zeros((len(y), n_vars), np.float32),
+                              np.broadcast_to(np.float32(0), (len(take), len(y))))
         c0_64 = np.concatenate([np.asarray(inits[j], np.float64) for j in take]) \
             if pop["total_c"] else np.zeros(0)
         co = co_inproc.get_inproc_co(device_id, variant)
-        r = co.optimize_ex(pop, max_iter, ad_mode=ad_mode, precision=precision,
-                           c_init=c0_64, xs=X, ym=y[None, :])
+        with co.lock:
+            if not co.data_matches(X, y):
+                co.upload_data(X, y)
+            r = co.optimize_data(pop, max_iter, ad_mode=ad_mode, precision=precision,
+                                 c_init=c0_64)
         N = len(y)
         for slot, j in enumerate(take):
             _, _, c_off, K = (int(v) for v in pop["metas"][slot])

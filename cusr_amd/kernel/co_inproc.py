@@ -34,6 +34,7 @@ CO_ERR_SUM_NODES = -3
 CO_ERR_NULLARG = -4
 CO_ERR_OOM = -5
 CO_ERR_PROGRAM = -6
+CO_ERR_DATA = -7
 
 CO_MAX_K = 16
 CO_MAX_STACK = 16
@@ -56,6 +57,7 @@ _ERR_MSG = {
     CO_ERR_NULLARG: "null pointer / bad argument",
     CO_ERR_OOM: "out of memory growing a device buffer",
     CO_ERR_PROGRAM: "malformed expression (unknown op, bad node, rank or variable index)",
+    CO_ERR_DATA: "no data set uploaded, or the population's N / n_vars differ from it",
 }
 
 
@@ -101,7 +103,8 @@ _HERE = Path(__file__).resolve().parent
 # every extern "C" symbol of include/cusr_co.h
 EXPORTED = ("co_init", "co_optimize", "co_last_split", "co_teardown", "co_options_default",
             "co_optimize_ex", "co_eval_ex", "co_upload_ex", "co_fit_resident",
-            "co_last_kernel_ms", "co_last_bin_ms", "co_decode")
+            "co_last_kernel_ms", "co_last_bin_ms", "co_decode", "co_data_upload",
+            "co_optimize_data")
 
 
 def lib_path(variant: str = "ad") -> Path:
@@ -169,6 +172,10 @@ def _bind(lib) -> None:
     lib.co_upload_ex.restype = ctypes.c_int
     lib.co_fit_resident.argtypes = [_VP, ctypes.POINTER(CoOptions)] + [_VP] * 5
     lib.co_fit_resident.restype = ctypes.c_int
+    lib.co_data_upload.argtypes = [_VP, ctypes.c_int, ctypes.c_int, _VP, _VP]
+    lib.co_data_upload.restype = ctypes.c_int
+    lib.co_optimize_data.argtypes = [_VP, ctypes.POINTER(CoOptions), ctypes.POINTER(PopHeader)] + [_VP] * 10
+    lib.co_optimize_data.restype = ctypes.c_int
     lib.co_last_kernel_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
     lib.co_last_kernel_ms.restype = ctypes.c_int
     lib.co_last_bin_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
@@ -247,6 +254,11 @@ class InProcessCO:
         self._handle = _VP()
         self._torn = False
         self._resident = (0, 0)
+        self._data = None        # host copy of the uploaded data set (xs, y)
+        # calls on one handle are not thread-safe (the library's buffers are
+        # per handle); callers that pair upload_data with optimize_data from
+        # several threads hold this across the pair
+        self.lock = threading.RLock()
         rc = self._lib.co_init(self.device_id, ctypes.byref(self._handle))
         if rc != CO_OK:
             raise COError(rc, "co_init")
@@ -366,6 +378,64 @@ class InProcessCO:
         if rc != CO_OK:
             raise COError(rc, "co_upload_ex")
         self._resident = (int(pop["M"]), int(pop["total_c"]))
+
+    def upload_data(self, xs, y) -> None:
+        """Keep one data set (xs [N, D], target y [N], fp64) on the device for
+        optimize_data; it stays until the next upload_data or teardown."""
+        self._check()
+        x, px = _arr(xs, np.float64)
+        yy, py = _arr(y, np.float64)
+        if x.ndim != 2 or yy.size != x.shape[0]:
+            raise ValueError(f"xs must be [N, D] and y [N]; got {x.shape} and {yy.shape}")
+        self._data = None
+        rc = self._lib.co_data_upload(self._handle, int(x.shape[0]), int(x.shape[1]), px, py)
+        if rc != CO_OK:
+            raise COError(rc, "co_data_upload")
+        self._data = (x.copy(), yy.copy())
+
+    def data_matches(self, xs, y) -> bool:
+        """True when (xs, y) equal the uploaded data set value for value."""
+        if self._data is None:
+            return False
+        x0, y0 = self._data
+        xs, y = np.asarray(xs), np.asarray(y).ravel()
+        return (xs.shape == x0.shape and y.shape == y0.shape and np.array_equal(xs, x0)
+                and np.array_equal(y, y0))
+
+    def optimize_data(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
+                      precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
+                      fp64_guard: bool = True, partitions: int = 0, lm_order: int | None = None,
+                      c_init=None) -> dict:
+        """optimize_ex against the uploaded data set: pop's xs and ym are not
+        read or sent; only the programs and constants go to the device."""
+        self._check()
+        M, C = int(pop["M"]), int(pop["total_c"])
+        h = _header(pop)
+        o = default_options(ad_mode=int(ad_mode), precision=int(precision),
+                            max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
+                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions))
+        o.lm_order = self.default_order if lm_order is None else int(lm_order)
+        nt, pnt = _arr(pop["nt"], np.int32)
+        nv, pnv = _arr(pop["nv"], np.float32)
+        ci, pci = _arr(pop["ci"], np.int32)
+        me, pme = _metas(pop)
+        c0, pc0 = _sized(pop["c_init"] if c_init is None else c_init, np.float64, C, "c_init")
+        if c0.size == 0:
+            c0, pc0 = _arr(np.zeros(1), np.float64)
+        out = {"c_final": np.zeros(max(C, 1)), "status": np.zeros(max(M, 1), np.int32),
+               "loss_init": np.zeros(max(M, 1)), "loss_final": np.zeros(max(M, 1)),
+               "iters": np.zeros(max(M, 1), np.int32)}
+        rc = self._lib.co_optimize_data(
+            self._handle, ctypes.byref(o), ctypes.byref(h), pnt, pnv, pci, pme, pc0,
+            *(out[k].ctypes.data_as(_VP) for k in
+              ("c_final", "status", "loss_init", "loss_final", "iters")))
+        if rc != CO_OK:
+            raise COError(rc, "co_optimize_data")
+        self._resident = (M, C)
+        out["c_final"] = out["c_final"][:C]
+        for k in ("status", "loss_init", "loss_final", "iters"):
+            out[k] = out[k][:M]
+        return out
 
     def fit_resident(self, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                      precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,

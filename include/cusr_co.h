@@ -21,7 +21,8 @@
 extern "C" {
 #endif
 
-/* Return codes (cusr/kernel/co_lib.h:27-41, plus CO_ERR_PROGRAM). */
+/* Return codes (cusr/kernel/co_lib.h:27-41, plus CO_ERR_PROGRAM and
+ * CO_ERR_DATA). */
 #define CO_OK 0
 #define CO_ERR_BOUNDS 2      /* K_max, max_stack, n_vars or n_nodes beyond the device limits */
 #define CO_ERR_CUDA (-1)     /* HIP runtime error */
@@ -33,6 +34,8 @@ extern "C" {
                                 stack under/overflow, bad const rank or var index.
                                 Extension: the reference silently evaluates unknown
                                 ops to 0 (cusr/kernel/lm_core.cuh:82,100). */
+#define CO_ERR_DATA (-7)     /* co_optimize_data: no data set uploaded, or the header's
+                                N / n_vars differ from the uploaded one */
 
 /* Device limits of this build (the reference's are MAX_K=32, MAX_STACK=64,
  * cusr/kernel/ad_interp.cuh:34-39). Populations beyond them get CO_ERR_BOUNDS
@@ -170,6 +173,28 @@ int co_fit_resident(void *handle, const CoOptions *opt,
                     double *c_final_out, int32_t *status_out,
                     double *loss_init_out, double *loss_final_out,
                     int32_t *iters_out);
+
+/* Upload one data set, xs [N][n_vars] row-major and one target y [N], into
+ * buffers of the handle reserved for it. It stays on the device across calls
+ * until the next co_data_upload or co_teardown; the other entry points do not
+ * touch it. No counterpart in the reference: its GP bridge re-sends X and a
+ * y tiled to every expression with each population
+ * (cusr/demonstrator/kernel_bridge.py:200-206). Returns 0, CO_ERR_NULLARG
+ * (N < 0, n_vars outside 0..CO_MAX_VARS, null pointers with N > 0),
+ * CO_ERR_OOM or CO_ERR_CUDA. */
+int co_data_upload(void *handle, int N, int n_vars, const double *xs, const double *y);
+
+/* co_optimize_ex against the uploaded data set: every expression fits its
+ * target y; only the programs and c go to the device. header->N and
+ * header->n_vars must equal the data set's (else CO_ERR_DATA, before any
+ * copy); ym flags in the header are ignored. The population stays resident
+ * for co_fit_resident. Other codes and outputs as co_optimize_ex. */
+int co_optimize_data(void *handle, const CoOptions *opt, const PopHeader *header,
+                     const int32_t *nt, const float *nv, const int32_t *ci,
+                     const TreeMeta *metas, const double *c,
+                     double *c_final_out, int32_t *status_out,
+                     double *loss_init_out, double *loss_final_out,
+                     int32_t *iters_out);
 
 /* Device time of the last fit on the handle, from HIP events recorded on the
  * handle's stream before the first and after the last fit kernel. */

@@ -69,10 +69,17 @@ def eval_tree_arrays(nt, nv, ci, xs, c):
     return stack[0]
 
 
+def y_row(pop, m, ym=None):
+    """Target of expression m: row m of ym, or its one row when the
+    population has a shared target (pop.bin v2 flag)."""
+    ym = pop["ym"] if ym is None else ym
+    return ym[0] if pop.get("shared_y") and len(ym) == 1 else ym[m]
+
+
 def tree_view(pop, m):
     off, n, c_off, K = (int(v) for v in pop["metas"][m])
     sl = slice(off, off + n)
-    return pop["nt"][sl], pop["nv"][sl], pop["ci"][sl], pop["ym"][m], K
+    return pop["nt"][sl], pop["nv"][sl], pop["ci"][sl], y_row(pop, m), K
 
 
 def loss_pop(pop, c_final, xs=None, ym=None) -> np.ndarray:
@@ -85,6 +92,6 @@ def loss_pop(pop, c_final, xs=None, ym=None) -> np.ndarray:
         nt, nv, ci = pop["nt"][off:off + n], pop["nv"][off:off + n], pop["ci"][off:off + n]
         y = eval_tree_arrays(nt, nv, ci, xs, np.asarray(c_final[c_off:c_off + K], np.float64))
         if np.all(np.isfinite(y)):
-            r = y - np.asarray(ym[m], np.float64)
+            r = y - np.asarray(y_row(pop, m, ym), np.float64)
             out[m] = 0.5 * float(np.sum(r * r))
     return out

@@ -77,7 +77,7 @@ class ScipyPop:
                 continue
             status[m] = 2
             payloads.append((m, pop["nt"][off:off + n], pop["nv"][off:off + n],
-                             pop["ci"][off:off + n], xs, pop["ym"][m],
+                             pop["ci"][off:off + n], xs, interp.y_row(pop, m),
                              np.asarray(c_src[c_off:c_off + K], np.float64)))
         pool = self.pool() if payloads else None
         t_core = time.perf_counter()

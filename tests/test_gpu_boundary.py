@@ -180,3 +180,45 @@ def test_cli_reads_v2_f64_shared(tmp_path):
     o = lm_oracle.fit(shared, max_iter=20)
     assert np.mean(status == o["status"]) >= 0.99
     assert np.mean(c_final == o["c_final"].astype(np.float32)) >= 0.99
+
+
+@pytest.mark.parametrize("ad_mode,precision", [(0, 0), (1, 0), (0, 1)])
+def test_resident_data_equals_tiled(co, ad_mode, precision):
+    """co_data_upload + co_optimize_data: populations of different sizes fit
+    against one uploaded (X, y) give the fits of optimize_ex with y tiled,
+    bit for bit, also after other entry points used the handle in between."""
+    base = _shared_target(M=80, N=300, seed=12)
+    X, y = base["xs"].astype(np.float64), base["ym"][0].astype(np.float64)
+    _say(f"resident data ad_mode={ad_mode} precision={precision}")
+    co.upload_data(X, y)
+    for M, seed in ((80, None), (33, 44)):
+        pop = base if seed is None else dict(synth("C1", M, 300, seed=seed)[0])
+        pop = dict(pop, xs=base["xs"], ym=np.tile(base["ym"][0], (M, 1)))
+        want = co.optimize_ex(pop, 25, ad_mode=ad_mode, precision=precision)
+        co.evaluate(synth("C2", 16, 64)[0])      # other work on the handle in between
+        got = co.optimize_data(pop, 25, ad_mode=ad_mode, precision=precision)
+        for k in ("c_final", "status", "loss_init", "loss_final", "iters"):
+            assert np.array_equal(got[k], want[k], equal_nan=True), (M, k)
+        # the population stays resident on the data set for co_fit_resident
+        again = co.fit_resident(25, ad_mode=ad_mode, precision=precision)
+        assert np.array_equal(again["c_final"], want["c_final"], equal_nan=True)
+
+
+def test_resident_data_errors(co):
+    pop, _ = synth("C1", 8, 40)
+    fresh = ci.InProcessCO(device_id=0, variant="ad")
+    try:
+        with pytest.raises(ci.COError) as e:
+            fresh.optimize_data(pop, 5)                 # nothing uploaded
+        assert e.value.code == ci.CO_ERR_DATA
+        fresh.upload_data(pop["xs"], pop["ym"][0])
+        other, _ = synth("C1", 8, 41)
+        with pytest.raises(ci.COError) as e:
+            fresh.optimize_data(other, 5)               # N differs
+        assert e.value.code == ci.CO_ERR_DATA
+        r = fresh.optimize_data(pop, 5)
+        assert r["status"].shape == (8,)
+    finally:
+        fresh.teardown()
+    with pytest.raises(ValueError):
+        co.upload_data(np.zeros((10, 2)), np.zeros(9))

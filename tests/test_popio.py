@@ -107,3 +107,21 @@ def test_oracle_shared_target_equals_tiled(ad_mode):
     b = lm_oracle.fit(popio.share_y(tiled), max_iter=20, ad_mode=ad_mode)
     for k in ("c_final", "status", "loss_init", "loss_final", "iters"):
         assert np.array_equal(a[k], b[k], equal_nan=True), k
+
+
+def test_numpy_oracle_reads_shared_target():
+    """The numpy scorer and the scipy CPU path see the shared row as every
+    expression's target."""
+    from oracle import interp
+    from oracle.scipy_pop import ScipyPop
+
+    tiled = _shared_pop(M=12, N=40)
+    shared = popio.share_y(tiled)
+    c = np.asarray(tiled["c_init"], np.float64)
+    assert np.array_equal(interp.loss_pop(shared, c), interp.loss_pop(tiled, c))
+    sp = ScipyPop(nproc=2)
+    try:
+        a, b = sp.fit_pop(tiled), sp.fit_pop(shared)
+    finally:
+        sp.close()
+    assert np.array_equal(a["c_final"], b["c_final"]) and np.array_equal(a["status"], b["status"])
