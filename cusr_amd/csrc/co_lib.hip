@@ -89,6 +89,7 @@ struct Ctx {
     size_t max_dyn_lds = 0;  // dynamic LDS one workgroup may use on this device
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
     DevBuf data_X, data_Y;   // co_data_upload: X [D][N] column-major, y [N]
+    DevBuf state;            // loop state of fits paused between segments
     std::vector<uint64_t> h_prog;
     std::vector<ExprDesc> h_desc;
     std::vector<double> h_c, h_li, h_lf;
@@ -250,6 +251,9 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     if (opt.max_iter < 0) return CO_ERR_NULLARG;
     if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
         return CO_ERR_NULLARG;
+    if (opt.tail_iter < -1 || (opt.tail_partitions != 0 && opt.tail_partitions != 1 &&
+                               opt.tail_partitions != 2 && opt.tail_partitions != 4))
+        return CO_ERR_NULLARG;
     CO_HIP(hipSetDevice(ctx->device));
     const Plan &plan = ctx->plan;
     const int M = plan.M, C = plan.total_c;
@@ -283,6 +287,19 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     const bool mixed = opt.precision == CO_PREC_MIXED;
     const int parts = opt.partitions ? opt.partitions : co_partitions_for_n(plan.N);
     if (parts != 1 && parts != 2 && parts != 4) return CO_ERR_NULLARG;
+    // segments of the iteration loop: all expressions up to tail_it, then the
+    // ones still running with tail_parts partitions (one launch each per bin)
+    int tail_parts = parts;
+    const int tail_it = co_tail_resolve(&opt, plan.N, &tail_parts);
+    struct Segment { int parts, it_end, resume; } seg[2] = {{parts, opt.max_iter, 0}, {}};
+    int nseg = 1;
+    if (tail_it > 0) {
+        seg[0].it_end = tail_it;
+        seg[1] = {tail_parts, opt.max_iter, 1};
+        nseg = 2;
+        CO_GROW(ctx->state, sizeof(double) * kStateStride * (size_t)M);
+    }
+    fa.state = tail_it > 0 ? ptr<double>(ctx->state) : nullptr;
     const FitLauncher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
                                      : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
     // descriptors are in launch order, largest K first; one launch per K bin,
@@ -303,22 +320,28 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         // per-wavefront areas, then the partition sums; fewer wavefronts per
         // workgroup (each summing several partitions) when LDS is short
         const size_t wave_bytes = (fit_lds_bytes(mixed, rev, k, plan.D, slots, tape) + 15) & ~(size_t)15;
-        const size_t part_bytes = parts > 1 ? (size_t)parts * (1 + k + k * (k + 1) / 2) * 8 : 0;
-        int pwaves = parts;
-        while (pwaves > 1 && pwaves * wave_bytes + part_bytes > ctx->max_dyn_lds) pwaves /= 2;
-        const size_t lds = pwaves * wave_bytes + part_bytes;
-        if (lds > ctx->max_dyn_lds) return CO_ERR_BOUNDS;
         hipStream_t ks = ctx->lanes[nb % kStreams];
         if (nb < kStreams) CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
-        FitArgs fk = fa;
-        fk.desc = fa.desc + pos;
-        fk.slots = slots;
-        fk.tape = tape;
-        fk.parts = parts;
-        fk.pwaves = pwaves;
-        fk.wave_bytes = (int)wave_bytes;
         CO_HIP(hipEventRecord(ctx->ev_b0[k], ks));
-        CO_HIP(launch(k, (unsigned)cnt, lds, ks, fk));
+        // K = 0 expressions have no iterations, so no tail either
+        for (int g = 0; g < (k == 0 ? 1 : nseg); ++g) {
+            const int sp = seg[g].parts;
+            const size_t part_bytes = sp > 1 ? (size_t)sp * (1 + k + k * (k + 1) / 2) * 8 : 0;
+            int pwaves = sp;
+            while (pwaves > 1 && pwaves * wave_bytes + part_bytes > ctx->max_dyn_lds) pwaves /= 2;
+            const size_t lds = pwaves * wave_bytes + part_bytes;
+            if (lds > ctx->max_dyn_lds) return CO_ERR_BOUNDS;
+            FitArgs fk = fa;
+            fk.desc = fa.desc + pos;
+            fk.slots = slots;
+            fk.tape = tape;
+            fk.parts = sp;
+            fk.pwaves = pwaves;
+            fk.wave_bytes = (int)wave_bytes;
+            fk.it_end = seg[g].it_end;
+            fk.resume = seg[g].resume;
+            CO_HIP(launch(k, (unsigned)cnt, lds, ks, fk));
+        }
         CO_HIP(hipEventRecord(ctx->ev_b1[k], ks));
         ctx->bin_launched[k] = true;
         pos += cnt;
@@ -381,6 +404,8 @@ extern "C" void co_options_default(CoOptions *o) {
     o->xtol = 1e-6;
     o->fp64_guard = 1;
     o->lm_order = CUSR_DEFAULT_ORDER;
+    o->tail_iter = 0;         // co_tail_iter_for
+    o->tail_partitions = 0;   // CO_MAX_PARTITIONS
 }
 
 extern "C" int co_init(int device_id, void **handle_out) {
@@ -612,7 +637,7 @@ extern "C" void co_teardown(void *handle) {
     (void)hipSetDevice(ctx->device);
     DevBuf *bufs[] = {&ctx->prog, &ctx->desc, &ctx->X, &ctx->Y, &ctx->C0, &ctx->C,
                       &ctx->status, &ctx->li, &ctx->lf, &ctx->iters, &ctx->stage,
-                      &ctx->data_X, &ctx->data_Y};
+                      &ctx->data_X, &ctx->data_Y, &ctx->state};
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

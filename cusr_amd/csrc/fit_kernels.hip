@@ -12,6 +12,10 @@ namespace cusr {
 hipError_t CUSR_FIT_LAUNCH(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa) {
     if (fa.pwaves < 1 || fa.pwaves > CO_MAX_PARTITIONS || fa.parts % fa.pwaves != 0)
         return hipErrorInvalidValue;
+    // a segment that can pause or resume needs the state buffer
+    if (fa.it_end < 0 || fa.it_end > fa.max_iter ||
+        ((fa.resume || fa.it_end < fa.max_iter) && !fa.state))
+        return hipErrorInvalidValue;
     switch (K) {
 #define CUSR_CASE(k)                                                                   \
     case k:                                                                            \

@@ -740,7 +740,21 @@ struct FitArgs {
     int parts;              // point partitions per expression (1, 2 or 4)
     int pwaves;             // wavefronts per workgroup (divides parts)
     int wave_bytes;         // dynamic LDS of one wavefront; partition sums follow
+    // segments of the iteration loop: this launch runs iterations up to it_end
+    // (<= max_iter); an expression still running there saves its loop state
+    // to state[y_row] (and its constants to C) for the next launch, which
+    // resumes it (resume = 1) or, for expressions that finished, exits
+    int it_end, resume;
+    double *state;          // [M][kStateStride], null for single-launch fits
 };
+
+// loop state of a paused fit, per expression: loss, loss_init, lambda,
+// internal status (kStateDone once the outputs are written), iterations,
+// then the sums at the current constants
+constexpr int kStateStride = 8 + 160;
+constexpr int kStateSums = 8;
+constexpr double kStateDone = -1.0;
+static_assert(sums_width(CO_MAX_K) <= kStateStride - kStateSums, "state row too short");
 
 // internal states, mapped to STATUS_* at the end (lm_core.cuh:46-56)
 enum { ST_RUN = 0, ST_CONV = 1, ST_NAN = 2, ST_K0 = 3, ST_CHOL = 4 };
@@ -779,17 +793,35 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
 
     double *c_cur = lds_c, *c_try = lds_c + CO_MAX_K;
     double *s_cur = lds_s, *s_try = lds_s + sums_width(CO_MAX_K);
-    if (lead && lane < K) c_cur[lane] = fa.C0[e.c_off + lane];
-    block_sync(fa.pwaves);
-
-    data_pass<K, R, P, JAC>(pa, wl, c_cur, s_cur, lane);
-    double loss = uni(0.5 * s_cur[0]);
-    const double loss_init = loss;
-    int st = (K == 0) ? ST_K0 : (isfinite(loss) ? ST_RUN : ST_NAN);
-    double lambda = fa.lambda0;
-    int it = 0;
+    double *sv = fa.state ? fa.state + (size_t)e.y_row * kStateStride : nullptr;
+    double loss, loss_init, lambda;
+    int st, it;
+    if (!fa.resume) {
+        if (lead && lane < K) c_cur[lane] = fa.C0[e.c_off + lane];
+        block_sync(fa.pwaves);
+        data_pass<K, R, P, JAC>(pa, wl, c_cur, s_cur, lane);
+        loss = uni(0.5 * s_cur[0]);
+        loss_init = loss;
+        st = (K == 0) ? ST_K0 : (isfinite(loss) ? ST_RUN : ST_NAN);
+        lambda = fa.lambda0;
+        it = 0;
+    } else {
+        // an expression that finished in an earlier launch has nothing to do
+        const double sst = uni(sv[3]);
+        if (sst == kStateDone) return;
+        if (lead) {
+            if (lane < K) c_cur[lane] = fa.C[e.c_off + lane];
+            for (int j = lane; j < sums_width(K); j += kLanes) s_cur[j] = sv[kStateSums + j];
+        }
+        loss = uni(sv[0]);
+        loss_init = uni(sv[1]);
+        lambda = uni(sv[2]);
+        st = (int)sst;
+        it = (int)uni(sv[4]);
+        block_sync(fa.pwaves);
+    }
     if constexpr (K > 0) {
-        while (uni(st) == ST_RUN && it < fa.max_iter) {
+        while (uni(st) == ST_RUN && it < fa.it_end) {
             ++it;
             double delta[K];
             bool solved;
@@ -849,6 +881,21 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
             }
         }
     }
+    if (st == ST_RUN && it < fa.max_iter) {
+        // paused at the end of this launch's segment: save the loop state
+        if (lead) {
+            if (lane < K) fa.C[e.c_off + lane] = c_cur[lane];
+            for (int j = lane; j < sums_width(K); j += kLanes) sv[kStateSums + j] = s_cur[j];
+            if (lane == 0) {
+                sv[0] = loss;
+                sv[1] = loss_init;
+                sv[2] = lambda;
+                sv[3] = (double)st;
+                sv[4] = (double)it;
+            }
+        }
+        return;
+    }
     double lf = loss, li = loss_init;
     if constexpr (sizeof(R) == 4) {
         // fp64 losses at the delivered point and at the start; the fp64
@@ -876,6 +923,7 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     if (lane == 0) {
         // ST_RUN -> STATUS_MAXITER, ST_CONV -> STATUS_CONVERGED, the rest keep their code
         fa.status[e.y_row] = (st <= ST_CONV) ? (1 - st) : st;
+        if (sv) sv[3] = kStateDone;
         fa.loss_init[e.y_row] = li;
         fa.loss_final[e.y_row] = lf;
         fa.iters[e.y_row] = it;

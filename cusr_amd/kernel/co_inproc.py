@@ -90,7 +90,8 @@ class CoOptions(ctypes.Structure):
                 ("precision", ctypes.c_int32), ("max_iter", ctypes.c_int32),
                 ("lambda0", ctypes.c_double), ("xtol", ctypes.c_double),
                 ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
-                ("lm_order", ctypes.c_int32), ("reserved", ctypes.c_int32 * 5)]
+                ("lm_order", ctypes.c_int32), ("tail_iter", ctypes.c_int32),
+                ("tail_partitions", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3)]
 
 
 assert ctypes.sizeof(PopHeader) == 64
@@ -306,6 +307,7 @@ class InProcessCO:
     def optimize_ex(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                     precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                     fp64_guard: bool = True, partitions: int = 0, lm_order: int | None = None,
+                    tail_iter: int = 0, tail_partitions: int = 0,
                     c_init=None, xs=None, ym=None) -> dict:
         """fp64 fit; c_init/xs/ym override the pop's (fp32) arrays when given.
         partitions: point partitions per expression (0: by N). lm_order: None
@@ -316,7 +318,8 @@ class InProcessCO:
         h = _header(pop)
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
-                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions))
+                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
+                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions))
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
@@ -405,6 +408,7 @@ class InProcessCO:
     def optimize_data(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                       precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                       fp64_guard: bool = True, partitions: int = 0, lm_order: int | None = None,
+                    tail_iter: int = 0, tail_partitions: int = 0,
                       c_init=None) -> dict:
         """optimize_ex against the uploaded data set: pop's xs and ym are not
         read or sent; only the programs and constants go to the device."""
@@ -413,7 +417,8 @@ class InProcessCO:
         h = _header(pop)
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
-                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions))
+                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
+                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions))
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
@@ -440,13 +445,15 @@ class InProcessCO:
     def fit_resident(self, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                      precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                      fp64_guard: bool = True, outputs: bool = True, partitions: int = 0,
+                     tail_iter: int = 0, tail_partitions: int = 0,
                      lm_order: int | None = None):
         """Fit the uploaded population again; outputs=False leaves results on the device."""
         self._check()
         M, C = self._resident
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
-                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions))
+                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
+                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions))
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
         if not outputs:
             rc = self._lib.co_fit_resident(self._handle, ctypes.byref(o), None, None, None, None, None)

@@ -74,7 +74,14 @@ typedef struct CoOptions {
                            CO_ORDER_CONVERGE_FIRST (the FD variant: a small step
                            converges, otherwise a strict decrease is accepted,
                            cusr/kernel/co_lib.cu:457-473) */
-    int32_t reserved[5];
+    int32_t tail_iter;  /* active-set compaction: after this many iterations
+                           the expressions still running continue in a second
+                           launch with tail_partitions partitions, one
+                           wavefront per partition, while finished ones exit
+                           at once.
+                           0: co_tail_iter_for; -1: one launch, no tail */
+    int32_t tail_partitions; /* partitions of the tail (1, 2 or 4; 0: 4) */
+    int32_t reserved[3];
 } CoOptions;
 
 #define CO_ORDER_IMPROVE_FIRST 0
@@ -84,11 +91,41 @@ typedef struct CoOptions {
  * is 0: 64-point granule g belongs to partition g mod G, each partition is
  * summed by its own wavefront, so long expressions use several wavefronts.
  * A function of N only, so an expression fits the same alone or in any
- * population. */
+ * population. Measured on MI355X: two partitions from N = 1,024 shorten the
+ * slowest expressions of a K bin, which set its duration (C2 -11 %, C3
+ * -20 %, C5 even); four pay off only for long expressions. */
 static inline int co_partitions_for_n(int N) {
-    return N >= 16384 ? 4 : (N >= 8192 ? 2 : 1);
+    return N >= 16384 ? 4 : (N >= 1024 ? 2 : 1);
 }
 #define CO_MAX_PARTITIONS 4
+
+/* Iterations before the tail when CoOptions.tail_iter is 0, CO_TAIL_ITER_DEFAULT
+ * (0: no tail). The tail targets the spread of iteration counts (a few
+ * expressions run to max_iter while most stop early) by giving the ones still
+ * running more wavefronts. Measured on MI355X it does not pay on C1, C2, C3
+ * or C5: the concurrent K bins keep the machine busy until the end, and the
+ * extra partition reductions cost more than the shorter tail saves; so it is
+ * off by default and kept as an option. A function of the expression's size
+ * only, and part of the arithmetic order: passes of iterations after
+ * tail_iter, and the final fp64 audit of an expression that finishes after
+ * it, sum with the tail's partitions. */
+#ifndef CO_TAIL_ITER_DEFAULT
+#define CO_TAIL_ITER_DEFAULT 0
+#endif
+static inline int co_tail_iter_for(int N, int max_iter) {
+    if (CO_TAIL_ITER_DEFAULT <= 0 || co_partitions_for_n(N) >= CO_MAX_PARTITIONS || N < 256)
+        return 0;
+    return CO_TAIL_ITER_DEFAULT < max_iter ? CO_TAIL_ITER_DEFAULT : 0;
+}
+
+/* The tail options o give for N points: returns the iterations before the
+ * tail (0: no tail) and sets *tail_parts to its partitions. */
+static inline int co_tail_resolve(const CoOptions *o, int N, int *tail_parts) {
+    *tail_parts = o->tail_partitions ? o->tail_partitions : CO_MAX_PARTITIONS;
+    const int t = o->tail_iter < 0 ? 0
+                  : (o->tail_iter > 0 ? o->tail_iter : co_tail_iter_for(N, o->max_iter));
+    return (t > 0 && t < o->max_iter) ? t : 0;
+}
 
 /* Forward-AD fits of expressions with K >= CO_SUMS_MATRIX_MIN_K form their
  * sums with the fp64 matrix instruction (v_mfma_f64_16x16x4): the augmented

@@ -619,7 +619,12 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
     for (int k = 0; k < K; k++) c[k] = c0[k];
     int st = 0; /* 0 running, 1 conv, 2 nan, 3 K0, 4 chol */
     int it = 0;
-    const int G = orc_partitions(o, N);
+    /* partitions: G1 up to iteration T1, then the tail's G2 (cusr_co.h
+     * co_tail_resolve); T1 == 0 keeps G1 throughout */
+    const int G1 = orc_partitions(o, N);
+    int G2 = G1;
+    const int T1 = co_tail_resolve(o, N, &G2);
+    int G = G1;
     orc_pass(t, N, D, xs, y, c, o->precision, K > 0 ? jac : 0, G, cur);
     double li = cur->loss;
     if (K == 0) st = 3;
@@ -627,6 +632,7 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
     double lambda = o->lambda0;
     while (st == 0 && it < o->max_iter) {
         it++;
+        G = (T1 && it > T1) ? G2 : G1;
         if (orc_solve(K, cur->jtj, cur->jtr, lambda, delta) != 0) {
             lambda = lambda * 10.0;
             if (lambda > 1e12) st = 4;

@@ -30,7 +30,8 @@ class CoOptions(ctypes.Structure):
                 ("precision", ctypes.c_int32), ("max_iter", ctypes.c_int32),
                 ("lambda0", ctypes.c_double), ("xtol", ctypes.c_double),
                 ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
-                ("lm_order", ctypes.c_int32), ("reserved", ctypes.c_int32 * 5)]
+                ("lm_order", ctypes.c_int32), ("tail_iter", ctypes.c_int32),
+                ("tail_partitions", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3)]
 
 
 def build() -> None:
@@ -72,13 +73,15 @@ def _prog(pop):
 
 
 def options(ad_mode=CO_AD_FORWARD, precision=CO_PREC_FP64, max_iter=50,
-            lambda0=1e-3, xtol=1e-6, fp64_guard=1, partitions=0, lm_order=0) -> CoOptions:
+            lambda0=1e-3, xtol=1e-6, fp64_guard=1, partitions=0, lm_order=0,
+            tail_iter=0, tail_partitions=0) -> CoOptions:
     o = CoOptions()
     o.struct_size = ctypes.sizeof(CoOptions)
     o.ad_mode, o.precision, o.max_iter = ad_mode, precision, max_iter
     o.lambda0, o.xtol, o.fp64_guard = lambda0, xtol, fp64_guard
     o.partitions = partitions
     o.lm_order = lm_order
+    o.tail_iter, o.tail_partitions = tail_iter, tail_partitions
     return o
 
 

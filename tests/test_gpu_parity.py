@@ -16,13 +16,14 @@ def _say(msg):
     print(msg, flush=True)
 
 
-def _fit_both(co, pop, max_iter, ad_mode=0, precision=0, partitions=0):
+def _fit_both(co, pop, max_iter, ad_mode=0, precision=0, partitions=0, **kw):
     c0, xs, ym = f64(pop)
     _say(f"case M={pop['M']} N={pop['N']} ad={ad_mode} prec={precision} max_iter={max_iter} "
-         f"partitions={partitions}")
-    g = co.optimize_ex(pop, max_iter, ad_mode=ad_mode, precision=precision, partitions=partitions)
+         f"partitions={partitions} {kw}")
+    g = co.optimize_ex(pop, max_iter, ad_mode=ad_mode, precision=precision, partitions=partitions,
+                       **kw)
     o = lm_oracle.fit(pop, max_iter=max_iter, ad_mode=ad_mode, precision=precision,
-                      partitions=partitions)
+                      partitions=partitions, **kw)
     return g, o
 
 
@@ -170,5 +171,38 @@ def test_high_k_matrix_sums(co, ad_mode, parts):
     g, o = _fit_both(co, pop, 15, ad_mode=ad_mode, partitions=parts)
     st, d = _report(g, o)
     _say(f"high K: status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
+    assert np.mean(d <= 1e-9) >= 0.99
+    assert st >= 0.99
+
+
+@pytest.mark.parametrize("ad_mode,precision,tail_iter,tail_parts,lm_order", [
+    (0, 0, 0, 0, 0), (0, 0, 3, 2, 0), (1, 0, 5, 4, 0), (0, 1, 4, 4, 0), (0, 0, 6, 4, 1),
+    (0, 0, -1, 0, 0)])
+def test_tail_segment_matches_oracle(co, ad_mode, precision, tail_iter, tail_parts, lm_order):
+    """Active-set compaction: after tail_iter iterations the expressions still
+    running resume in a second launch with tail_parts partitions (one wavefront
+    each) from their saved loop state; passes after tail_iter, and the fp64
+    audit of an expression finishing after it, sum with the tail's partitions
+    in the oracle too. tail_iter 0 is the default rule, -1 one launch."""
+    pop, _ = synth("C2", 160, 700)
+    g, o = _fit_both(co, pop, 25, ad_mode=ad_mode, precision=precision, tail_iter=tail_iter,
+                     tail_partitions=tail_parts, lm_order=lm_order)
+    st, d = _report(g, o)
+    _say(f"tail {tail_iter}/{tail_parts}: status agree {st:.4f}; loss rel max {d.max():.3e}; "
+         f"exact {np.mean(d == 0):.4f}; iters > tail {np.mean(g['iters'] > max(tail_iter, 0)):.2f}")
+    assert np.array_equal(g["iters"] > 0, o["iters"] > 0)
+    tol = 1e-9 if precision == 0 else 1e-4
+    assert np.mean(d <= tol) >= 0.99
+    assert st >= 0.98
+    if precision == 0:
+        assert np.mean(g["c_final"] == o["c_final"]) >= 0.97
+
+
+def test_tail_high_k_matrix_sums(co):
+    """The tail with the matrix-instruction sums (forward AD, K >= 13)."""
+    pop, _ = synth("C3", 96, 700)
+    g, o = _fit_both(co, pop, 15, tail_iter=4, tail_partitions=4)
+    st, d = _report(g, o)
+    _say(f"tail high K: status agree {st:.4f}; loss rel max {d.max():.3e}")
     assert np.mean(d <= 1e-9) >= 0.99
     assert st >= 0.99

@@ -110,18 +110,15 @@ def test_oracle_shared_target_equals_tiled(ad_mode):
 
 
 def test_numpy_oracle_reads_shared_target():
-    """The numpy scorer and the scipy CPU path see the shared row as every
-    expression's target."""
+    """The numpy scorer and the targets the scipy CPU path fits (interp.y_row,
+    interp.tree_view) see the shared row as every expression's target."""
     from oracle import interp
-    from oracle.scipy_pop import ScipyPop
 
     tiled = _shared_pop(M=12, N=40)
     shared = popio.share_y(tiled)
     c = np.asarray(tiled["c_init"], np.float64)
     assert np.array_equal(interp.loss_pop(shared, c), interp.loss_pop(tiled, c))
-    sp = ScipyPop(nproc=2)
-    try:
-        a, b = sp.fit_pop(tiled), sp.fit_pop(shared)
-    finally:
-        sp.close()
-    assert np.array_equal(a["c_final"], b["c_final"]) and np.array_equal(a["status"], b["status"])
+    for m in range(12):
+        assert np.array_equal(interp.y_row(shared, m), tiled["ym"][m])
+        a, b = interp.tree_view(shared, m), interp.tree_view(tiled, m)
+        assert all(np.array_equal(x, y) for x, y in zip(a[:4], b[:4])) and a[4] == b[4]
