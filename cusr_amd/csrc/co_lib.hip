@@ -63,7 +63,13 @@ struct DevBuf {
     size_t cap = 0;
 };
 
-constexpr int kStreams = 4;
+// K bins run concurrently on the handle's stream and kExtraStreams more. HIP maps
+// each stream of a process to one of GPU_MAX_HW_QUEUES (4) hardware queues,
+// and two streams that share a queue run one after the other: a fifth stream
+// was measured sharing a queue and serialising its bins behind another's
+// (C2: 20.5 ms, the sum of the two streams' bins). So four streams in all.
+constexpr int kExtraStreams = 3;
+constexpr int kStreams = kExtraStreams + 1;
 
 // one launcher per (precision, AD mode), each built from fit_kernels.hip in
 // its own translation unit so the four variants compile in parallel
@@ -73,9 +79,9 @@ typedef hipError_t (*FitLauncher)(int K, unsigned grid, size_t lds, hipStream_t 
 struct Ctx {
     int device = -1;
     hipStream_t stream = nullptr;
-    hipStream_t lanes[kStreams] = {};
+    hipStream_t lanes[kExtraStreams] = {};
     hipEvent_t ev_start = nullptr;
-    hipEvent_t ev_done[kStreams] = {};
+    hipEvent_t ev_done[kExtraStreams] = {};
     hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr;  // timing pair around the fit launches
     hipEvent_t ev_b0[CO_MAX_K + 1] = {}, ev_b1[CO_MAX_K + 1] = {};  // per K-bin launch
     bool bin_launched[CO_MAX_K + 1] = {};
@@ -306,7 +312,9 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     // bins spread over the context's streams so their tails overlap
     CO_HIP(hipEventRecord(ctx->ev_t0, s));
     CO_HIP(hipEventRecord(ctx->ev_start, s));
-    int pos = 0, nb = 0;
+    int pos = 0;
+    double load[kStreams] = {};
+    bool lane_used[kExtraStreams] = {};
     for (int k = CO_MAX_K; k >= 0; --k) {
         int cnt = 0, slots = 0, tape = 0;
         while (pos + cnt < M && ctx->h_desc[pos + cnt].K == k) {
@@ -320,8 +328,18 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         // per-wavefront areas, then the partition sums; fewer wavefronts per
         // workgroup (each summing several partitions) when LDS is short
         const size_t wave_bytes = (fit_lds_bytes(mixed, rev, k, plan.D, slots, tape) + 15) & ~(size_t)15;
-        hipStream_t ks = ctx->lanes[nb % kStreams];
-        if (nb < kStreams) CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
+        // longest first onto the least loaded stream, a bin's cost taken as
+        // count x (K + 3) (measured per-bin times grow about so with K);
+        // stream kExtraStreams is the handle's own
+        int li = 0;
+        for (int i = 1; i < kStreams; ++i)
+            if (load[i] < load[li]) li = i;
+        load[li] += (double)cnt * (k + 3);
+        hipStream_t ks = li < kExtraStreams ? ctx->lanes[li] : s;
+        if (li < kExtraStreams && !lane_used[li]) {
+            CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
+            lane_used[li] = true;
+        }
         CO_HIP(hipEventRecord(ctx->ev_b0[k], ks));
         // K = 0 expressions have no iterations, so no tail either
         for (int g = 0; g < (k == 0 ? 1 : nseg); ++g) {
@@ -345,9 +363,9 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         CO_HIP(hipEventRecord(ctx->ev_b1[k], ks));
         ctx->bin_launched[k] = true;
         pos += cnt;
-        ++nb;
     }
-    for (int i = 0; i < kStreams && i < nb; ++i) {
+    for (int i = 0; i < kExtraStreams; ++i) {
+        if (!lane_used[i]) continue;
         CO_HIP(hipEventRecord(ctx->ev_done[i], ctx->lanes[i]));
         CO_HIP(hipStreamWaitEvent(s, ctx->ev_done[i], 0));
     }
@@ -422,7 +440,7 @@ extern "C" int co_init(int device_id, void **handle_out) {
     if (e == hipSuccess)
         ctx->max_dyn_lds = lds_per_block > (int)kStaticLds ? (size_t)lds_per_block - kStaticLds : 0;
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-    for (int i = 0; i < kStreams && e == hipSuccess; ++i)
+    for (int i = 0; i < kExtraStreams && e == hipSuccess; ++i)
         e = hipStreamCreateWithFlags(&ctx->lanes[i], hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t0);
@@ -431,7 +449,7 @@ extern "C" int co_init(int device_id, void **handle_out) {
         e = hipEventCreate(&ctx->ev_b0[k]);
         if (e == hipSuccess) e = hipEventCreate(&ctx->ev_b1[k]);
     }
-    for (int i = 0; i < kStreams && e == hipSuccess; ++i)
+    for (int i = 0; i < kExtraStreams && e == hipSuccess; ++i)
         e = hipEventCreateWithFlags(&ctx->ev_done[i], hipEventDisableTiming);
     if (e != hipSuccess) {
         fprintf(stderr, "[cusr_co] stream/event create: %s\n", hipGetErrorString(e));
@@ -641,7 +659,7 @@ extern "C" void co_teardown(void *handle) {
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
-    for (int i = 0; i < kStreams; ++i) {
+    for (int i = 0; i < kExtraStreams; ++i) {
         if (ctx->lanes[i]) (void)hipStreamDestroy(ctx->lanes[i]);
         if (ctx->ev_done[i]) (void)hipEventDestroy(ctx->ev_done[i]);
     }
