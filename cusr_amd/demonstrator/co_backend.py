@@ -22,6 +22,8 @@ status == CONVERGED (kernel_bridge.py:216).
 """
 from __future__ import annotations
 
+import hashlib
+from collections import OrderedDict
 from dataclasses import dataclass
 
 import numpy as np
@@ -110,29 +112,105 @@ def fit_natives(skeletons, inits, natives, X, y, *, max_iter: int = 50, fallback
     return results, stats
 
 
+def data_key(X, y) -> bytes:
+    """Digest of one problem's (X, y) as fp64 values."""
+    h = hashlib.blake2b(digest_size=16)
+    for a in (np.ascontiguousarray(X, np.float64), np.ascontiguousarray(y, np.float64).ravel()):
+        h.update(str(a.shape).encode())
+        h.update(a.tobytes())
+    return h.digest()
+
+
+def structure_key(nt, nv, ci) -> bytes:
+    """Digest of an expression's prefix arrays (its structure, constants aside)."""
+    h = hashlib.blake2b(digest_size=16)
+    for a, dt in ((nt, np.int32), (nv, np.float32), (ci, np.int32)):
+        h.update(np.ascontiguousarray(a, dt).tobytes())
+        h.update(b"|")
+    return h.digest()
+
+
+class WarmStartCache:
+    """Best constants found so far per (data set, expression structure), LRU
+    bounded. In a GP loop the same structure comes back generation after
+    generation (elites, unchanged copies, converging populations); starting it
+    from its best fitted constants instead of the inherited ones turns a fresh
+    LM fit into a few polishing iterations. This is the warm start the
+    reference plans (docs/kernel/OPTIMIZATION_BACKLOG.md:124-126,
+    docs/PAPER.md:24: 50 iterations down to 5-10), whose missing piece there
+    is writing fitted constants back for reuse."""
+
+    def __init__(self, capacity: int = 200_000):
+        self.capacity = int(capacity)
+        self._d: OrderedDict[bytes, tuple[np.ndarray, float]] = OrderedDict()
+
+    def __len__(self):
+        return len(self._d)
+
+    def get(self, dkey: bytes, skey: bytes):
+        v = self._d.get(dkey + skey)
+        if v is not None:
+            self._d.move_to_end(dkey + skey)
+        return v
+
+    def put(self, dkey: bytes, skey: bytes, constants, loss: float) -> None:
+        """Keep constants if they beat what is stored (finite losses only)."""
+        if not np.isfinite(loss):
+            return
+        key = dkey + skey
+        old = self._d.get(key)
+        if old is None or loss < old[1]:
+            self._d[key] = (np.array(constants, np.float64), float(loss))
+        self._d.move_to_end(key)
+        while len(self._d) > self.capacity:
+            self._d.popitem(last=False)
+
+
 class KernelLM:
-    """The fitter behind the demonstrator's ConstantOptimizer protocol."""
+    """The fitter behind the demonstrator's ConstantOptimizer protocol.
+
+    warm_start=True starts every candidate whose structure was fitted before
+    on the same (X, y) from the best constants found for it (WarmStartCache)
+    instead of its passed initial values; last_stats["n_warm"] counts them."""
 
     name = "cuda_kernel_lm"
 
     def __init__(self, max_iter: int = 50, fallback=None, variant: str = "ad", device_id: int = 0,
-                 ad_mode: int = 0, precision: int = 0):
+                 ad_mode: int = 0, precision: int = 0, warm_start: bool = False,
+                 cache_capacity: int = 200_000):
         self.max_iter = int(max_iter)
         self.fallback = fallback
         self.variant = variant
         self.device_id = int(device_id)
         self.ad_mode = int(ad_mode)
         self.precision = int(precision)
+        self.warm_start = bool(warm_start)
+        self.cache = WarmStartCache(cache_capacity) if warm_start else None
         self.last_stats: dict = {}
         self.cum_stats: dict = {}
 
     def fit_batch(self, skeletons, inits, X, y, *, max_iter=100, native=None) -> list[COResult]:
         if native is None:
             raise ValueError("KernelLM needs the prefix arrays of every candidate via native=")
+        n_warm = 0
+        keys = None
+        if self.cache is not None:
+            dkey = data_key(X, y)
+            keys = [structure_key(*nat) for nat in native]
+            inits = list(inits)
+            for j, sk in enumerate(keys):
+                hit = self.cache.get(dkey, sk)
+                if hit is not None and len(hit[0]) == len(np.atleast_1d(inits[j])):
+                    inits[j] = hit[0].copy()
+                    n_warm += 1
         results, stats = fit_natives(skeletons, inits, native, X, y, max_iter=self.max_iter,
                                      fallback=self.fallback, variant=self.variant,
                                      device_id=self.device_id, ad_mode=self.ad_mode,
                                      precision=self.precision)
+        if self.cache is not None:
+            for sk, r in zip(keys, results):
+                self.cache.put(dkey, sk, r.constants, r.final_loss)
+        stats["n_warm"] = n_warm
         self.last_stats = stats
         for k, v in stats.items():
             self.cum_stats[k] = self.cum_stats.get(k, 0) + v

@@ -74,7 +74,7 @@ def test_kernel_lm_fit_batch_aligned_with_fallback():
     res = lm.fit_batch(None, inits, X, y, native=nat)
     assert len(res) == 13 and res[5].n_iter == -7
     assert lm.last_stats == dict(n_total=13, n_kernel=12, n_fallback=1, n_overflow=1,
-                                 n_kmismatch=0)
+                                 n_kmismatch=0, n_warm=0)
     for j, r in enumerate(res):
         if j == 5:
             continue
@@ -106,3 +106,55 @@ def test_fit_natives_reuses_resident_data():
         got = np.concatenate([r.constants for r in res])
         assert np.array_equal(got, ref["c_final"])
         assert [r.n_iter for r in res] == ref["iters"].tolist()
+
+
+def test_warm_start_cache_keys_and_policy():
+    nat, _ = _candidates(3)
+    k0 = co_backend.structure_key(*nat[0])
+    assert k0 == co_backend.structure_key(*(np.array(a) for a in nat[0]))
+    assert k0 != co_backend.structure_key(*nat[1])
+    nt, nv, ci = nat[0]
+    assert k0 != co_backend.structure_key(nt, nv + np.float32(1), ci)   # another operator
+    X = np.arange(12.0).reshape(6, 2)
+    d = co_backend.data_key(X, np.ones(6))
+    assert d == co_backend.data_key(X.copy(), np.ones(6)) != co_backend.data_key(X, np.zeros(6))
+    cache = co_backend.WarmStartCache(capacity=2)
+    cache.put(d, k0, [1.0, 2.0], 0.5)
+    cache.put(d, k0, [9.0, 9.0], 0.7)            # worse: kept the better one
+    assert cache.get(d, k0)[0].tolist() == [1.0, 2.0]
+    cache.put(d, k0, [3.0, 4.0], 0.1)            # better: replaced
+    assert cache.get(d, k0)[0].tolist() == [3.0, 4.0]
+    cache.put(d, k0, [5.0, 6.0], float("inf"))   # non-finite: ignored
+    assert cache.get(d, k0)[1] == 0.1
+    k1, k2 = co_backend.structure_key(*nat[1]), co_backend.structure_key(*nat[2])
+    cache.put(d, k1, [1.0], 1.0)
+    cache.get(d, k0)                             # k0 most recently used
+    cache.put(d, k2, [1.0, 1.0], 1.0)            # evicts k1
+    assert len(cache) == 2 and cache.get(d, k1) is None and cache.get(d, k0) is not None
+    assert cache.get(co_backend.data_key(X, np.zeros(6)), k0) is None   # other data set
+
+
+@pytest.mark.gpu
+def test_kernel_lm_warm_start_reuses_fitted_constants():
+    """A second generation of the same structures starts from the constants
+    the first fitted: every candidate is warm, none gets worse, and the LM
+    loops are much shorter."""
+    rng = np.random.default_rng(7)
+    X = rng.uniform(-2, 2, size=(400, 2))
+    y = np.sin(0.7 * X[:, 1]) * 1.3 + 0.5 * X[:, 0] - 0.2 + 0.01 * rng.normal(size=400)
+    nat, inits = _candidates(30, seed=5)
+    lm = co_backend.KernelLM(max_iter=50, warm_start=True)
+    first = lm.fit_batch(None, inits, X, y, native=nat)
+    assert lm.last_stats["n_warm"] == 0
+    fresh = [rng.normal(size=len(c)) for c in inits]       # the next generation's inherited values
+    second = lm.fit_batch(None, fresh, X, y, native=nat)
+    assert lm.last_stats["n_warm"] == 30
+    it1 = np.mean([r.n_iter for r in first])
+    it2 = np.mean([r.n_iter for r in second])
+    print(f"warm start: mean iterations {it1:.1f} -> {it2:.1f}", flush=True)
+    assert it2 < 0.5 * it1
+    for a, b in zip(first, second):
+        assert b.final_loss <= a.final_loss * (1 + 1e-12) + 1e-300
+    # the cold path ignores the cache
+    cold = co_backend.KernelLM(max_iter=50).fit_batch(None, fresh, X, y, native=nat)
+    assert np.mean([r.n_iter for r in cold]) > it2
