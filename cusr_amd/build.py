@@ -55,33 +55,35 @@ def build(jobs: int | None = None, verbose: bool = False, defines=(), out: Path 
           cli: bool = True) -> Path:
     """Compile everything; `defines` adds -D flags (tuning variants) and `out`
     redirects the library (the CLI is only built for the default library)."""
-    BUILD.mkdir(exist_ok=True)
     extra = [f"-D{d}" for d in defines]
     lib = Path(out) if out is not None else LIB
+    # a redirected build keeps its objects apart, so builds can run side by side
+    bdir = BUILD if out is None else BUILD / Path(out).stem
+    bdir.mkdir(parents=True, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 4)
     compiles = []
     for rtype, ad, name in FIT_VARIANTS:
-        obj = BUILD / f"fit_{name}.o"
+        obj = bdir / f"fit_{name}.o"
         compiles.append([HIPCC, *DEVICE_FLAGS, *extra, "-x", "hip", f"-DCUSR_FIT_R={rtype}",
                          f"-DCUSR_FIT_AD={ad}", f"-DCUSR_FIT_LAUNCH={name}", "-c",
                          str(CSRC / "fit_kernels.hip"), "-o", str(obj)])
     compiles.append([HIPCC, *DEVICE_FLAGS, *extra, "-x", "hip", "-c", str(CSRC / "co_lib.hip"),
-                     "-o", str(BUILD / "co_lib.o")])
+                     "-o", str(bdir / "co_lib.o")])
     compiles.append([HIPCC, *DEVICE_FLAGS, "-x", "hip", "-c", str(CSRC / "program.cpp"),
-                     "-o", str(BUILD / "program.o")])
+                     "-o", str(bdir / "program.o")])
     default = out is None
     if default:
         compiles.append([HIPCC, *DEVICE_FLAGS, *extra, "-x", "hip", "-DCUSR_DEFAULT_ORDER=1", "-c",
-                         str(CSRC / "co_lib.hip"), "-o", str(BUILD / "co_lib_fd.o")])
+                         str(CSRC / "co_lib.hip"), "-o", str(bdir / "co_lib_fd.o")])
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         for err in ex.map(_run, compiles):
             if verbose and err.strip():
                 print(err, file=sys.stderr)
     objs = [str(c[c.index("-o") + 1]) for c in compiles]
     fit_objs = [o for o in objs if "co_lib" not in Path(o).name]
-    links = [(lib, fit_objs + [str(BUILD / "co_lib.o")])]
+    links = [(lib, fit_objs + [str(bdir / "co_lib.o")])]
     if default:
-        links.append((LIB_FD, fit_objs + [str(BUILD / "co_lib_fd.o")]))
+        links.append((LIB_FD, fit_objs + [str(bdir / "co_lib_fd.o")]))
     for target, lobjs in links:
         tmp = target.with_suffix(".so.tmp")
         _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *lobjs])

@@ -247,12 +247,6 @@ __device__ __forceinline__ void binary_p(int f, const R *l, const R *rv, bool wa
     }
 }
 
-// operators whose derivative can be an exact structural zero (select rule)
-__device__ __forceinline__ bool op_selects(int f) {
-    return f == OP_MAX || f == OP_MIN || f == OP_LT || f == OP_GT || f == OP_LE ||
-           f == OP_GE || f == OP_PDIV || f == OP_CEXP;
-}
-
 template <typename R>
 __device__ __forceinline__ R safe_mul(R a, R b) {
     return (a == R(0) || b == R(0)) ? R(0) : a * b;
@@ -273,33 +267,91 @@ __device__ __forceinline__ R &lds_at(R *base, int idx, int p, int lane) {
     return base[(idx * P + p) * kLanes + lane];
 }
 
+// In-place tangent scaling. ScaleAsm<R, P>::run<J>(t, d, z, m, sel) multiplies
+// the P tangents t[p] (entry J of point p) by d[p] when bit J of the
+// wave-uniform mask m is set; when sel is non-zero it then sets the lanes of
+// lane mask z[p] (the points whose partial is a flat branch) to exactly 0.
+// Test, branches, multiplies and zeroing sit in one asm block whose tangent
+// operands are read and written in the same registers: written as C++, the
+// conditional update is a merge of old and new values, which the register
+// allocator resolved with copies of the whole tangent array at every
+// interpreter step. The arithmetic is the same IEEE v_mul_f64 / v_mul_f32; a
+// zeroed lane is the select z ? 0 : t*d, done by masking exec to z around one
+// move and restoring it.
+#define CUSR_SKIP_HEAD "s_bitcmp1_b32 %[m], %[j]\n\ts_cbranch_scc0 .Lcusr_skip%=\n\t"
+#define CUSR_SEL_TEST "s_cmp_lg_u32 %[sel], 0\n\ts_cbranch_scc0 .Lcusr_skip%=\n\t"
+#define CUSR_SKIP_TAIL ".Lcusr_skip%=:"
+#define CUSR_MUL(op, i) op " %[t" #i "], %[t" #i "], %[d" #i "]\n\t"
+#define CUSR_ZERO(mov, i) \
+    "s_and_saveexec_b64 %[sv], %[z" #i "]\n\t" mov " %[t" #i "], 0\n\ts_mov_b64 exec, %[sv]\n\t"
+#define CUSR_T(i) [t##i] "+v"(t[i])
+#define CUSR_D(i) [d##i] "v"(d[i])
+#define CUSR_Z(i) [z##i] "s"(z[i])
+#define CUSR_IN [m] "s"(m), [sel] "s"(sel), [j] "n"(J)
+
+template <typename R, int P> struct ScaleAsm;
+#define CUSR_SCALE_ASM(R, MUL, MOV)                                                              \
+    template <> struct ScaleAsm<R, 1> {                                                          \
+        template <int J>                                                                         \
+        static __device__ __forceinline__ void run(R *t, const R *d, const uint64_t *z,          \
+                                                   uint32_t m, uint32_t sel) {                   \
+            uint64_t sv;                                                                         \
+            __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_SEL_TEST CUSR_ZERO(MOV, 0)     \
+                                 CUSR_SKIP_TAIL                                                  \
+                             : CUSR_T(0), [sv] "=&s"(sv)                                         \
+                             : CUSR_IN, CUSR_D(0), CUSR_Z(0));                                   \
+        }                                                                                        \
+    };                                                                                           \
+    template <> struct ScaleAsm<R, 2> {                                                          \
+        template <int J>                                                                         \
+        static __device__ __forceinline__ void run(R *t, const R *d, const uint64_t *z,          \
+                                                   uint32_t m, uint32_t sel) {                   \
+            uint64_t sv;                                                                         \
+            __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_MUL(MUL, 1) CUSR_SEL_TEST      \
+                                 CUSR_ZERO(MOV, 0) CUSR_ZERO(MOV, 1) CUSR_SKIP_TAIL              \
+                             : CUSR_T(0), CUSR_T(1), [sv] "=&s"(sv)                              \
+                             : CUSR_IN, CUSR_D(0), CUSR_D(1), CUSR_Z(0), CUSR_Z(1));             \
+        }                                                                                        \
+    };                                                                                           \
+    template <> struct ScaleAsm<R, 4> {                                                          \
+        template <int J>                                                                         \
+        static __device__ __forceinline__ void run(R *t, const R *d, const uint64_t *z,          \
+                                                   uint32_t m, uint32_t sel) {                   \
+            uint64_t sv;                                                                         \
+            __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_MUL(MUL, 1) CUSR_MUL(MUL, 2)   \
+                                 CUSR_MUL(MUL, 3) CUSR_SEL_TEST CUSR_ZERO(MOV, 0)                \
+                                     CUSR_ZERO(MOV, 1) CUSR_ZERO(MOV, 2) CUSR_ZERO(MOV, 3)       \
+                                         CUSR_SKIP_TAIL                                          \
+                             : CUSR_T(0), CUSR_T(1), CUSR_T(2), CUSR_T(3), [sv] "=&s"(sv)        \
+                             : CUSR_IN, CUSR_D(0), CUSR_D(1), CUSR_D(2), CUSR_D(3), CUSR_Z(0),   \
+                               CUSR_Z(1), CUSR_Z(2), CUSR_Z(3));                                 \
+        }                                                                                        \
+    };
+CUSR_SCALE_ASM(double, "v_mul_f64", "v_mov_b64")
+CUSR_SCALE_ASM(float, "v_mul_f32", "v_mov_b32")
+#undef CUSR_SCALE_ASM
+
+// Entries J..K-1 of the tangent rows, one asm block per entry.
+template <int K, int J, typename R, int P>
+__device__ __forceinline__ void scale_entries(R *T, const R *d, const uint64_t *z, uint32_t m,
+                                              uint32_t sel) {
+    if constexpr (J < K) {
+        R t[P];
+        CUSR_FOR_P t[p] = T[p * K + J];
+        ScaleAsm<R, P>::template run<J>(t, d, z, m, sel);
+        CUSR_FOR_P T[p * K + J] = t[p];
+        scale_entries<K, J + 1, R, P>(T, d, z, m, sel);
+    }
+}
+
 // T[p*K + j] *= d[p] for j in [lo, hi); with sel, zero where z[p] instead.
-// The j loop is unrolled over the compile-time K with one scalar branch per j
-// (the asm marker with j as operand keeps the branches distinct, so they are
-// not merged into one dynamically indexed access), and T stays in registers
-// with static indices.
 template <int K, typename R, int P>
 __device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, const bool *z,
                                             bool sel) {
-    if (hi <= lo) return;
     const uint32_t mask = ((1u << hi) - 1u) & ~((1u << lo) - 1u);
-    if (!sel) {
-#pragma unroll
-        for (int j = 0; j < K; ++j) {
-            if (mask & (1u << j)) {
-                __asm__ volatile("; scale %0" ::"n"(j));
-                CUSR_FOR_P T[p * K + j] = T[p * K + j] * d[p];
-            }
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < K; ++j) {
-            if (mask & (1u << j)) {
-                __asm__ volatile("; select %0" ::"n"(j));
-                CUSR_FOR_P T[p * K + j] = z[p] ? R(0) : T[p * K + j] * d[p];
-            }
-        }
-    }
+    uint64_t zm[P];
+    CUSR_FOR_P zm[p] = __builtin_amdgcn_ballot_w64(z[p]);
+    scale_entries<K, 0, R, P>(T, d, zm, mask, sel ? 1u : 0u);
 }
 
 // T[p*K + k] += v[p] for a wave-uniform k (same branch scheme as scale_range).
@@ -349,14 +401,7 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
             const int bk = ins_bkind(ins), bi = ins_bidx(ins);
             fetch<R, P>(bk, bi, acc, w, cs, lane, b);
             binary_p<R, P>(fid, a, b, JAC == 2 || mid < hi, o, d1, d2, z1, z2);
-            if constexpr (JAC == 1) {
-                // a constant operand k owns the range [k, k+1) and its tangent
-                // starts at 1, so one rule covers leaves and subtrees; the
-                // partials of ADD (and the left one of SUB) are exactly 1
-                const bool sel = op_selects(fid);
-                if (fid != OP_ADD && fid != OP_SUB) scale_range<K, R, P>(T, lo, mid, d1, z1, sel);
-                if (fid != OP_ADD) scale_range<K, R, P>(T, mid, hi, d2, z2, sel);
-            } else if constexpr (JAC == 2) {
+            if constexpr (JAC == 2) {
                 const int t = ins_tape(ins);
                 CUSR_FOR_P {
                     lds_at<R, P>(w.tape, t, p, lane) = d1[p];
@@ -365,12 +410,21 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
             }
         } else {
             unary_p<R, P>(fid, a, o, d1, z1);
-            if constexpr (JAC == 1) {
-                if (fid != OP_IDENT) scale_range<K, R, P>(T, lo, hi, d1, z1, fid == OP_CEXP);
-            } else if constexpr (JAC == 2) {
+            CUSR_FOR_P { d2[p] = d1[p]; z2[p] = z1[p]; }   // unused: scale_b is never set
+            if constexpr (JAC == 2) {
                 const int t = ins_tape(ins);
                 CUSR_FOR_P lds_at<R, P>(w.tape, t, p, lane) = d1[p];
             }
+        }
+        if constexpr (JAC == 1) {
+            // a constant operand k owns the range [k, k+1) and its tangent
+            // starts at 1, so one rule covers leaves and subtrees; the decode
+            // sets scale_a / scale_b only where a partial is not exactly 1
+            // (not for ADD, SUB's left operand or the identity) and the
+            // range is non-empty, and sel for the flat-branch operators
+            const bool sel = ins_sel(ins);
+            if (ins_scale_a(ins)) scale_range<K, R, P>(T, lo, mid, d1, z1, sel);
+            if (ins_scale_b(ins)) scale_range<K, R, P>(T, mid, hi, d2, z2, sel);
         }
         if (ins_toslot(ins)) {
             const int di = ins_didx(ins);
@@ -592,11 +646,11 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
         wave_sync_lds();
         return;
     }
-    // partition sums added in partition order by one lane
+    // partition sums added in partition order, sum q by lane q mod 64 of the
+    // first wavefront
     __syncthreads();
-    if (a.wave == 0 && lane == 0) {
-#pragma unroll
-        for (int q = 0; q < W; ++q) {
+    if (a.wave == 0) {
+        for (int q = lane; q < W; q += kLanes) {
             double v = a.part[q];
             for (int g = 1; g < a.parts; ++g) v = v + a.part[g * W + q];
             out[q] = v;

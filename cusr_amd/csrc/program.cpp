@@ -39,6 +39,38 @@ static bool binary_op(int f) {
     }
 }
 
+// Relative device cost of one instruction per interpreter pass (VALU
+// instructions per 64 lanes x 4 points, measured with SQ_INSTS_VALU on
+// single-operator expressions); only the launch order within a K bin uses it.
+static int op_cost(int f) {
+    switch (f) {
+    case OP_ADD: case OP_SUB: return 12;
+    case OP_MUL: return 23;
+    case OP_SQUARE: return 83;
+    case OP_DIV: case OP_LOOSE_DIV: case OP_PDIV: case OP_SQRT: case OP_LOOSE_SQRT: return 224;
+    case OP_EXP: case OP_CEXP: return 284;
+    case OP_SIN: case OP_COS: return 333;
+    case OP_LOG: case OP_LOOSE_LOG: case OP_PLOG: return 391;
+    case OP_TAN: case OP_POW: case OP_LOOSE_POW: return 450;
+    default: return 100;
+    }
+}
+
+// Forward-AD flags of an instruction (program.h bits 47..49): flat-branch
+// select rule, and which of its rank ranges get scaled. ADD's partials and
+// SUB's left one are exactly 1; the identity has no partial to apply.
+static uint64_t flag_bits(int f, bool bin, int lo, int mid, int hi) {
+    const bool sel = f == OP_MAX || f == OP_MIN || f == OP_LT || f == OP_GT || f == OP_LE ||
+                     f == OP_GE || f == OP_PDIV || f == OP_CEXP;
+    const bool unit_a = bin ? (f == OP_ADD || f == OP_SUB) : (f == OP_IDENT);
+    const bool unit_b = !bin || f == OP_ADD;
+    uint64_t w = 0;
+    if (sel) w |= (uint64_t)1 << 47;
+    if (!unit_a && mid > lo) w |= (uint64_t)1 << 48;
+    if (!unit_b && hi > mid) w |= (uint64_t)1 << 49;
+    return w;
+}
+
 // Integral node value in [0, limit) or -1.
 static int node_int(float v, int limit) {
     if (!(v >= 0.0f) || v >= (float)limit) return -1;
@@ -159,6 +191,7 @@ static int decode_tree(const int32_t *nt, const float *nv, const int32_t *ci, in
         if (bin) w |= (uint64_t)b.kind << 13 | (uint64_t)(b.idx & 15) << 15;
         w |= (uint64_t)lo << 24 | (uint64_t)mid << 29 | (uint64_t)hi << 34;
         w |= (uint64_t)tape << 39;
+        w |= flag_bits(f, bin, lo, mid, hi);
         tape += bin ? 2 : 1;
         out[nins] = w;
         s.opd.push_back({OPD_ACC, 0, nins});
@@ -276,10 +309,26 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
     if (stack) memcpy(stack, depth.data(), sizeof(int32_t) * M);
     if (n_ins) memcpy(n_ins, nins.data(), sizeof(int32_t) * M);
     if (descs) {
-        // launch position p runs expression ord[M-1-p]: largest K first, so the
-        // longest-running workgroups start earliest
+        // launch positions: K bins largest K first; within a bin the costliest
+        // programs first (fixed per-pass cost plus op_cost of each
+        // instruction), so the longest-running workgroups start earliest and
+        // a bin ends on cheap ones. Ties keep the order of ord reversed.
+        std::vector<int32_t> launch(M);
+        std::vector<int64_t> cost(M);
+        for (int m = 0; m < M; m++) {
+            int64_t c = 229;
+            for (int i = 0; i < nins[m]; i++) c += op_cost(ins_fid(prog[poff[m] + i]));
+            cost[m] = c;
+        }
+        for (int p = 0; p < M; p++) launch[p] = ord[M - 1 - p];
+        for (int k = CO_MAX_K, p0 = 0; k >= 0; --k) {
+            const int cnt = start[k + 1] - start[k];
+            std::stable_sort(launch.begin() + p0, launch.begin() + p0 + cnt,
+                             [&](int32_t a, int32_t b) { return cost[a] > cost[b]; });
+            p0 += cnt;
+        }
         for (int p = 0; p < M; p++) {
-            const int m = ord[M - 1 - p];
+            const int m = launch[p];
             ExprDesc &d = descs[p];
             d.prog_off = poff[m];
             d.n = nins[m];

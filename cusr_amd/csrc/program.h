@@ -27,6 +27,12 @@
 //   bits 34..38  hi      (unary: mid == hi)
 //   bits 39..46  tape    first reverse-AD tape slot of this instruction
 //                        (one slot per operand)
+//   bit  47      sel     the partials have flat branches: where a point's
+//                        partial is a structural zero its tangents become 0
+//   bit  48      scale_a forward AD scales ranks [lo, mid) by the partial of
+//                        the left / only operand (set when that range is
+//                        non-empty and the partial is not exactly 1)
+//   bit  49      scale_b forward AD scales ranks [mid, hi) by the right partial
 // Constants are ranked in prefix order (cusr/benchmark/popio.py:87-91), so the
 // constants of a subtree form one contiguous rank range; forward AD scales
 // only those ranks.
@@ -65,6 +71,9 @@ static inline __host__ __device__ int ins_lo(uint64_t w) { return (int)((w >> 24
 static inline __host__ __device__ int ins_mid(uint64_t w) { return (int)((w >> 29) & 31u); }
 static inline __host__ __device__ int ins_hi(uint64_t w) { return (int)((w >> 34) & 31u); }
 static inline __host__ __device__ int ins_tape(uint64_t w) { return (int)((w >> 39) & 255u); }
+static inline __host__ __device__ int ins_sel(uint64_t w) { return (int)((w >> 47) & 1u); }
+static inline __host__ __device__ int ins_scale_a(uint64_t w) { return (int)((w >> 48) & 1u); }
+static inline __host__ __device__ int ins_scale_b(uint64_t w) { return (int)((w >> 49) & 1u); }
 
 struct Plan {
     int32_t M, N, D, total_nodes, total_c;
