@@ -45,7 +45,7 @@ constexpr float kCexpCap32 = 485165184.0f;         // exp(20) rounded to float
 // the reverse-AD tape in LDS small.
 // Per-K tables for fp64 forward AD, K = 0..16 (overridable for tuning).
 #ifndef CUSR_P64_TABLE
-#define CUSR_P64_TABLE 4, 4, 4, 4, 4, 4, 4, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1
+#define CUSR_P64_TABLE 4, 4, 4, 4, 4, 4, 4, 4, 4, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
 #ifndef CUSR_P32_TABLE
 #define CUSR_P32_TABLE 4, 4, 4, 4, 4, 4, 4, 4, 4, 2, 2, 2, 2, 2, 2, 2, 2
@@ -325,6 +325,25 @@ template <typename R, int P> struct ScaleAsm;
                              : CUSR_T(0), CUSR_T(1), CUSR_T(2), CUSR_T(3), [sv] "=&s"(sv)        \
                              : CUSR_IN, CUSR_D(0), CUSR_D(1), CUSR_D(2), CUSR_D(3), CUSR_Z(0),   \
                                CUSR_Z(1), CUSR_Z(2), CUSR_Z(3));                                 \
+        }                                                                                        \
+    };                                                                                           \
+    template <> struct ScaleAsm<R, 8> {                                                          \
+        template <int J>                                                                         \
+        static __device__ __forceinline__ void run(R *t, const R *d, const uint64_t *z,          \
+                                                   uint32_t m, uint32_t sel) {                   \
+            uint64_t sv;                                                                         \
+            __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_MUL(MUL, 1) CUSR_MUL(MUL, 2)   \
+                                 CUSR_MUL(MUL, 3) CUSR_MUL(MUL, 4) CUSR_MUL(MUL, 5)              \
+                                     CUSR_MUL(MUL, 6) CUSR_MUL(MUL, 7) CUSR_SEL_TEST             \
+                                         CUSR_ZERO(MOV, 0) CUSR_ZERO(MOV, 1) CUSR_ZERO(MOV, 2)   \
+                                             CUSR_ZERO(MOV, 3) CUSR_ZERO(MOV, 4)                 \
+                                                 CUSR_ZERO(MOV, 5) CUSR_ZERO(MOV, 6)             \
+                                                     CUSR_ZERO(MOV, 7) CUSR_SKIP_TAIL            \
+                             : CUSR_T(0), CUSR_T(1), CUSR_T(2), CUSR_T(3), CUSR_T(4), CUSR_T(5), \
+                               CUSR_T(6), CUSR_T(7), [sv] "=&s"(sv)                              \
+                             : CUSR_IN, CUSR_D(0), CUSR_D(1), CUSR_D(2), CUSR_D(3), CUSR_D(4),   \
+                               CUSR_D(5), CUSR_D(6), CUSR_D(7), CUSR_Z(0), CUSR_Z(1), CUSR_Z(2), \
+                               CUSR_Z(3), CUSR_Z(4), CUSR_Z(5), CUSR_Z(6), CUSR_Z(7));           \
         }                                                                                        \
     };
 CUSR_SCALE_ASM(double, "v_mul_f64", "v_mov_b64")
