@@ -312,29 +312,40 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     // bins spread over the context's streams so their tails overlap
     CO_HIP(hipEventRecord(ctx->ev_t0, s));
     CO_HIP(hipEventRecord(ctx->ev_start, s));
-    int pos = 0;
+    // K bins: launch position, size and LDS rows, then a stream each,
+    // longest first onto the least loaded stream, a bin's cost taken as
+    // count x (K + 3) (measured per-bin times grow about so with K);
+    // stream kExtraStreams is the handle's own
+    struct Bin { int pos, cnt, slots, tape, stream; } bins[CO_MAX_K + 1];
     double load[kStreams] = {};
-    bool lane_used[kExtraStreams] = {};
-    for (int k = CO_MAX_K; k >= 0; --k) {
-        int cnt = 0, slots = 0, tape = 0;
-        while (pos + cnt < M && ctx->h_desc[pos + cnt].K == k) {
-            const ExprDesc &d = ctx->h_desc[pos + cnt];
-            if (d.slots > slots) slots = d.slots;
-            if (d.tape > tape) tape = d.tape;
-            ++cnt;
+    for (int k = CO_MAX_K, pos = 0; k >= 0; --k) {
+        Bin &b = bins[k];
+        b = {pos, 0, 0, 0, -1};
+        while (pos < M && ctx->h_desc[pos].K == k) {
+            const ExprDesc &d = ctx->h_desc[pos];
+            if (d.slots > b.slots) b.slots = d.slots;
+            if (d.tape > b.tape) b.tape = d.tape;
+            ++b.cnt;
+            ++pos;
         }
-        if (cnt == 0) continue;
-        if (!rev) tape = 0;
-        // per-wavefront areas, then the partition sums; fewer wavefronts per
-        // workgroup (each summing several partitions) when LDS is short
-        const size_t wave_bytes = (fit_lds_bytes(mixed, rev, k, plan.D, slots, tape) + 15) & ~(size_t)15;
-        // longest first onto the least loaded stream, a bin's cost taken as
-        // count x (K + 3) (measured per-bin times grow about so with K);
-        // stream kExtraStreams is the handle's own
+        if (b.cnt == 0) continue;
+        if (!rev) b.tape = 0;
         int li = 0;
         for (int i = 1; i < kStreams; ++i)
             if (load[i] < load[li]) li = i;
-        load[li] += (double)cnt * (k + 3);
+        load[li] += (double)b.cnt * (k + 3);
+        b.stream = li;
+    }
+    // launched largest K first (small-K bins first measured slower on C2)
+    bool lane_used[kExtraStreams] = {};
+    for (int k = CO_MAX_K; k >= 0; --k) {
+        const Bin &b = bins[k];
+        if (b.cnt == 0) continue;
+        const int cnt = b.cnt, li = b.stream;
+        // per-wavefront areas, then the partition sums; fewer wavefronts per
+        // workgroup (each summing several partitions) when LDS is short
+        const size_t wave_bytes =
+            (fit_lds_bytes(mixed, rev, k, plan.D, b.slots, b.tape) + 15) & ~(size_t)15;
         hipStream_t ks = li < kExtraStreams ? ctx->lanes[li] : s;
         if (li < kExtraStreams && !lane_used[li]) {
             CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
@@ -350,9 +361,9 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
             const size_t lds = pwaves * wave_bytes + part_bytes;
             if (lds > ctx->max_dyn_lds) return CO_ERR_BOUNDS;
             FitArgs fk = fa;
-            fk.desc = fa.desc + pos;
-            fk.slots = slots;
-            fk.tape = tape;
+            fk.desc = fa.desc + b.pos;
+            fk.slots = b.slots;
+            fk.tape = b.tape;
             fk.parts = sp;
             fk.pwaves = pwaves;
             fk.wave_bytes = (int)wave_bytes;
@@ -362,7 +373,6 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         }
         CO_HIP(hipEventRecord(ctx->ev_b1[k], ks));
         ctx->bin_launched[k] = true;
-        pos += cnt;
     }
     for (int i = 0; i < kExtraStreams; ++i) {
         if (!lane_used[i]) continue;
