@@ -19,9 +19,12 @@ roofline: the dominant launch is the fit kernel of the K bin that runs
 longest; its algorithmic HBM bytes (cusr_amd/benchmark/accounting.py: per LM
 iteration of each active expression two point-passes that each read y, X once
 per pass, the bytecode) over its duration from HIP events recorded around
-that launch on the stream it runs on. The same object carries the VALU figure
-(algorithmic flops over the same duration), the roof this kernel is actually
-under. traffic: measured HBM bytes of that launch, from the rocprofv3
+that launch on the stream it runs on. The same object carries the VALU figures,
+the roof this kernel is actually under: algorithmic flops over the same
+duration (a lower bound: a transcendental counts 2 flops), and, when the
+committed rocprofv3 counter summary (profiles/lm_fit_c2_valu.json) was taken on
+this workload, the measured VALU busy fraction of the whole fit and of the
+dominant kernel running alone. traffic: measured HBM bytes of that launch, from the rocprofv3
 FETCH_SIZE / WRITE_SIZE summary committed under profiles/, when it was taken
 on this workload. cpu_baseline: the reference CPU path (scipy LM per
 expression over a process pool) on a sample of the same population sized to
@@ -44,6 +47,8 @@ sys.path.insert(0, str(REPO))
 HBM_PEAK_GBS = 8000.0
 FP64_VECTOR_PEAK_TFLOPS = 78.6
 FP32_VECTOR_PEAK_TFLOPS = 157.3
+MI355X_SIMDS = 256 * 4          # CUs x SIMDs; a wave64 VALU op issues in 4 cycles
+MI355X_CLOCK_HZ = 2.4e9         # peak engine clock
 HEADLINE_METRIC = "expressions fitted/sec (16k exprs, K=1-8, N=1024, fp64) + achieved HBM GB/s"
 
 
@@ -114,6 +119,46 @@ def load_traffic(workload_key, kernel):
     return None
 
 
+def load_valu(workload_key):
+    """Per-kernel SQ counters (SQ_ACTIVE_INST_VALU: quad-cycles of VALU issue,
+    summed over waves) from the committed rocprofv3 --pmc summary, when that
+    summary was taken on this workload."""
+    p = REPO / "profiles" / "lm_fit_c2_valu.json"
+    if not p.exists():
+        return None
+    d = json.loads(p.read_text())
+    if d.get("workload_key") != workload_key:
+        return None
+    return d["kernels"]
+
+
+def valu_issue(workload_key, kname_of, bins, device_ms, kdom):
+    """Measured VALU busy fraction: SQ_ACTIVE_INST_VALU x 4 cycles over the
+    machine's VALU cycles (1024 SIMDs at the 2.4 GHz peak clock, so a lower
+    bound) -- for the whole fit (all K bins over the fit's device time) and
+    for the dominant kernel running alone (its counter-run dispatch)."""
+    ctr = load_valu(workload_key)
+    if not ctr:
+        return None
+    cyc = 4.0 / (MI355X_SIMDS * MI355X_CLOCK_HZ)
+    tot, missing = 0.0, []
+    for k, v in enumerate(bins):
+        if v < 0:
+            continue
+        e = next((e for n, e in ctr.items() if kname_of(k) in n), None)
+        if e is None:
+            missing.append(k)
+            continue
+        tot += e["SQ_ACTIVE_INST_VALU"]
+    if missing:
+        return None
+    dom = next(e for n, e in ctr.items() if kname_of(kdom) in n)
+    return {"whole_fit_frac": tot * cyc / (device_ms / 1e3),
+            "dominant_alone_frac": dom["SQ_ACTIVE_INST_VALU"] * cyc / (dom["alone_ms"] / 1e3),
+            "dominant_alone_ms": dom["alone_ms"], "clock_ghz": MI355X_CLOCK_HZ / 1e9,
+            "simds": MI355X_SIMDS, "source": "profiles/lm_fit_c2_valu.json"}
+
+
 def workload_text(cfg, pop):
     return (f"{cfg.name}: {pop['M']} expressions, depth<={cfg.depth}, <={cfg.max_nodes} nodes, "
             f"K {cfg.k_lo}-{cfg.k_hi}, D={cfg.D}, N={cfg.N}, {cfg.max_iter} LM iterations, "
@@ -121,8 +166,8 @@ def workload_text(cfg, pop):
             f"{'mixed fp32/fp64' if cfg.precision else 'fp64'}")
 
 
-def roofline(pop, cfg, iters, bins, kname_of):
-    """Dominant launch (longest K bin) against HBM, with its VALU figure."""
+def roofline(pop, cfg, iters, bins, kname_of, device_ms=None):
+    """Dominant launch (longest K bin) against HBM, with its VALU figures."""
     from cusr_amd.benchmark import accounting
 
     K = pop["metas"][:, 3]
@@ -134,12 +179,15 @@ def roofline(pop, cfg, iters, bins, kname_of):
     tflops = w["flops"] / dom_s / 1e12
     kname = kname_of(kdom)
     key = f"{cfg.name}:{pop['M']}x{pop['N']}:seed{cfg.seed}:it{cfg.max_iter}"
+    valu = {"achieved": tflops, "peak": vpeak, "unit": "TFLOP/s", "frac": tflops / vpeak,
+            "algorithmic_flops_per_launch": w["flops"]}
+    if device_ms:
+        valu["measured_issue"] = valu_issue(key, kname_of, bins, device_ms, kdom)
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(key, kname),
             "kernel": kname, "expressions_in_launch": int(np.sum(K == kdom)),
             "launch_ms": float(bins[kdom]), "algorithmic_bytes_per_launch": w["bytes"],
-            "valu": {"achieved": tflops, "peak": vpeak, "unit": "TFLOP/s",
-                     "frac": tflops / vpeak, "algorithmic_flops_per_launch": w["flops"]}}
+            "valu": valu}
 
 
 def run_resident(args, cfg, co, pop):
@@ -174,7 +222,7 @@ def run_resident(args, cfg, co, pop):
     bins = np.mean(np.asarray(bin_ms), axis=0)
     rname = "double" if cfg.precision == 0 else "float"
     roof = roofline(pop, cfg, res["iters"], bins,
-                    lambda k: f"lm_fit_kernel<{k}, {rname}, {cfg.ad_mode}>")
+                    lambda k: f"lm_fit_kernel<{k}, {rname}, {cfg.ad_mode}>", device_ms=kms)
     whole = accounting.algorithmic_work(pop, res["iters"], cfg.ad_mode)
     status_counts = np.bincount(res["status"], minlength=5).tolist()
     _say(f"{args.steps} steps: {ms_per_step:.2f} ms/step, device {kms:.2f} ms/fit, "

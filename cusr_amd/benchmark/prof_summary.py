@@ -2,12 +2,15 @@
 
     python -m cusr_amd.benchmark.prof_summary trace  <run_results.db> [--match lm_fit]
     python -m cusr_amd.benchmark.prof_summary pmc    <run_results.db> [--match lm_fit]
+    python -m cusr_amd.benchmark.prof_summary valu   <run_results.db> [--match lm_fit]
+           [--out JSON --workload-key KEY]
     python -m cusr_amd.benchmark.prof_summary traffic <fetch.db> <write.db> --kernel NAME
            --calib-fetch-bytes F --calib-write-bytes W [--out JSON --workload-key KEY]
 
 trace: per kernel, calls and average / min / max / total duration plus the
 register and grid figures of the dispatch. pmc: per kernel, the average of
-every counter per dispatch. traffic: HBM bytes per dispatch of each matching kernel from
+every counter per dispatch. valu: the same as JSON, with each kernel's
+dispatch duration (counter runs serialise dispatches). traffic: HBM bytes per dispatch of each matching kernel from
 a FETCH_SIZE run and a WRITE_SIZE run, each scaled by the ratio of the known
 bytes of the copy calibration kernel (bench.py --copy-calibration: the
 widen_kernel dispatch with the largest grid) to what the same counter read
@@ -71,6 +74,25 @@ def pmc(db, match=None):
     return "\n".join(out)
 
 
+def valu(db, match=None, workload_key=None):
+    """Per kernel: the average per dispatch of every collected counter and
+    the dispatch duration (counter runs serialise dispatches, so these are
+    the kernels running alone)."""
+    d = pmc_per_dispatch(db, match)
+    durs = collections.defaultdict(list)
+    for name, dur in _rows(db, "select name, duration from kernels"):
+        if name in d:
+            durs[name].append(dur / 1e6)
+    out = {"kernels": {}}
+    for name in sorted(d):
+        e = dict(d[name])
+        e["alone_ms"] = statistics.mean(durs[name]) if durs[name] else None
+        out["kernels"][name] = e
+    if workload_key:
+        out["workload_key"] = workload_key
+    return out
+
+
 def _calib(db, counter):
     """Counter value of the largest widen_kernel dispatch."""
     rows = _rows(db, "select dispatch_id, max(grid_size), sum(value) from counters_collection "
@@ -107,7 +129,7 @@ def traffic(fetch_db, write_db, kernel, calib_fetch, calib_write):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["trace", "pmc", "traffic"])
+    ap.add_argument("mode", choices=["trace", "pmc", "traffic", "valu"])
     ap.add_argument("dbs", nargs="+")
     ap.add_argument("--match", default=None)
     ap.add_argument("--kernel", default=None)
@@ -120,6 +142,12 @@ def main():
         print(trace(a.dbs[0], a.match))
     elif a.mode == "pmc":
         print(pmc(a.dbs[0], a.match))
+    elif a.mode == "valu":
+        t = valu(a.dbs[0], a.match, a.workload_key)
+        print(json.dumps(t, indent=1))
+        if a.out:
+            with open(a.out, "w") as fh:
+                json.dump(t, fh, indent=1)
     else:
         t = traffic(a.dbs[0], a.dbs[1], a.kernel, a.calib_fetch_bytes, a.calib_write_bytes)
         if a.workload_key:
