@@ -421,18 +421,15 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
             fetch<R, P>(bk, bi, acc, w, cs, lane, b);
             binary_p<R, P>(fid, a, b, JAC == 2 || mid < hi, o, d1, d2, z1, z2);
             if constexpr (JAC == 2) {
-                const int t = ins_tape(ins);
-                CUSR_FOR_P {
-                    lds_at<R, P>(w.tape, t, p, lane) = d1[p];
-                    lds_at<R, P>(w.tape, t + 1, p, lane) = d2[p];
-                }
+                const int t = ins_tape(ins), ta = ins_tape_a(ins);
+                if (ta) CUSR_FOR_P lds_at<R, P>(w.tape, t, p, lane) = d1[p];
+                if (ins_tape_b(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, t + ta, p, lane) = d2[p];
             }
         } else {
             unary_p<R, P>(fid, a, o, d1, z1);
             CUSR_FOR_P { d2[p] = d1[p]; z2[p] = z1[p]; }   // unused: scale_b is never set
             if constexpr (JAC == 2) {
-                const int t = ins_tape(ins);
-                CUSR_FOR_P lds_at<R, P>(w.tape, t, p, lane) = d1[p];
+                if (ins_tape_a(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, ins_tape(ins), p, lane) = d1[p];
             }
         }
         if constexpr (JAC == 1) {
@@ -471,14 +468,23 @@ __device__ __forceinline__ void reverse_pass(ProgPtr prog, int n, const WaveLds<
         } else {
             CUSR_FOR_P adj[p] = accadj[p];
         }
-        const int t = ins_tape(ins);
+        const int t = ins_tape(ins), ta = ins_tape_a(ins);
         const int nop = ins_binary(ins) ? 2 : 1;
         for (int side = 0; side < nop; ++side) {
             const int kind = side ? ins_bkind(ins) : ins_akind(ins);
             const int idx = side ? ins_bidx(ins) : ins_aidx(ins);
             if (kind == OPD_VAR) continue;
             R g[P];
-            CUSR_FOR_P g[p] = safe_mul<R>(adj[p], lds_at<R, P>(w.tape, t + side, p, lane));
+            if (side ? ins_tape_b(ins) : ta) {
+                const int slot = t + (side ? ta : 0);
+                CUSR_FOR_P g[p] = safe_mul<R>(adj[p], lds_at<R, P>(w.tape, slot, p, lane));
+            } else if (side && ins_fid(ins) == OP_SUB) {
+                // safe_mul(adj, -1) without the tape: -adj, and 0 for a zero adjoint
+                CUSR_FOR_P g[p] = (adj[p] == R(0)) ? R(0) : -adj[p];
+            } else {
+                // safe_mul(adj, +1): ADD, SUB's left operand, the identity
+                CUSR_FOR_P g[p] = (adj[p] == R(0)) ? R(0) : adj[p];
+            }
             if (kind == OPD_ACC) {
                 CUSR_FOR_P accadj[p] = g[p];
             } else if (kind == OPD_SLOT) {

@@ -192,7 +192,12 @@ static int decode_tree(const int32_t *nt, const float *nv, const int32_t *ci, in
         w |= (uint64_t)lo << 24 | (uint64_t)mid << 29 | (uint64_t)hi << 34;
         w |= (uint64_t)tape << 39;
         w |= flag_bits(f, bin, lo, mid, hi);
-        tape += bin ? 2 : 1;
+        // reverse-AD tape slots only for partials that are read and not exactly +-1
+        const bool unit = bin && (f == OP_ADD || f == OP_SUB);
+        const bool ta = a.kind != OPD_VAR && !unit;
+        const bool tb = bin && b.kind != OPD_VAR && !unit;
+        w |= (uint64_t)(ta ? 1 : 0) << 50 | (uint64_t)(tb ? 1 : 0) << 51;
+        tape += (ta ? 1 : 0) + (tb ? 1 : 0);
         out[nins] = w;
         s.opd.push_back({OPD_ACC, 0, nins});
         nins++;
@@ -204,8 +209,7 @@ static int decode_tree(const int32_t *nt, const float *nv, const int32_t *ci, in
         uint64_t w = (uint64_t)OP_IDENT;
         w |= (uint64_t)a.kind << 7 | (uint64_t)(a.idx & 15) << 9;
         w |= (uint64_t)lo << 24 | (uint64_t)hi << 29 | (uint64_t)hi << 34;
-        w |= (uint64_t)tape << 39;
-        tape += 1;
+        w |= (uint64_t)tape << 39;   // the identity's partial is +1: no tape slot
         out[nins++] = w;
     }
     if (tape > 255) return CO_ERR_BOUNDS;

@@ -26,13 +26,18 @@
 //   bits 29..33  mid     constant ranks of the right operand: [mid, hi)
 //   bits 34..38  hi      (unary: mid == hi)
 //   bits 39..46  tape    first reverse-AD tape slot of this instruction
-//                        (one slot per operand)
 //   bit  47      sel     the partials have flat branches: where a point's
 //                        partial is a structural zero its tangents become 0
 //   bit  48      scale_a forward AD scales ranks [lo, mid) by the partial of
 //                        the left / only operand (set when that range is
 //                        non-empty and the partial is not exactly 1)
 //   bit  49      scale_b forward AD scales ranks [mid, hi) by the right partial
+//   bit  50      tape_a  reverse AD keeps the left / only partial in tape slot
+//                        `tape`; without it the partial is never read (a
+//                        variable operand) or exactly +1 (ADD, SUB's left)
+//   bit  51      tape_b  the right partial is kept, in slot tape + tape_a;
+//                        without it it is never read or exactly +1 (ADD) / -1
+//                        (SUB)
 // Constants are ranked in prefix order (cusr/benchmark/popio.py:87-91), so the
 // constants of a subtree form one contiguous rank range; forward AD scales
 // only those ranks.
@@ -74,6 +79,8 @@ static inline __host__ __device__ int ins_tape(uint64_t w) { return (int)((w >> 
 static inline __host__ __device__ int ins_sel(uint64_t w) { return (int)((w >> 47) & 1u); }
 static inline __host__ __device__ int ins_scale_a(uint64_t w) { return (int)((w >> 48) & 1u); }
 static inline __host__ __device__ int ins_scale_b(uint64_t w) { return (int)((w >> 49) & 1u); }
+static inline __host__ __device__ int ins_tape_a(uint64_t w) { return (int)((w >> 50) & 1u); }
+static inline __host__ __device__ int ins_tape_b(uint64_t w) { return (int)((w >> 51) & 1u); }
 
 struct Plan {
     int32_t M, N, D, total_nodes, total_c;
