@@ -257,7 +257,9 @@ def run_rounds(args, cfg, co, gen):
         n_fit = int(np.count_nonzero(pop["metas"][:, 3] > 0))
         lat.append(dt)
         fits += n_fit
-        rounds.append({"round": r, "ms": dt, "device_ms": co.last_kernel_ms(), "fits": n_fit,
+        setup_ms, loop_ms = co.last_split()
+        rounds.append({"round": r, "ms": dt, "device_ms": co.last_kernel_ms(),
+                       "setup_ms": setup_ms, "fit_and_readback_ms": loop_ms, "fits": n_fit,
                        "status_counts": np.bincount(res["status"], minlength=5).tolist()})
         _say(f"round {r}: {dt:.1f} ms end to end, device {co.last_kernel_ms():.1f} ms, "
              f"{n_fit} fits")

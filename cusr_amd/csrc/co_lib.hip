@@ -63,6 +63,19 @@ struct DevBuf {
     size_t cap = 0;
 };
 
+// Page-locked host staging for the decoded programs (hipHostMalloc), grown
+// with 25 % headroom and never shrunk. Copies to the device from it run at
+// DMA speed; from pageable memory the runtime stages them through buffers of
+// its own (C5: 9.5 ms of setup per round, most of it those copies).
+template <typename T>
+struct HostBuf {
+    T *p = nullptr;
+    size_t cap = 0;   // elements
+    T *data() { return p; }
+    T &operator[](size_t i) { return p[i]; }
+    const T &operator[](size_t i) const { return p[i]; }
+};
+
 // K bins run concurrently on the handle's stream and kExtraStreams more. HIP maps
 // each stream of a process to one of GPU_MAX_HW_QUEUES (4) hardware queues,
 // and two streams that share a queue run one after the other: a fifth stream
@@ -96,8 +109,8 @@ struct Ctx {
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
     DevBuf data_X, data_Y;   // co_data_upload: X [D][N] column-major, y [N]
     DevBuf state;            // loop state of fits paused between segments
-    std::vector<uint64_t> h_prog;
-    std::vector<ExprDesc> h_desc;
+    HostBuf<uint64_t> h_prog;
+    HostBuf<ExprDesc> h_desc;
     std::vector<double> h_c, h_li, h_lf;
 };
 
@@ -130,6 +143,32 @@ int grow(DevBuf &b, size_t bytes) {
 #define CO_GROW(buf, bytes)                   \
     do {                                      \
         int r_ = grow((buf), (bytes));        \
+        if (r_ != CO_OK) return r_;           \
+    } while (0)
+
+template <typename T>
+int grow_host(HostBuf<T> &b, size_t n) {
+    if (n == 0) n = 1;
+    if (n <= b.cap) return CO_OK;
+    if (b.p) (void)hipHostFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    const size_t want = n + n / 4;
+    void *q = nullptr;
+    hipError_t e = hipHostMalloc(&q, want * sizeof(T), hipHostMallocDefault);
+    if (e != hipSuccess) {
+        fprintf(stderr, "[cusr_co] hipHostMalloc(%zu) failed: %s\n", want * sizeof(T),
+                hipGetErrorString(e));
+        return (e == hipErrorOutOfMemory) ? CO_ERR_OOM : CO_ERR_CUDA;
+    }
+    b.p = (T *)q;
+    b.cap = want;
+    return CO_OK;
+}
+
+#define CO_GROW_HOST(buf, n)                  \
+    do {                                      \
+        int r_ = grow_host((buf), (n));       \
         if (r_ != CO_OK) return r_;           \
     } while (0)
 
@@ -174,8 +213,8 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
     CO_HIP(hipSetDevice(ctx->device));
     ctx->resident = false;
     const int M = h->M_prob;
-    ctx->h_prog.resize(h->total_nodes > 0 ? h->total_nodes : 1);
-    ctx->h_desc.resize(M > 0 ? M : 1);
+    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? (size_t)h->total_nodes : 1);
+    CO_GROW_HOST(ctx->h_desc, M > 0 ? (size_t)M : 1);
     int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
                                ctx->h_desc.data(), nullptr, nullptr, &ctx->plan);
     if (rc != CO_OK) return rc;
@@ -560,8 +599,8 @@ extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, c
     CO_HIP(hipSetDevice(ctx->device));
     ctx->resident = false;  // the evaluation reuses the population buffers
     const int M = h->M_prob;
-    ctx->h_prog.resize(h->total_nodes > 0 ? h->total_nodes : 1);
-    ctx->h_desc.resize(M > 0 ? M : 1);
+    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? (size_t)h->total_nodes : 1);
+    CO_GROW_HOST(ctx->h_desc, M > 0 ? (size_t)M : 1);
     int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
                                ctx->h_desc.data(), nullptr, nullptr, nullptr);
     if (rc != CO_OK || M == 0) return rc;
@@ -668,6 +707,8 @@ extern "C" void co_teardown(void *handle) {
                       &ctx->data_X, &ctx->data_Y, &ctx->state};
     for (DevBuf *b : bufs)
         if (b->p) (void)hipFree(b->p);
+    if (ctx->h_prog.p) (void)hipHostFree(ctx->h_prog.p);
+    if (ctx->h_desc.p) (void)hipHostFree(ctx->h_desc.p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     for (int i = 0; i < kExtraStreams; ++i) {
         if (ctx->lanes[i]) (void)hipStreamDestroy(ctx->lanes[i]);

@@ -244,6 +244,7 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
     }
     std::vector<int> count(CO_MAX_K + 1, 0);
     std::vector<int32_t> depth(M), tapes(M), poff(M), nins(M), slots(M), rcs(M, CO_OK);
+    std::vector<int64_t> cost(descs ? M : 0);
     // programs are laid out expression after expression (prefix sum of
     // n_nodes), which equals node_offset for well-formed populations and
     // keeps overlapping metas from aliasing each other's instructions
@@ -271,6 +272,12 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
                                  t.n_nodes, t.K, h->n_vars, out, &nins[m], &depth[m], &tapes[m],
                                  &slots[m], s);
             if (rcs[m] != CO_OK) return;
+            if (descs) {
+                // launch-order estimate: fixed per-pass cost plus op_cost per instruction
+                int64_t c = 229;
+                for (int i = 0; i < nins[m]; i++) c += op_cost(ins_fid(out[i]));
+                cost[m] = c;
+            }
         }
     };
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
@@ -317,20 +324,25 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
         // programs first (fixed per-pass cost plus op_cost of each
         // instruction), so the longest-running workgroups start earliest and
         // a bin ends on cheap ones. Ties keep the order of ord reversed.
-        std::vector<int32_t> launch(M);
-        std::vector<int64_t> cost(M);
-        for (int m = 0; m < M; m++) {
-            int64_t c = 229;
-            for (int i = 0; i < nins[m]; i++) c += op_cost(ins_fid(prog[poff[m] + i]));
-            cost[m] = c;
-        }
-        for (int p = 0; p < M; p++) launch[p] = ord[M - 1 - p];
-        for (int k = CO_MAX_K, p0 = 0; k >= 0; --k) {
-            const int cnt = start[k + 1] - start[k];
-            std::stable_sort(launch.begin() + p0, launch.begin() + p0 + cnt,
-                             [&](int32_t a, int32_t b) { return cost[a] > cost[b]; });
-            p0 += cnt;
-        }
+        // two stable counting-sort passes over reversed ord: by cost
+        // descending (clamped to kCostBuckets), then by K descending; ties
+        // keep the order of ord reversed
+        constexpr int kCostBuckets = 1 << 15;
+        std::vector<int32_t> a(M), launch(M);
+        for (int p = 0; p < M; p++) a[p] = ord[M - 1 - p];
+        std::vector<int32_t> next(kCostBuckets + 1, 0);
+        auto bucket = [&](int32_t m) {
+            const int64_t c = cost[m] < kCostBuckets - 1 ? cost[m] : kCostBuckets - 1;
+            return (int)(kCostBuckets - 1 - c);
+        };
+        for (int p = 0; p < M; p++) next[bucket(a[p]) + 1]++;
+        for (int i = 0; i < kCostBuckets; i++) next[i + 1] += next[i];
+        for (int p = 0; p < M; p++) launch[next[bucket(a[p])]++] = a[p];
+        std::vector<int32_t> knext(CO_MAX_K + 2, 0);
+        for (int p = 0; p < M; p++) knext[CO_MAX_K - metas[launch[p]].K + 1]++;
+        for (int i = 0; i <= CO_MAX_K; i++) knext[i + 1] += knext[i];
+        for (int p = 0; p < M; p++) a[knext[CO_MAX_K - metas[launch[p]].K]++] = launch[p];
+        launch.swap(a);
         for (int p = 0; p < M; p++) {
             const int m = launch[p];
             ExprDesc &d = descs[p];
