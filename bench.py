@@ -22,7 +22,7 @@ per pass, the bytecode) over its duration from HIP events recorded around
 that launch on the stream it runs on. The same object carries the VALU figures,
 the roof this kernel is actually under: algorithmic flops over the same
 duration (a lower bound: a transcendental counts 2 flops), and, when the
-committed rocprofv3 counter summary (profiles/lm_fit_c2_valu.json) was taken on
+committed rocprofv3 counter summary (profiles/lm_fit_<config>_valu.json) was taken on
 this workload, the measured VALU busy fraction of the whole fit and of the
 dominant kernel running alone. traffic: measured HBM bytes of that launch, from the rocprofv3
 FETCH_SIZE / WRITE_SIZE summary committed under profiles/, when it was taken
@@ -103,11 +103,17 @@ def copy_calibration(co, pop):
          f"{8 * n} bytes written")
 
 
+def _profile(workload_key, what):
+    """profiles/lm_fit_<config>_<what>.json for the configuration named in
+    the workload key (C1..C5)."""
+    return REPO / "profiles" / f"lm_fit_{workload_key.split(':')[0].lower()}_{what}.json"
+
+
 def load_traffic(workload_key, kernel):
     """HBM bytes per launch of `kernel`, from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel), when that
     summary was taken on this workload."""
-    p = REPO / "profiles" / "lm_fit_c2_traffic.json"
+    p = _profile(workload_key, "traffic")
     if not p.exists():
         return None
     d = json.loads(p.read_text())
@@ -123,7 +129,7 @@ def load_valu(workload_key):
     """Per-kernel SQ counters (SQ_ACTIVE_INST_VALU: quad-cycles of VALU issue,
     summed over waves) from the committed rocprofv3 --pmc summary, when that
     summary was taken on this workload."""
-    p = REPO / "profiles" / "lm_fit_c2_valu.json"
+    p = _profile(workload_key, "valu")
     if not p.exists():
         return None
     d = json.loads(p.read_text())
@@ -156,7 +162,7 @@ def valu_issue(workload_key, kname_of, bins, device_ms, kdom):
     return {"whole_fit_frac": tot * cyc / (device_ms / 1e3),
             "dominant_alone_frac": dom["SQ_ACTIVE_INST_VALU"] * cyc / (dom["alone_ms"] / 1e3),
             "dominant_alone_ms": dom["alone_ms"], "clock_ghz": MI355X_CLOCK_HZ / 1e9,
-            "simds": MI355X_SIMDS, "source": "profiles/lm_fit_c2_valu.json"}
+            "simds": MI355X_SIMDS, "source": str(_profile(workload_key, "valu").relative_to(REPO))}
 
 
 def workload_text(cfg, pop):

@@ -1016,13 +1016,19 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
 #ifndef CUSR_W64_TABLE
 #define CUSR_W64_TABLE 1, 1, 1, 2, 2, 2, 2, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
+// fp64 reverse AD: no cap except K = 9 (256 VGPRs with 23 spilled beats 300
+// at one wave per SIMD; from K = 10 the spills grow to 76 and more)
+#ifndef CUSR_WREV64_TABLE
+#define CUSR_WREV64_TABLE 1, 1, 1, 1, 1, 1, 1, 1, 1, 2, 1, 1, 1, 1, 1, 1, 1
+#endif
 #ifndef CUSR_WAVES_OTHER
 #define CUSR_WAVES_OTHER 1
 #endif
 constexpr int kW64[CO_MAX_K + 1] = {CUSR_W64_TABLE};
+constexpr int kWRev64[CO_MAX_K + 1] = {CUSR_WREV64_TABLE};
 template <typename R, int K, int AD>
 constexpr int waves_per_eu() {
-    return (sizeof(R) == 8 && AD == CO_AD_FORWARD) ? kW64[K] : CUSR_WAVES_OTHER;
+    return sizeof(R) == 8 ? (AD == CO_AD_FORWARD ? kW64[K] : kWRev64[K]) : CUSR_WAVES_OTHER;
 }
 template <int K, typename R, int AD>
 __global__ void __launch_bounds__(kLanes * CO_MAX_PARTITIONS, (waves_per_eu<R, K, AD>()))
