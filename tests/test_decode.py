@@ -113,6 +113,44 @@ def test_stack_depth_and_k_bins(idx):
     assert orc_rc == 0 and np.array_equal(orc_stack, stack)
 
 
+# flat-branch operators (the select rule): MAX, MIN, LT, GT, LE, GE, PDIV, CEXP
+SELECT_OPS = {8, 9, 10, 11, 12, 13, 32, 33}
+
+
+@pytest.mark.parametrize("idx", range(9))
+def test_ad_flags_and_tape_slots(idx):
+    """Per-instruction AD fields (bits 47..51): reverse-AD tape slots are dense
+    and in execution order; a side has one exactly when its partial is read
+    (not a variable) and not exactly +-1 (ADD, SUB, the identity); forward-AD
+    scale flags never point at an empty rank range."""
+    pop = _pops()[idx]
+    rc, prog, order, bins, stack = ci.decode(pop)
+    assert rc == 0
+    for m in range(pop["M"]):
+        o, n, _, _ = (int(v) for v in pop["metas"][m])
+        nxt = 0
+        for w in prog[o:o + n]:
+            w = int(w)
+            if w == 0:
+                break
+            f = fields(w)
+            sel, sa, sb, ta, tb = ((w >> b) & 1 for b in (47, 48, 49, 50, 51))
+            assert f["tape"] == nxt
+            nxt += ta + tb
+            unit = f["fid"] in (1, 2) or f["fid"] == OP_IDENT
+            assert ta == int(f["ak"] != 1 and not unit)
+            assert tb == int(bool(f["bin"]) and f["bk"] != 1 and not unit)
+            assert sel == int(f["fid"] in SELECT_OPS)
+            if sa:
+                assert f["mid"] > f["lo"] and f["fid"] not in (1, 2, OP_IDENT)
+            if sb:
+                assert f["bin"] and f["hi"] > f["mid"] and f["fid"] != 1
+            # a scaled range is exactly a non-empty one whose partial is not 1
+            if f["bin"]:
+                assert sa == int(f["mid"] > f["lo"] and f["fid"] not in (1, 2))
+                assert sb == int(f["hi"] > f["mid"] and f["fid"] != 1)
+
+
 def test_reference_header_stats():
     """pop1000.bin header matches the reference golden manifest."""
     pop = ref_pop("pop1000.bin")
