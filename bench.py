@@ -272,7 +272,8 @@ def run_rounds(args, cfg, co, gen):
         last = (pop, res, co.last_bin_ms())
     value = fits / (sum(lat) / 1e3)
     pop, res, bins = last
-    roof = roofline(pop, cfg, res["iters"], bins, lambda k: f"lm_fit_kernel<{k}, float, 0>")
+    roof = roofline(pop, cfg, res["iters"], bins, lambda k: f"lm_fit_kernel<{k}, float, 0>",
+                    device_ms=rounds[-1]["device_ms"])
     fit = {"rounds": rounds, "mean_round_ms": float(np.mean(lat)),
            "p50_round_ms": float(np.median(lat)),
            "target": "tiled [M][N]" if args.tiled else "shared row [N] (pop.bin v2)"}

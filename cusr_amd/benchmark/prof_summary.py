@@ -3,7 +3,7 @@
     python -m cusr_amd.benchmark.prof_summary trace  <run_results.db> [--match lm_fit]
     python -m cusr_amd.benchmark.prof_summary pmc    <run_results.db> [--match lm_fit]
     python -m cusr_amd.benchmark.prof_summary valu   <run_results.db> [--match lm_fit]
-           [--out JSON --workload-key KEY]
+           [--out JSON --workload-key KEY] [--last]
     python -m cusr_amd.benchmark.prof_summary traffic <fetch.db> <write.db> --kernel NAME
            --calib-fetch-bytes F --calib-write-bytes W [--out JSON --workload-key KEY]
 
@@ -53,10 +53,17 @@ def trace(db, match=None):
     return "\n".join(out)
 
 
-def pmc_per_dispatch(db, match=None):
+def pmc_per_dispatch(db, match=None, last=False):
+    """Per kernel, each counter's mean over its dispatches (last: the value of
+    the kernel's last dispatch only)."""
     rows = _rows(db, "select kernel_name, dispatch_id, counter_name, sum(value) "
                      "from counters_collection group by kernel_name, dispatch_id, counter_name")
     acc = collections.defaultdict(lambda: collections.defaultdict(list))
+    if last:
+        top = {}
+        for name, disp, _ctr, _val in rows:
+            top[name] = max(top.get(name, disp), disp)
+        rows = [r for r in rows if r[1] == top[r[0]]]
     for name, _disp, ctr, val in rows:
         if match and match not in name:
             continue
@@ -74,14 +81,18 @@ def pmc(db, match=None):
     return "\n".join(out)
 
 
-def valu(db, match=None, workload_key=None):
+def valu(db, match=None, workload_key=None, last=False):
     """Per kernel: the average per dispatch of every collected counter and
     the dispatch duration (counter runs serialise dispatches, so these are
-    the kernels running alone)."""
-    d = pmc_per_dispatch(db, match)
+    the kernels running alone); last: the kernel's last dispatch only."""
+    d = pmc_per_dispatch(db, match, last)
     durs = collections.defaultdict(list)
-    for name, dur in _rows(db, "select name, duration from kernels"):
-        if name in d:
+    rows = _rows(db, "select name, dispatch_id, duration from kernels")
+    top = {}
+    for name, disp, _dur in rows:
+        top[name] = max(top.get(name, disp), disp)
+    for name, disp, dur in rows:
+        if name in d and (not last or disp == top[name]):
             durs[name].append(dur / 1e6)
     out = {"kernels": {}}
     for name in sorted(d):
@@ -137,13 +148,16 @@ def main():
     ap.add_argument("--calib-write-bytes", type=float, default=None)
     ap.add_argument("--out", default=None)
     ap.add_argument("--workload-key", default=None)
+    ap.add_argument("--last", action="store_true",
+                    help="valu: each kernel's last dispatch only (runs whose earlier "
+                         "dispatches are warm-ups of another shape)")
     a = ap.parse_args()
     if a.mode == "trace":
         print(trace(a.dbs[0], a.match))
     elif a.mode == "pmc":
         print(pmc(a.dbs[0], a.match))
     elif a.mode == "valu":
-        t = valu(a.dbs[0], a.match, a.workload_key)
+        t = valu(a.dbs[0], a.match, a.workload_key, a.last)
         print(json.dumps(t, indent=1))
         if a.out:
             with open(a.out, "w") as fh:
