@@ -29,7 +29,8 @@ LIB_FD = KDIR / "libcusr_co_fd.so"
 CLI = KDIR / "batch_lm_ad"
 CLI_FD = KDIR / "batch_lm"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-ARCH = "gfx950"
+# offload target; CUSR_OFFLOAD_ARCH selects a feature variant (e.g. gfx950:xnack-)
+ARCH = os.environ.get("CUSR_OFFLOAD_ARCH", "gfx950")
 
 # -ffp-contract=off: fused multiply-adds only where fma() is written, so the
 # device arithmetic order is the one the CPU oracle reproduces.
