@@ -57,6 +57,15 @@ constexpr int points_per_pass() {
     return (AD == CO_AD_REVERSE) ? 1 : (sizeof(R) == 4) ? kP32[K] : kP64[K];
 }
 
+// Points per lane of the mixed-precision fit's fp64 guard passes: as many as
+// fit the LDS bytes of the fit's own passes (fp32 at P points -> fp64 at P/2).
+template <typename R, int K, int AD>
+constexpr int audit_points() {
+    return points_per_pass<R, K, AD>() * (int)sizeof(R) / 8 > 0
+               ? points_per_pass<R, K, AD>() * (int)sizeof(R) / 8
+               : 1;
+}
+
 // scalar-cache view of the program (constant address space)
 typedef const __attribute__((address_space(4))) uint64_t *ProgPtr;
 
@@ -978,17 +987,20 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     double lf = loss, li = loss_init;
     if constexpr (sizeof(R) == 4) {
         // fp64 losses at the delivered point and at the start; the fp64
-        // value pass reuses the same LDS at one point per lane
-        WaveLds<double, 1> w64;
+        // value pass reuses the same LDS bytes per row and lane (half the
+        // points of the fp32 passes). A lane's points are summed in the same
+        // ascending order at any number of points per pass.
+        constexpr int AP = audit_points<R, K, AD>();
+        WaveLds<double, AP> w64;
         w64.x = (double *)my_lds;
-        w64.slot = w64.x + (size_t)fa.D * kLanes;
-        w64.tape = w64.slot + (size_t)fa.slots * kLanes;
-        data_pass<K, double, 1, 0>(pa, w64, c_cur, s_try, lane);
+        w64.slot = w64.x + (size_t)fa.D * AP * kLanes;
+        w64.tape = w64.slot + (size_t)fa.slots * AP * kLanes;
+        data_pass<K, double, AP, 0>(pa, w64, c_cur, s_try, lane);
         lf = uni(0.5 * s_try[0]);
         if (fa.pwaves > 1) __syncthreads();
         if (lead && lane < K) c_try[lane] = fa.C0[e.c_off + lane];
         block_sync(fa.pwaves);
-        data_pass<K, double, 1, 0>(pa, w64, c_try, s_try, lane);
+        data_pass<K, double, AP, 0>(pa, w64, c_try, s_try, lane);
         li = uni(0.5 * s_try[0]);
     }
     bool revert = false;
@@ -1043,11 +1055,11 @@ lm_fit_kernel(FitArgs fa) {
 }
 
 // Dynamic LDS bytes one wavefront of a fit launch needs (the mixed-precision
-// fp64 audit pass reuses the same bytes at one point per lane).
+// fp64 audit pass reuses the same bytes at audit_points per lane).
 template <typename R, int K, int AD>
 constexpr size_t fit_lds_bytes_t(int D, int slots, int tape) {
     const size_t a = (size_t)(D + slots + tape) * points_per_pass<R, K, AD>() * kLanes * sizeof(R);
-    const size_t b = (size_t)(D + slots) * kLanes * sizeof(double);
+    const size_t b = (size_t)(D + slots) * audit_points<R, K, AD>() * kLanes * sizeof(double);
     return (matrix_sums<K, AD>() ? kJtBytes + (size_t)K * (K + 1) * sizeof(double) : 0) +
            (a > b ? a : b);
 }
