@@ -50,11 +50,15 @@ constexpr float kCexpCap32 = 485165184.0f;         // exp(20) rounded to float
 #ifndef CUSR_P32_TABLE
 #define CUSR_P32_TABLE 4, 4, 4, 4, 4, 4, 4, 4, 4, 2, 2, 2, 2, 2, 2, 2, 2
 #endif
+#ifndef CUSR_PREV_TABLE
+#define CUSR_PREV_TABLE 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1
+#endif
 constexpr int kP64[CO_MAX_K + 1] = {CUSR_P64_TABLE};
 constexpr int kP32[CO_MAX_K + 1] = {CUSR_P32_TABLE};
+constexpr int kPRev[CO_MAX_K + 1] = {CUSR_PREV_TABLE};   // reverse AD (tape in LDS)
 template <typename R, int K, int AD>
 constexpr int points_per_pass() {
-    return (AD == CO_AD_REVERSE) ? 1 : (sizeof(R) == 4) ? kP32[K] : kP64[K];
+    return (AD == CO_AD_REVERSE) ? kPRev[K] : (sizeof(R) == 4) ? kP32[K] : kP64[K];
 }
 
 // Points per lane of the mixed-precision fit's fp64 guard passes: as many as
