@@ -362,6 +362,15 @@ template <typename R, int P> struct ScaleAsm;
 CUSR_SCALE_ASM(double, "v_mul_f64", "v_mov_b64")
 CUSR_SCALE_ASM(float, "v_mul_f32", "v_mov_b32")
 #undef CUSR_SCALE_ASM
+#undef CUSR_SKIP_HEAD
+#undef CUSR_SEL_TEST
+#undef CUSR_SKIP_TAIL
+#undef CUSR_MUL
+#undef CUSR_ZERO
+#undef CUSR_T
+#undef CUSR_D
+#undef CUSR_Z
+#undef CUSR_IN
 
 // Entries J..K-1 of the tangent rows, one asm block per entry.
 template <int K, int J, typename R, int P>
