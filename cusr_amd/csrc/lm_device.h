@@ -290,7 +290,7 @@ __device__ __forceinline__ R &lds_at(R *base, int idx, int p, int lane) {
 // allocator resolved with copies of the whole tangent array at every
 // interpreter step. The arithmetic is the same IEEE v_mul_f64 / v_mul_f32; a
 // zeroed lane is the select z ? 0 : t*d, done by masking exec to z around one
-// move and restoring it.
+// move and restoring it. The blocks set SCC (declared clobbered).
 #define CUSR_SKIP_HEAD "s_bitcmp1_b32 %[m], %[j]\n\ts_cbranch_scc0 .Lcusr_skip%=\n\t"
 #define CUSR_SEL_TEST "s_cmp_lg_u32 %[sel], 0\n\ts_cbranch_scc0 .Lcusr_skip%=\n\t"
 #define CUSR_SKIP_TAIL ".Lcusr_skip%=:"
@@ -312,7 +312,7 @@ template <typename R, int P> struct ScaleAsm;
             __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_SEL_TEST CUSR_ZERO(MOV, 0)     \
                                  CUSR_SKIP_TAIL                                                  \
                              : CUSR_T(0), [sv] "=&s"(sv)                                         \
-                             : CUSR_IN, CUSR_D(0), CUSR_Z(0));                                   \
+                             : CUSR_IN, CUSR_D(0), CUSR_Z(0) : "scc");                                   \
         }                                                                                        \
     };                                                                                           \
     template <> struct ScaleAsm<R, 2> {                                                          \
@@ -323,7 +323,7 @@ template <typename R, int P> struct ScaleAsm;
             __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_MUL(MUL, 1) CUSR_SEL_TEST      \
                                  CUSR_ZERO(MOV, 0) CUSR_ZERO(MOV, 1) CUSR_SKIP_TAIL              \
                              : CUSR_T(0), CUSR_T(1), [sv] "=&s"(sv)                              \
-                             : CUSR_IN, CUSR_D(0), CUSR_D(1), CUSR_Z(0), CUSR_Z(1));             \
+                             : CUSR_IN, CUSR_D(0), CUSR_D(1), CUSR_Z(0), CUSR_Z(1) : "scc");             \
         }                                                                                        \
     };                                                                                           \
     template <> struct ScaleAsm<R, 4> {                                                          \
@@ -337,7 +337,7 @@ template <typename R, int P> struct ScaleAsm;
                                          CUSR_SKIP_TAIL                                          \
                              : CUSR_T(0), CUSR_T(1), CUSR_T(2), CUSR_T(3), [sv] "=&s"(sv)        \
                              : CUSR_IN, CUSR_D(0), CUSR_D(1), CUSR_D(2), CUSR_D(3), CUSR_Z(0),   \
-                               CUSR_Z(1), CUSR_Z(2), CUSR_Z(3));                                 \
+                               CUSR_Z(1), CUSR_Z(2), CUSR_Z(3) : "scc");                                 \
         }                                                                                        \
     };                                                                                           \
     template <> struct ScaleAsm<R, 8> {                                                          \
@@ -356,7 +356,7 @@ template <typename R, int P> struct ScaleAsm;
                                CUSR_T(6), CUSR_T(7), [sv] "=&s"(sv)                              \
                              : CUSR_IN, CUSR_D(0), CUSR_D(1), CUSR_D(2), CUSR_D(3), CUSR_D(4),   \
                                CUSR_D(5), CUSR_D(6), CUSR_D(7), CUSR_Z(0), CUSR_Z(1), CUSR_Z(2), \
-                               CUSR_Z(3), CUSR_Z(4), CUSR_Z(5), CUSR_Z(6), CUSR_Z(7));           \
+                               CUSR_Z(3), CUSR_Z(4), CUSR_Z(5), CUSR_Z(6), CUSR_Z(7) : "scc");           \
         }                                                                                        \
     };
 CUSR_SCALE_ASM(double, "v_mul_f64", "v_mov_b64")
