@@ -1,6 +1,7 @@
 """Summarise a rocprofv3 database (rocpd SQLite) as a markdown table.
 
     python -m cusr_amd.benchmark.prof_summary trace  <run_results.db> [--match lm_fit]
+           [--skip W --take T]
     python -m cusr_amd.benchmark.prof_summary pmc    <run_results.db> [--match lm_fit]
     python -m cusr_amd.benchmark.prof_summary valu   <run_results.db> [--match lm_fit]
            [--out JSON --workload-key KEY] [--last]
@@ -33,13 +34,20 @@ def _rows(db, sql):
         con.close()
 
 
-def trace(db, match=None):
+def trace(db, match=None, skip=0, take=None):
+    """skip / take: per kernel, drop its first `skip` dispatches and keep the
+    next `take` (a benchmark's timed steps after its warm-up)."""
     rows = _rows(db, "select name, duration, vgpr_count, accum_vgpr_count, sgpr_count, "
-                     "scratch_size, lds_size, grid_x, workgroup_x from kernels")
+                     "scratch_size, lds_size, grid_x, workgroup_x from kernels "
+                     "order by dispatch_id")
     by = collections.defaultdict(list)
+    seen = collections.Counter()
     meta = {}
     for name, dur, vg, ag, sg, scr, lds, gx, wx in rows:
         if match and match not in name:
+            continue
+        seen[name] += 1
+        if seen[name] <= skip or (take is not None and seen[name] > skip + take):
             continue
         by[name].append(dur / 1e6)
         meta[name] = (vg, ag, sg, scr, lds, gx // max(wx, 1))
@@ -148,12 +156,16 @@ def main():
     ap.add_argument("--calib-write-bytes", type=float, default=None)
     ap.add_argument("--out", default=None)
     ap.add_argument("--workload-key", default=None)
+    ap.add_argument("--skip", type=int, default=0,
+                    help="trace: drop each kernel's first SKIP dispatches")
+    ap.add_argument("--take", type=int, default=None,
+                    help="trace: then keep TAKE dispatches per kernel")
     ap.add_argument("--last", action="store_true",
                     help="valu: each kernel's last dispatch only (runs whose earlier "
                          "dispatches are warm-ups of another shape)")
     a = ap.parse_args()
     if a.mode == "trace":
-        print(trace(a.dbs[0], a.match))
+        print(trace(a.dbs[0], a.match, a.skip, a.take))
     elif a.mode == "pmc":
         print(pmc(a.dbs[0], a.match))
     elif a.mode == "valu":
