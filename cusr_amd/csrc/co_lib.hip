@@ -576,6 +576,47 @@ extern "C" int co_data_upload(void *handle, int N, int n_vars, const double *xs,
     return CO_OK;
 }
 
+// True when p is device memory the handle's device can read (a torch CUDA
+// tensor's data on that device, for instance).
+static bool on_device(const void *p, int device) {
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();   // a pageable host pointer is not an error to keep
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice && a.device == device;
+}
+
+extern "C" int co_data_upload_device(void *handle, int N, int n_vars, const double *xs_dev,
+                                     const double *y_dev) {
+    if (!handle || N < 0 || n_vars < 0 || n_vars > CO_MAX_VARS) return CO_ERR_NULLARG;
+    if (N > 0 && (!y_dev || (n_vars > 0 && !xs_dev))) return CO_ERR_NULLARG;
+    Ctx *ctx = (Ctx *)handle;
+    CO_HIP(hipSetDevice(ctx->device));
+    // every pointer checked before anything is copied
+    if (N > 0 && (!on_device(y_dev, ctx->device) ||
+                  (n_vars > 0 && !on_device(xs_dev, ctx->device))))
+        return CO_ERR_DATA;
+    ctx->data_N = -1;   // no data set until this upload completes
+    if (ctx->on_data) ctx->resident = false;
+    const size_t nX = (size_t)N * n_vars;
+    CO_GROW(ctx->data_X, sizeof(double) * nX);
+    CO_GROW(ctx->data_Y, sizeof(double) * N);
+    hipStream_t s = ctx->stream;
+    if (nX) {
+        // row-major [N][D] straight from the caller's memory to column-major
+        transpose_x_kernel<double><<<blocks_for(nX, 256), 256, 0, s>>>(
+            xs_dev, ptr<double>(ctx->data_X), N, n_vars);
+        CO_HIP(hipGetLastError());
+    }
+    if (N)
+        CO_HIP(hipMemcpyAsync(ctx->data_Y.p, y_dev, 8 * (size_t)N, hipMemcpyDeviceToDevice, s));
+    CO_HIP(hipStreamSynchronize(s));
+    ctx->data_N = N;
+    ctx->data_D = n_vars;
+    return CO_OK;
+}
+
 extern "C" int co_optimize_data(void *handle, const CoOptions *opt, const PopHeader *h,
                                 const int32_t *nt, const float *nv, const int32_t *ci,
                                 const TreeMeta *metas, const double *c, double *c_final_out,

@@ -105,7 +105,7 @@ _HERE = Path(__file__).resolve().parent
 EXPORTED = ("co_init", "co_optimize", "co_last_split", "co_teardown", "co_options_default",
             "co_optimize_ex", "co_eval_ex", "co_upload_ex", "co_fit_resident",
             "co_last_kernel_ms", "co_last_bin_ms", "co_decode", "co_data_upload",
-            "co_optimize_data")
+            "co_optimize_data", "co_data_upload_device")
 
 
 def lib_path(variant: str = "ad") -> Path:
@@ -175,6 +175,8 @@ def _bind(lib) -> None:
     lib.co_fit_resident.restype = ctypes.c_int
     lib.co_data_upload.argtypes = [_VP, ctypes.c_int, ctypes.c_int, _VP, _VP]
     lib.co_data_upload.restype = ctypes.c_int
+    lib.co_data_upload_device.argtypes = [_VP, ctypes.c_int, ctypes.c_int, _VP, _VP]
+    lib.co_data_upload_device.restype = ctypes.c_int
     lib.co_optimize_data.argtypes = [_VP, ctypes.POINTER(CoOptions), ctypes.POINTER(PopHeader)] + [_VP] * 10
     lib.co_optimize_data.restype = ctypes.c_int
     lib.co_last_kernel_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
@@ -395,6 +397,33 @@ class InProcessCO:
         if rc != CO_OK:
             raise COError(rc, "co_data_upload")
         self._data = (x.copy(), yy.copy())
+
+    def upload_data_device(self, xs, y) -> None:
+        """upload_data from device tensors (torch, float64, contiguous, on this
+        handle's device): xs [N, D] and y [N] are copied device to device,
+        never through host memory. Waits for the current torch stream first,
+        so the tensors are complete when the library reads them."""
+        self._check()
+        import torch
+
+        if not (isinstance(xs, torch.Tensor) and isinstance(y, torch.Tensor)):
+            raise TypeError("upload_data_device takes torch tensors")
+        if xs.dtype != torch.float64 or y.dtype != torch.float64:
+            raise ValueError("xs and y must be float64")
+        if xs.dim() != 2 or y.dim() != 1 or y.shape[0] != xs.shape[0]:
+            raise ValueError(f"xs must be [N, D] and y [N]; got {tuple(xs.shape)} and "
+                             f"{tuple(y.shape)}")
+        if not (xs.is_contiguous() and y.is_contiguous()):
+            raise ValueError("xs and y must be contiguous")
+        for t in (xs, y):
+            if t.is_cuda:
+                torch.cuda.current_stream(t.device).synchronize()
+        self._data = None
+        rc = self._lib.co_data_upload_device(self._handle, int(xs.shape[0]), int(xs.shape[1]),
+                                             ctypes.c_void_p(xs.data_ptr()),
+                                             ctypes.c_void_p(y.data_ptr()))
+        if rc != CO_OK:
+            raise COError(rc, "co_data_upload_device")
 
     def data_matches(self, xs, y) -> bool:
         """True when (xs, y) equal the uploaded data set value for value."""

@@ -35,7 +35,9 @@ extern "C" {
                                 Extension: the reference silently evaluates unknown
                                 ops to 0 (cusr/kernel/lm_core.cuh:82,100). */
 #define CO_ERR_DATA (-7)     /* co_optimize_data: no data set uploaded, or the header's
-                                N / n_vars differ from the uploaded one */
+                                N / n_vars differ from the uploaded one;
+                                co_data_upload_device: a pointer that is not
+                                device memory of the handle's device */
 
 /* Device limits of this build (the reference's are MAX_K=32, MAX_STACK=64,
  * cusr/kernel/ad_interp.cuh:34-39). Populations beyond them get CO_ERR_BOUNDS
@@ -220,6 +222,20 @@ int co_fit_resident(void *handle, const CoOptions *opt,
  * (N < 0, n_vars outside 0..CO_MAX_VARS, null pointers with N > 0),
  * CO_ERR_OOM or CO_ERR_CUDA. */
 int co_data_upload(void *handle, int N, int n_vars, const double *xs, const double *y);
+
+/* co_data_upload from device memory: xs_dev (N * n_vars fp64, row-major) and
+ * y_dev (N fp64) are device pointers on the handle's device, such as the data
+ * of torch CUDA tensors. They are copied device to device (X transposed on the
+ * device), so the data set never crosses PCIe. The caller's data must be
+ * complete when called (synchronize the stream that produced it); the
+ * library does not keep the pointers. No counterpart in the reference: it is
+ * the data-residency half of the zero-copy entry its in-process plan
+ * describes as the end state (docs/kernel/INPROCESS_CO_PLAN.md:69-75).
+ * Returns as co_data_upload, and CO_ERR_DATA when a pointer is not device
+ * memory of the handle's device; then nothing is copied and the previous data
+ * set stays. */
+int co_data_upload_device(void *handle, int N, int n_vars, const double *xs_dev,
+                          const double *y_dev);
 
 /* co_optimize_ex against the uploaded data set: every expression fits its
  * target y; only the programs and c go to the device. header->N and

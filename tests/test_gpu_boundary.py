@@ -223,3 +223,21 @@ def test_resident_data_errors(co):
         fresh.teardown()
     with pytest.raises(ValueError):
         co.upload_data(np.zeros((10, 2)), np.zeros(9))
+
+
+def test_resident_data_from_device_tensors():
+    """co_data_upload_device from torch CUDA tensors equals co_data_upload from
+    host arrays bit for bit; host pointers are refused with CO_ERR_DATA. Runs
+    in a child process (tests/torch_interop_check.py) that imports torch
+    before loading the library, so both share torch's HIP runtime: this test
+    process loaded the library first and holds the system runtime."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    script = Path(__file__).resolve().parent / "torch_interop_check.py"
+    _say("resident data from device tensors (child process, torch first)")
+    r = subprocess.run([sys.executable, "-u", str(script)], capture_output=True, text=True,
+                       timeout=180)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "torch interop ok" in r.stdout
