@@ -119,8 +119,9 @@ def load_traffic(workload_key, kernel):
     d = json.loads(p.read_text())
     if d.get("workload_key") != workload_key:
         return None
+    # instances chosen by N carry one more template argument (<K, R, AD, 1>)
     for name, v in d["kernels"].items():
-        if kernel in name:
+        if kernel.rstrip(">") in name:
             return v["bytes_per_launch"]
     return None
 
@@ -151,14 +152,14 @@ def valu_issue(workload_key, kname_of, bins, device_ms, kdom):
     for k, v in enumerate(bins):
         if v < 0:
             continue
-        e = next((e for n, e in ctr.items() if kname_of(k) in n), None)
+        e = next((e for n, e in ctr.items() if kname_of(k).rstrip(">") in n), None)
         if e is None:
             missing.append(k)
             continue
         tot += e["SQ_ACTIVE_INST_VALU"]
     if missing:
         return None
-    dom = next(e for n, e in ctr.items() if kname_of(kdom) in n)
+    dom = next(e for n, e in ctr.items() if kname_of(kdom).rstrip(">") in n)
     return {"whole_fit_frac": tot * cyc / (device_ms / 1e3),
             "dominant_alone_frac": dom["SQ_ACTIVE_INST_VALU"] * cyc / (dom["alone_ms"] / 1e3),
             "dominant_alone_ms": dom["alone_ms"], "clock_ghz": MI355X_CLOCK_HZ / 1e9,

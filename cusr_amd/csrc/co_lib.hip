@@ -181,11 +181,16 @@ unsigned blocks_for(size_t n, unsigned t) { return (unsigned)((n + t - 1) / t); 
 // dynamic budget
 constexpr size_t kStaticLds = 2 * CO_MAX_K * 8 + 2 * 153 * 8;
 
+// the launcher's choice of instance (fit_kernels.hip): the large-N one from
+// kLargeN points where its tables differ
 template <typename R, int AD>
-size_t lds_for_k(int K, int D, int slots, int tape) {
+size_t lds_for_k(int K, int N, int D, int slots, int tape) {
     switch (K) {
-#define CUSR_LDS_CASE(k) \
-    case k: return fit_lds_bytes_t<R, k, AD>(D, slots, tape);
+#define CUSR_LDS_CASE(k)                                                        \
+    case k:                                                                     \
+        return (large_n_variant<R, k, AD>() && N >= kLargeN)                    \
+                   ? fit_lds_bytes_t<R, k, AD, 1>(D, slots, tape)               \
+                   : fit_lds_bytes_t<R, k, AD, 0>(D, slots, tape);
     CUSR_LDS_CASE(0) CUSR_LDS_CASE(1) CUSR_LDS_CASE(2) CUSR_LDS_CASE(3) CUSR_LDS_CASE(4)
     CUSR_LDS_CASE(5) CUSR_LDS_CASE(6) CUSR_LDS_CASE(7) CUSR_LDS_CASE(8) CUSR_LDS_CASE(9)
     CUSR_LDS_CASE(10) CUSR_LDS_CASE(11) CUSR_LDS_CASE(12) CUSR_LDS_CASE(13)
@@ -195,12 +200,12 @@ size_t lds_for_k(int K, int D, int slots, int tape) {
     }
 }
 
-size_t fit_lds_bytes(bool mixed, bool rev, int K, int D, int slots, int tape) {
+size_t fit_lds_bytes(bool mixed, bool rev, int K, int N, int D, int slots, int tape) {
     if (mixed)
-        return rev ? lds_for_k<float, CO_AD_REVERSE>(K, D, slots, tape)
-                   : lds_for_k<float, CO_AD_FORWARD>(K, D, slots, tape);
-    return rev ? lds_for_k<double, CO_AD_REVERSE>(K, D, slots, tape)
-               : lds_for_k<double, CO_AD_FORWARD>(K, D, slots, tape);
+        return rev ? lds_for_k<float, CO_AD_REVERSE>(K, N, D, slots, tape)
+                   : lds_for_k<float, CO_AD_FORWARD>(K, N, D, slots, tape);
+    return rev ? lds_for_k<double, CO_AD_REVERSE>(K, N, D, slots, tape)
+               : lds_for_k<double, CO_AD_FORWARD>(K, N, D, slots, tape);
 }
 
 // Check, decode and upload one population into the context (fp32 or fp64
@@ -384,7 +389,7 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         // per-wavefront areas, then the partition sums; fewer wavefronts per
         // workgroup (each summing several partitions) when LDS is short
         const size_t wave_bytes =
-            (fit_lds_bytes(mixed, rev, k, plan.D, b.slots, b.tape) + 15) & ~(size_t)15;
+            (fit_lds_bytes(mixed, rev, k, plan.N, plan.D, b.slots, b.tape) + 15) & ~(size_t)15;
         hipStream_t ks = li < kExtraStreams ? ctx->lanes[li] : s;
         if (li < kExtraStreams && !lane_used[li]) {
             CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));

@@ -17,9 +17,17 @@ hipError_t CUSR_FIT_LAUNCH(int K, unsigned grid, size_t lds, hipStream_t s, cons
         ((fa.resume || fa.it_end < fa.max_iter) && !fa.state))
         return hipErrorInvalidValue;
     switch (K) {
-#define CUSR_CASE(k)                                                                   \
-    case k:                                                                            \
-        lm_fit_kernel<k, CUSR_FIT_R, CUSR_FIT_AD><<<grid, kLanes * fa.pwaves, lds, s>>>(fa); \
+// the large-N instance where its tables differ (large_n_variant), chosen by N
+#define CUSR_CASE(k)                                                                        \
+    case k:                                                                                 \
+        if constexpr (large_n_variant<CUSR_FIT_R, k, CUSR_FIT_AD>()) {                      \
+            if (fa.N >= kLargeN) {                                                          \
+                lm_fit_kernel<k, CUSR_FIT_R, CUSR_FIT_AD, 1>                                \
+                    <<<grid, kLanes * fa.pwaves, lds, s>>>(fa);                             \
+                break;                                                                      \
+            }                                                                               \
+        }                                                                                   \
+        lm_fit_kernel<k, CUSR_FIT_R, CUSR_FIT_AD, 0><<<grid, kLanes * fa.pwaves, lds, s>>>(fa); \
         break;
         CUSR_CASE(0) CUSR_CASE(1) CUSR_CASE(2) CUSR_CASE(3) CUSR_CASE(4) CUSR_CASE(5)
         CUSR_CASE(6) CUSR_CASE(7) CUSR_CASE(8) CUSR_CASE(9) CUSR_CASE(10) CUSR_CASE(11)

@@ -53,20 +53,31 @@ constexpr float kCexpCap32 = 485165184.0f;         // exp(20) rounded to float
 #ifndef CUSR_PREV_TABLE
 #define CUSR_PREV_TABLE 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
+// fp64 forward AD from kLargeN points on (C4's N = 100,000): each pass streams
+// y from memory, and two points per lane with three waves per SIMD at K = 5, 6
+// hide the loads better (C4 -6 %; at N = 1,024 four points measured faster).
+// Points per pass do not change any summation order.
+#ifndef CUSR_P64_LARGE_N_TABLE
+#define CUSR_P64_LARGE_N_TABLE 4, 4, 4, 4, 4, 2, 2, 4, 4, 1, 1, 1, 1, 1, 1, 1, 1
+#endif
+constexpr int kLargeN = 16384;
 constexpr int kP64[CO_MAX_K + 1] = {CUSR_P64_TABLE};
+constexpr int kP64LargeN[CO_MAX_K + 1] = {CUSR_P64_LARGE_N_TABLE};
 constexpr int kP32[CO_MAX_K + 1] = {CUSR_P32_TABLE};
 constexpr int kPRev[CO_MAX_K + 1] = {CUSR_PREV_TABLE};   // reverse AD (tape in LDS)
-template <typename R, int K, int AD>
+template <typename R, int K, int AD, int LN = 0>
 constexpr int points_per_pass() {
-    return (AD == CO_AD_REVERSE) ? kPRev[K] : (sizeof(R) == 4) ? kP32[K] : kP64[K];
+    return (AD == CO_AD_REVERSE) ? kPRev[K]
+           : (sizeof(R) == 4)    ? kP32[K]
+                                 : (LN ? kP64LargeN[K] : kP64[K]);
 }
 
 // Points per lane of the mixed-precision fit's fp64 guard passes: as many as
 // fit the LDS bytes of the fit's own passes (fp32 at P points -> fp64 at P/2).
-template <typename R, int K, int AD>
+template <typename R, int K, int AD, int LN = 0>
 constexpr int audit_points() {
-    return points_per_pass<R, K, AD>() * (int)sizeof(R) / 8 > 0
-               ? points_per_pass<R, K, AD>() * (int)sizeof(R) / 8
+    return points_per_pass<R, K, AD, LN>() * (int)sizeof(R) / 8 > 0
+               ? points_per_pass<R, K, AD, LN>() * (int)sizeof(R) / 8
                : 1;
 }
 
@@ -860,10 +871,10 @@ static_assert(sums_width(CO_MAX_K) <= kStateStride - kStateSums, "state row too 
 // internal states, mapped to STATUS_* at the end (lm_core.cuh:46-56)
 enum { ST_RUN = 0, ST_CONV = 1, ST_NAN = 2, ST_K0 = 3, ST_CHOL = 4 };
 
-template <int K, typename R, int AD>
+template <int K, typename R, int AD, int LN>
 __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, double *lds_c, double *lds_s,
                         char *lds_dyn, int lane, int wave) {
-    constexpr int P = points_per_pass<R, K, AD>();
+    constexpr int P = points_per_pass<R, K, AD, LN>();
     constexpr int JAC = (K == 0) ? 0 : (AD == CO_AD_REVERSE ? 2 : 1);
     char *my_lds = lds_dyn + (size_t)wave * fa.wave_bytes;
     const bool lead = wave == 0;     // the wavefront that writes shared state
@@ -1003,7 +1014,7 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
         // value pass reuses the same LDS bytes per row and lane (half the
         // points of the fp32 passes). A lane's points are summed in the same
         // ascending order at any number of points per pass.
-        constexpr int AP = audit_points<R, K, AD>();
+        constexpr int AP = audit_points<R, K, AD, LN>();
         WaveLds<double, AP> w64;
         w64.x = (double *)my_lds;
         w64.slot = w64.x + (size_t)fa.D * AP * kLanes;
@@ -1046,17 +1057,29 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
 #ifndef CUSR_WREV64_TABLE
 #define CUSR_WREV64_TABLE 1, 1, 1, 1, 1, 1, 1, 1, 1, 2, 1, 1, 1, 1, 1, 1, 1
 #endif
+#ifndef CUSR_W64_LARGE_N_TABLE
+#define CUSR_W64_LARGE_N_TABLE 1, 1, 1, 2, 2, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1
+#endif
 #ifndef CUSR_WAVES_OTHER
 #define CUSR_WAVES_OTHER 1
 #endif
 constexpr int kW64[CO_MAX_K + 1] = {CUSR_W64_TABLE};
+constexpr int kW64LargeN[CO_MAX_K + 1] = {CUSR_W64_LARGE_N_TABLE};
 constexpr int kWRev64[CO_MAX_K + 1] = {CUSR_WREV64_TABLE};
-template <typename R, int K, int AD>
+template <typename R, int K, int AD, int LN = 0>
 constexpr int waves_per_eu() {
-    return sizeof(R) == 8 ? (AD == CO_AD_FORWARD ? kW64[K] : kWRev64[K]) : CUSR_WAVES_OTHER;
+    return sizeof(R) == 8 ? (AD == CO_AD_FORWARD ? (LN ? kW64LargeN[K] : kW64[K]) : kWRev64[K])
+                          : CUSR_WAVES_OTHER;
 }
-template <int K, typename R, int AD>
-__global__ void __launch_bounds__(kLanes * CO_MAX_PARTITIONS, (waves_per_eu<R, K, AD>()))
+// True when the large-N tables give (R, K, AD) another kernel (only those
+// get an LN = 1 instance).
+template <typename R, int K, int AD>
+constexpr bool large_n_variant() {
+    return points_per_pass<R, K, AD, 1>() != points_per_pass<R, K, AD, 0>() ||
+           waves_per_eu<R, K, AD, 1>() != waves_per_eu<R, K, AD, 0>();
+}
+template <int K, typename R, int AD, int LN = 0>
+__global__ void __launch_bounds__(kLanes * CO_MAX_PARTITIONS, (waves_per_eu<R, K, AD, LN>()))
 lm_fit_kernel(FitArgs fa) {
     __shared__ double lds_c[2 * CO_MAX_K];
     __shared__ double lds_s[2 * sums_width(CO_MAX_K)];
@@ -1064,15 +1087,16 @@ lm_fit_kernel(FitArgs fa) {
     const ExprDesc e = fa.desc[blockIdx.x];
     const int lane = (int)threadIdx.x & (kLanes - 1);
     const int wave = uni((int)threadIdx.x >> 6);
-    fit_one<K, R, AD>(fa, e, lds_c, lds_s, lds_dyn, lane, wave);
+    fit_one<K, R, AD, LN>(fa, e, lds_c, lds_s, lds_dyn, lane, wave);
 }
 
 // Dynamic LDS bytes one wavefront of a fit launch needs (the mixed-precision
 // fp64 audit pass reuses the same bytes at audit_points per lane).
-template <typename R, int K, int AD>
+template <typename R, int K, int AD, int LN = 0>
 constexpr size_t fit_lds_bytes_t(int D, int slots, int tape) {
-    const size_t a = (size_t)(D + slots + tape) * points_per_pass<R, K, AD>() * kLanes * sizeof(R);
-    const size_t b = (size_t)(D + slots) * audit_points<R, K, AD>() * kLanes * sizeof(double);
+    const size_t a =
+        (size_t)(D + slots + tape) * points_per_pass<R, K, AD, LN>() * kLanes * sizeof(R);
+    const size_t b = (size_t)(D + slots) * audit_points<R, K, AD, LN>() * kLanes * sizeof(double);
     return (matrix_sums<K, AD>() ? kJtBytes + (size_t)K * (K + 1) * sizeof(double) : 0) +
            (a > b ? a : b);
 }
