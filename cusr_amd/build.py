@@ -57,8 +57,10 @@ def build(jobs: int | None = None, verbose: bool = False, defines=(), out: Path 
     """Compile everything; `defines` adds -D flags (tuning variants) and `out`
     redirects the library (the CLI is only built for the default library)."""
     extra = [f"-D{d}" for d in defines]
-    # CUSR_EXTRA_HIPCC_FLAGS: more device-compile flags for tuning builds
-    extra += os.environ.get("CUSR_EXTRA_HIPCC_FLAGS", "").split()
+    # CUSR_EXTRA_HIPCC_FLAGS: more device-compile flags, for redirected (tuning)
+    # builds only; the shipped libraries never pick them up from the environment
+    if out is not None:
+        extra += os.environ.get("CUSR_EXTRA_HIPCC_FLAGS", "").split()
     lib = Path(out) if out is not None else LIB
     # a redirected build keeps its objects apart, so builds can run side by side
     bdir = BUILD if out is None else BUILD / Path(out).stem

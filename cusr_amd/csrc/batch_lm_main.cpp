@@ -148,11 +148,10 @@ int main(int argc, char **argv) {
                pop_path, h.M_prob, h.total_nodes, h.total_c, h.N, h.n_vars, h.K_max,
                h.max_stack);
     const int rc0 = co_decode(&h, p.nt.data(), p.nv.data(), p.ci.data(), p.metas.data(), nullptr,
-                              nullptr, nullptr, nullptr);
+                              nullptr, nullptr, nullptr, nullptr, nullptr);
     if (rc0 == CO_ERR_BOUNDS) {
         fprintf(stderr, "[batch-lm] population beyond device bounds (K<=%d, stack<=%d, "
-                        "n_vars<=%d, nodes<=%d)\n", CO_MAX_K, CO_MAX_STACK, CO_MAX_VARS,
-                CO_MAX_NODES);
+                        "n_vars<=%d)\n", CO_MAX_K, CO_MAX_STACK, CO_MAX_VARS);
         return 2;
     }
     if (rc0 != CO_OK) {
@@ -172,6 +171,9 @@ int main(int argc, char **argv) {
     opt.max_iter = max_iter;
     opt.ad_mode = rev ? CO_AD_REVERSE : CO_AD_FORWARD;
     opt.precision = mixed ? CO_PREC_MIXED : CO_PREC_FP64;
+    // a float32 (v1) population fits as the reference's fp32 fit does: no
+    // constant beyond the fp32 range; a float64 (v2) one in full fp64
+    opt.f32_range = (pop_flags(&h) & POP_FLAG_F64) ? 0 : 1;
     int rc = co_optimize_ex(handle, &opt, &h, p.nt.data(), p.nv.data(), p.ci.data(),
                             p.metas.data(), p.c_init.data(), p.xs.data(), p.ym.data(), cf.data(),
                             status.data(), li.data(), lf.data(), iters.data());
@@ -180,9 +182,15 @@ int main(int argc, char **argv) {
         fprintf(stderr, "[batch-lm] fit failed (code %d)\n", rc);
         return rc == CO_ERR_BOUNDS ? 2 : 1;
     }
+    // float32 blobs: an expression whose fitted constants overflow fp32 gets
+    // its c_init back, as co_optimize does
     std::vector<float> cf32(C > 0 ? C : 1), li32(M > 0 ? M : 1), lf32(M > 0 ? M : 1);
-    for (size_t j = 0; j < C; j++) cf32[j] = (float)cf[j];
-    for (size_t m = 0; m < M; m++) { li32[m] = (float)li[m]; lf32[m] = (float)lf[m]; }
+    rc = co_narrow_fp32(&h, p.metas.data(), p.c_init.data(), cf.data(), li.data(), lf.data(),
+                        status.data(), cf32.data(), li32.data(), lf32.data());
+    if (rc < 0) {
+        fprintf(stderr, "[batch-lm] narrowing failed (code %d)\n", rc);
+        return 1;
+    }
     bool ok = write_blob(out_dir + "/status.bin", status.data(), 4 * M) &&
               write_blob(out_dir + "/c_final.bin", cf32.data(), 4 * C) &&
               write_blob(out_dir + "/loss_final.bin", lf32.data(), 4 * M) &&

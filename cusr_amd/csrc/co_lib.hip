@@ -13,6 +13,7 @@
 #include <string.h>
 #include <time.h>
 
+#include <cmath>
 #include <new>
 #include <vector>
 
@@ -96,22 +97,23 @@ struct Ctx {
     hipEvent_t ev_start = nullptr;
     hipEvent_t ev_done[kExtraStreams] = {};
     hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr;  // timing pair around the fit launches
-    hipEvent_t ev_b0[CO_MAX_K + 1] = {}, ev_b1[CO_MAX_K + 1] = {};  // per K-bin launch
-    bool bin_launched[CO_MAX_K + 1] = {};
+    hipEvent_t ev_b0[CO_BINS] = {}, ev_b1[CO_BINS] = {};  // per bin launch
+    bool bin_launched[CO_BINS] = {};
     Plan plan = {};
     bool resident = false;
     bool shared_y = false;   // the resident y is one row for every expression
     bool on_data = false;    // the resident population fits the uploaded data set
     int data_N = -1, data_D = 0;  // shape of the uploaded data set (-1: none)
     double last_kernel_ms = -1.0;
-    double last_bin_ms[CO_MAX_K + 1] = {};
-    size_t max_dyn_lds = 0;  // dynamic LDS one workgroup may use on this device
+    double last_bin_ms[CO_BINS] = {};
+    size_t lds_per_block = 0;  // LDS one workgroup may use on this device
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
     DevBuf data_X, data_Y;   // co_data_upload: X [D][N] column-major, y [N]
     DevBuf state;            // loop state of fits paused between segments
     HostBuf<uint64_t> h_prog;
     HostBuf<ExprDesc> h_desc;
-    std::vector<double> h_c, h_li, h_lf;
+    std::vector<double> h_c, h_li, h_lf, h_c0;   // co_optimize: fp64 results, c_init
+    std::vector<float> h_li32, h_lf32;
 };
 
 #define CO_HIP(call)                                                                    \
@@ -177,9 +179,12 @@ T *ptr(DevBuf &b) { return (T *)b.p; }
 
 unsigned blocks_for(size_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
 
-// static LDS of the fit kernel (constants and pass sums), kept out of the
-// dynamic budget
-constexpr size_t kStaticLds = 2 * CO_MAX_K * 8 + 2 * 153 * 8;
+// dynamic LDS a workgroup of a fit kernel family may use: the device's LDS
+// per workgroup less the family's static arrays (constants and pass sums)
+size_t max_dyn_lds(const Ctx *ctx, bool gen) {
+    const size_t st = fit_static_lds(gen);
+    return ctx->lds_per_block > st ? ctx->lds_per_block - st : 0;
+}
 
 // the launcher's choice of instance (fit_kernels.hip): the large-N one from
 // kLargeN points where its tables differ
@@ -201,6 +206,9 @@ size_t lds_for_k(int K, int N, int D, int slots, int tape) {
 }
 
 size_t fit_lds_bytes(bool mixed, bool rev, int K, int N, int D, int slots, int tape) {
+    if (K == CO_GENERAL_BIN)
+        return mixed ? fit_lds_bytes_gen<float>(D, slots, tape)
+                     : fit_lds_bytes_gen<double>(D, slots, tape);
     if (mixed)
         return rev ? lds_for_k<float, CO_AD_REVERSE>(K, N, D, slots, tape)
                    : lds_for_k<float, CO_AD_FORWARD>(K, N, D, slots, tape);
@@ -218,10 +226,11 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
     CO_HIP(hipSetDevice(ctx->device));
     ctx->resident = false;
     const int M = h->M_prob;
-    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? (size_t)h->total_nodes : 1);
+    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1);
     CO_GROW_HOST(ctx->h_desc, M > 0 ? (size_t)M : 1);
     int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
-                               ctx->h_desc.data(), nullptr, nullptr, &ctx->plan);
+                               ctx->h_desc.data(), nullptr, nullptr, nullptr, nullptr,
+                               &ctx->plan);
     if (rc != CO_OK) return rc;
     if (on_data && (ctx->data_N < 0 || h->N != ctx->data_N || h->n_vars != ctx->data_D))
         return CO_ERR_DATA;
@@ -236,7 +245,8 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
     const size_t nX = on_data ? 0 : (size_t)N * D;
     const size_t nY = on_data ? 0 : shared_y ? (size_t)N : (size_t)M * N;
     const size_t esz = in32 ? 4 : 8;
-    CO_GROW(ctx->prog, sizeof(uint64_t) * h->total_nodes);
+    const size_t words = (size_t)ctx->plan.words;
+    CO_GROW(ctx->prog, sizeof(uint64_t) * words);
     CO_GROW(ctx->desc, sizeof(ExprDesc) * M);
     CO_GROW(ctx->X, sizeof(double) * nX);
     CO_GROW(ctx->Y, sizeof(double) * nY);
@@ -252,8 +262,9 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
     CO_GROW(ctx->stage, stage);
     hipStream_t s = ctx->stream;
 
-    CO_HIP(hipMemcpyAsync(ctx->prog.p, ctx->h_prog.data(), sizeof(uint64_t) * h->total_nodes,
-                          hipMemcpyHostToDevice, s));
+    if (words)
+        CO_HIP(hipMemcpyAsync(ctx->prog.p, ctx->h_prog.data(), sizeof(uint64_t) * words,
+                              hipMemcpyHostToDevice, s));
     CO_HIP(hipMemcpyAsync(ctx->desc.p, ctx->h_desc.data(), sizeof(ExprDesc) * M,
                           hipMemcpyHostToDevice, s));
     // xs: row-major host array -> column-major fp64 on the device
@@ -290,6 +301,15 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
     return CO_OK;
 }
 
+// One launch of a fit: its bin, workgroups, LDS and stream (planned before
+// anything is launched, so a launch that cannot fit is refused up front).
+struct LaunchPlan {
+    int bin, pos, cnt, slots, tape, kmax, stream;
+    size_t wave_bytes;
+    int pwaves[2];
+    size_t lds[2];
+};
+
 // Fit the resident population; copy results to the host pointers that are
 // non-null (c_out and status_out too may be null: results then stay on the
 // device). Returns after the device work and copies are complete.
@@ -308,7 +328,7 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     const Plan &plan = ctx->plan;
     const int M = plan.M, C = plan.total_c;
     ctx->last_kernel_ms = 0.0;
-    for (int k = 0; k <= CO_MAX_K; ++k) {
+    for (int k = 0; k < CO_BINS; ++k) {
         ctx->bin_launched[k] = false;
         ctx->last_bin_ms[k] = -1.0;
     }
@@ -330,6 +350,7 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     fa.max_iter = opt.max_iter;
     fa.guard = opt.fp64_guard ? 1 : 0;
     fa.shared_y = ctx->shared_y ? 1 : 0;
+    fa.f32_range = opt.f32_range ? 1 : 0;
     fa.lm_order = opt.lm_order;
     fa.lambda0 = opt.lambda0;
     fa.xtol = opt.xtol;
@@ -347,83 +368,113 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         seg[0].it_end = tail_it;
         seg[1] = {tail_parts, opt.max_iter, 1};
         nseg = 2;
-        CO_GROW(ctx->state, sizeof(double) * kStateStride * (size_t)M);
     }
-    fa.state = tail_it > 0 ? ptr<double>(ctx->state) : nullptr;
-    const FitLauncher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
-                                     : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
-    // descriptors are in launch order, largest K first; one launch per K bin,
-    // bins spread over the context's streams so their tails overlap
-    CO_HIP(hipEventRecord(ctx->ev_t0, s));
-    CO_HIP(hipEventRecord(ctx->ev_start, s));
-    // K bins: launch position, size and LDS rows, then a stream each,
+    // bins in launch order (descriptors are in launch order): the general
+    // kernel's bin, then the fast K bins, largest K first; then a stream each,
     // longest first onto the least loaded stream, a bin's cost taken as
-    // count x (K + 3) (measured per-bin times grow about so with K);
-    // stream kExtraStreams is the handle's own
-    struct Bin { int pos, cnt, slots, tape, stream; } bins[CO_MAX_K + 1];
+    // count x (K + 3) (measured per-bin times grow about so with K; the
+    // general kernel's one point per lane counts four times); stream
+    // kExtraStreams is the handle's own
+    LaunchPlan lp[CO_BINS];
+    int nl = 0, kmax = 0;
     double load[kStreams] = {};
-    for (int k = CO_MAX_K, pos = 0; k >= 0; --k) {
-        Bin &b = bins[k];
-        b = {pos, 0, 0, 0, -1};
-        while (pos < M && ctx->h_desc[pos].K == k) {
+    for (int i = 0, pos = 0; i < CO_BINS; ++i) {
+        const int bin = i == 0 ? CO_GENERAL_BIN : CO_FAST_MAX_K - (i - 1);
+        const bool gen = bin == CO_GENERAL_BIN;
+        LaunchPlan b = {};
+        b.bin = bin;
+        b.pos = pos;
+        double cost = 0.0;
+        while (pos < M && (gen ? ctx->h_desc[pos].gen != 0
+                               : (!ctx->h_desc[pos].gen && ctx->h_desc[pos].K == bin))) {
             const ExprDesc &d = ctx->h_desc[pos];
             if (d.slots > b.slots) b.slots = d.slots;
             if (d.tape > b.tape) b.tape = d.tape;
+            if (d.K > b.kmax) b.kmax = d.K;
+            cost += (double)(d.K + 3) * (gen ? 4.0 : 1.0);
             ++b.cnt;
             ++pos;
         }
         if (b.cnt == 0) continue;
         if (!rev) b.tape = 0;
+        if (b.kmax > kmax) kmax = b.kmax;
         int li = 0;
-        for (int i = 1; i < kStreams; ++i)
-            if (load[i] < load[li]) li = i;
-        load[li] += (double)b.cnt * (k + 3);
+        for (int j = 1; j < kStreams; ++j)
+            if (load[j] < load[li]) li = j;
+        load[li] += cost;
         b.stream = li;
-    }
-    // launched largest K first (small-K bins first measured slower on C2)
-    bool lane_used[kExtraStreams] = {};
-    for (int k = CO_MAX_K; k >= 0; --k) {
-        const Bin &b = bins[k];
-        if (b.cnt == 0) continue;
-        const int cnt = b.cnt, li = b.stream;
         // per-wavefront areas, then the partition sums; fewer wavefronts per
         // workgroup (each summing several partitions) when LDS is short
-        const size_t wave_bytes =
-            (fit_lds_bytes(mixed, rev, k, plan.N, plan.D, b.slots, b.tape) + 15) & ~(size_t)15;
-        hipStream_t ks = li < kExtraStreams ? ctx->lanes[li] : s;
-        if (li < kExtraStreams && !lane_used[li]) {
-            CO_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
-            lane_used[li] = true;
-        }
-        CO_HIP(hipEventRecord(ctx->ev_b0[k], ks));
-        // K = 0 expressions have no iterations, so no tail either
-        for (int g = 0; g < (k == 0 ? 1 : nseg); ++g) {
+        b.wave_bytes =
+            (fit_lds_bytes(mixed, rev, bin, plan.N, plan.D, b.slots, b.tape) + 15) & ~(size_t)15;
+        const size_t cap = max_dyn_lds(ctx, gen);
+        const int ks = gen ? b.kmax : bin;
+        for (int g = 0; g < (b.kmax == 0 ? 1 : nseg); ++g) {
             const int sp = seg[g].parts;
-            const size_t part_bytes = sp > 1 ? (size_t)sp * (1 + k + k * (k + 1) / 2) * 8 : 0;
-            int pwaves = sp;
-            while (pwaves > 1 && pwaves * wave_bytes + part_bytes > ctx->max_dyn_lds) pwaves /= 2;
-            const size_t lds = pwaves * wave_bytes + part_bytes;
-            if (lds > ctx->max_dyn_lds) return CO_ERR_BOUNDS;
+            const size_t part_bytes = sp > 1 ? (size_t)sp * sums_width(ks) * 8 : 0;
+            int pw = sp;
+            while (pw > 1 && pw * b.wave_bytes + part_bytes > cap) pw /= 2;
+            b.pwaves[g] = pw;
+            b.lds[g] = pw * b.wave_bytes + part_bytes;
+            if (b.lds[g] > cap) return CO_ERR_BOUNDS;   // before any launch
+        }
+        lp[nl++] = b;
+    }
+    const int stride = state_stride_for(kmax);
+    if (tail_it > 0) CO_GROW(ctx->state, sizeof(double) * stride * (size_t)M);
+    fa.state = tail_it > 0 ? ptr<double>(ctx->state) : nullptr;
+    fa.state_stride = stride;
+    const FitLauncher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
+                                     : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
+    bool lane_used[kExtraStreams] = {};
+    // after the first launch an error must not return with work still running
+    // on the lanes: they are joined first
+    auto fail = [&](hipError_t e, int line) {
+        fprintf(stderr, "[cusr_co] HIP error %s at %s:%d\n", hipGetErrorString(e), __FILE__,
+                line);
+        for (int i = 0; i < kExtraStreams; ++i)
+            if (lane_used[i]) (void)hipStreamSynchronize(ctx->lanes[i]);
+        (void)hipStreamSynchronize(s);
+        return CO_ERR_CUDA;
+    };
+#define CO_LAUNCH_HIP(call)                          \
+    do {                                             \
+        hipError_t e_ = (call);                      \
+        if (e_ != hipSuccess) return fail(e_, __LINE__); \
+    } while (0)
+    CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t0, s));
+    CO_LAUNCH_HIP(hipEventRecord(ctx->ev_start, s));
+    for (int i = 0; i < nl; ++i) {
+        const LaunchPlan &b = lp[i];
+        hipStream_t ks = b.stream < kExtraStreams ? ctx->lanes[b.stream] : s;
+        if (b.stream < kExtraStreams && !lane_used[b.stream]) {
+            lane_used[b.stream] = true;
+            CO_LAUNCH_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
+        }
+        CO_LAUNCH_HIP(hipEventRecord(ctx->ev_b0[b.bin], ks));
+        // K = 0 expressions have no iterations, so no tail either
+        for (int g = 0; g < (b.kmax == 0 ? 1 : nseg); ++g) {
             FitArgs fk = fa;
             fk.desc = fa.desc + b.pos;
             fk.slots = b.slots;
             fk.tape = b.tape;
-            fk.parts = sp;
-            fk.pwaves = pwaves;
-            fk.wave_bytes = (int)wave_bytes;
+            fk.parts = seg[g].parts;
+            fk.pwaves = b.pwaves[g];
+            fk.wave_bytes = (int)b.wave_bytes;
             fk.it_end = seg[g].it_end;
             fk.resume = seg[g].resume;
-            CO_HIP(launch(k, (unsigned)cnt, lds, ks, fk));
+            CO_LAUNCH_HIP(launch(b.bin, (unsigned)b.cnt, b.lds[g], ks, fk));
         }
-        CO_HIP(hipEventRecord(ctx->ev_b1[k], ks));
-        ctx->bin_launched[k] = true;
+        CO_LAUNCH_HIP(hipEventRecord(ctx->ev_b1[b.bin], ks));
+        ctx->bin_launched[b.bin] = true;
     }
     for (int i = 0; i < kExtraStreams; ++i) {
         if (!lane_used[i]) continue;
-        CO_HIP(hipEventRecord(ctx->ev_done[i], ctx->lanes[i]));
-        CO_HIP(hipStreamWaitEvent(s, ctx->ev_done[i], 0));
+        CO_LAUNCH_HIP(hipEventRecord(ctx->ev_done[i], ctx->lanes[i]));
+        CO_LAUNCH_HIP(hipStreamWaitEvent(s, ctx->ev_done[i], 0));
     }
-    CO_HIP(hipEventRecord(ctx->ev_t1, s));
+    CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t1, s));
+#undef CO_LAUNCH_HIP
     if (c_out && C) CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, hipMemcpyDeviceToHost, s));
     if (status_out)
         CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M, hipMemcpyDeviceToHost, s));
@@ -435,7 +486,7 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     float ms = 0.0f;
     CO_HIP(hipEventElapsedTime(&ms, ctx->ev_t0, ctx->ev_t1));
     ctx->last_kernel_ms = ms;
-    for (int k = 0; k <= CO_MAX_K; ++k) {
+    for (int k = 0; k < CO_BINS; ++k) {
         if (!ctx->bin_launched[k]) continue;
         CO_HIP(hipEventElapsedTime(&ms, ctx->ev_b0[k], ctx->ev_b1[k]));
         ctx->last_bin_ms[k] = ms;
@@ -492,14 +543,14 @@ extern "C" int co_init(int device_id, void **handle_out) {
     hipError_t e = hipDeviceGetAttribute(&lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock,
                                          device_id);
     if (e == hipSuccess)
-        ctx->max_dyn_lds = lds_per_block > (int)kStaticLds ? (size_t)lds_per_block - kStaticLds : 0;
+        ctx->lds_per_block = lds_per_block > 0 ? (size_t)lds_per_block : 0;
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     for (int i = 0; i < kExtraStreams && e == hipSuccess; ++i)
         e = hipStreamCreateWithFlags(&ctx->lanes[i], hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t0);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t1);
-    for (int k = 0; k <= CO_MAX_K && e == hipSuccess; ++k) {
+    for (int k = 0; k < CO_BINS && e == hipSuccess; ++k) {
         e = hipEventCreate(&ctx->ev_b0[k]);
         if (e == hipSuccess) e = hipEventCreate(&ctx->ev_b1[k]);
     }
@@ -525,6 +576,7 @@ extern "C" int co_optimize(void *handle, const PopHeader *h, const int32_t *nt, 
     CoOptions opt;
     co_options_default(&opt);
     opt.max_iter = max_iter;
+    opt.f32_range = 1;   // the reference fits in fp32: no constant beyond its range
     const int M = h->M_prob > 0 ? h->M_prob : 0;
     const int C = h->total_c > 0 ? h->total_c : 0;
     ctx->h_c.resize(C > 0 ? C : 1);
@@ -533,12 +585,57 @@ extern "C" int co_optimize(void *handle, const PopHeader *h, const int32_t *nt, 
     int rc = fit_common(ctx, opt, h, nt, nv, ci, metas, c_init, xs, ym, true, ctx->h_c.data(),
                         status_out, ctx->h_li.data(), ctx->h_lf.data(), nullptr);
     if (rc != CO_OK) return rc;
-    for (int j = 0; j < C; j++) c_final_out[j] = (float)ctx->h_c[j];
+    ctx->h_c0.resize(C > 0 ? C : 1);
+    for (int j = 0; j < C; j++) ctx->h_c0[j] = c_init[j];
+    ctx->h_li32.resize(M > 0 ? M : 1);
+    ctx->h_lf32.resize(M > 0 ? M : 1);
+    rc = co_narrow_fp32(h, metas, ctx->h_c0.data(), ctx->h_c.data(), ctx->h_li.data(),
+                        ctx->h_lf.data(), status_out, c_final_out, ctx->h_li32.data(),
+                        ctx->h_lf32.data());
+    if (rc < 0) return rc;
     for (int m = 0; m < M; m++) {
-        if (loss_init_out) loss_init_out[m] = (float)ctx->h_li[m];
-        if (loss_final_out) loss_final_out[m] = (float)ctx->h_lf[m];
+        if (loss_init_out) loss_init_out[m] = ctx->h_li32[m];
+        if (loss_final_out) loss_final_out[m] = ctx->h_lf32[m];
     }
     return CO_OK;
+}
+
+extern "C" int co_narrow_fp32(const PopHeader *h, const TreeMeta *metas, const double *c_init,
+                              const double *c_final, const double *loss_init,
+                              const double *loss_final, int32_t *status, float *c_out,
+                              float *loss_init_out, float *loss_final_out) {
+    if (!h || h->M_prob < 0 || h->total_c < 0) return CO_ERR_NULLARG;
+    const int M = h->M_prob, C = h->total_c;
+    if ((M > 0 && (!metas || !loss_init || !loss_final || !status || !loss_init_out ||
+                   !loss_final_out)) ||
+        (C > 0 && (!c_init || !c_final || !c_out)))
+        return CO_ERR_NULLARG;
+    for (int m = 0; m < M; m++) {
+        const TreeMeta &t = metas[m];
+        if (t.K < 0 || t.c_offset < 0 || (long)t.c_offset + t.K > (long)C) return CO_ERR_PROGRAM;
+    }
+    for (int j = 0; j < C; j++) c_out[j] = (float)c_final[j];
+    int demoted = 0;
+    for (int m = 0; m < M; m++) {
+        const TreeMeta &t = metas[m];
+        const float lf = (float)loss_final[m];
+        loss_init_out[m] = (float)loss_init[m];
+        loss_final_out[m] = lf;
+        if (t.K == 0) continue;
+        // a value the fp64 fit left finite that the fp32 carrier cannot hold
+        bool lost = std::isfinite(loss_final[m]) && !std::isfinite(lf);
+        for (int j = 0; j < t.K && !lost; j++) {
+            const double v = c_final[t.c_offset + j];
+            lost = std::isfinite(v) && !std::isfinite((float)v);
+        }
+        if (!lost) continue;
+        // as the fp64 guard treats a non-finite loss (lm_core.cuh:299-351)
+        for (int j = 0; j < t.K; j++) c_out[t.c_offset + j] = (float)c_init[t.c_offset + j];
+        loss_final_out[m] = (float)loss_init[m];
+        if (status[m] == STATUS_CONVERGED) status[m] = STATUS_MAXITER;
+        ++demoted;
+    }
+    return demoted;
 }
 
 extern "C" int co_optimize_ex(void *handle, const CoOptions *opt, const PopHeader *h,
@@ -581,15 +678,23 @@ extern "C" int co_data_upload(void *handle, int N, int n_vars, const double *xs,
     return CO_OK;
 }
 
-// True when p is device memory the handle's device can read (a torch CUDA
-// tensor's data on that device, for instance).
-static bool on_device(const void *p, int device) {
+// True when [p, p + bytes) is device memory of the handle's device, inside one
+// allocation (a torch CUDA tensor's storage on that device, for instance).
+static bool on_device(const void *p, size_t bytes, int device) {
     hipPointerAttribute_t a;
     if (hipPointerGetAttributes(&a, p) != hipSuccess) {
         (void)hipGetLastError();   // a pageable host pointer is not an error to keep
         return false;
     }
-    return a.type == hipMemoryTypeDevice && a.device == device;
+    if (a.type != hipMemoryTypeDevice || a.device != device) return false;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    const uintptr_t lo = (uintptr_t)base, at = (uintptr_t)p;
+    return at >= lo && bytes <= size && at - lo <= size - bytes;
 }
 
 extern "C" int co_data_upload_device(void *handle, int N, int n_vars, const double *xs_dev,
@@ -598,9 +703,10 @@ extern "C" int co_data_upload_device(void *handle, int N, int n_vars, const doub
     if (N > 0 && (!y_dev || (n_vars > 0 && !xs_dev))) return CO_ERR_NULLARG;
     Ctx *ctx = (Ctx *)handle;
     CO_HIP(hipSetDevice(ctx->device));
-    // every pointer checked before anything is copied
-    if (N > 0 && (!on_device(y_dev, ctx->device) ||
-                  (n_vars > 0 && !on_device(xs_dev, ctx->device))))
+    // every pointer and extent checked before anything is copied
+    if (N > 0 && (!on_device(y_dev, sizeof(double) * (size_t)N, ctx->device) ||
+                  (n_vars > 0 && !on_device(xs_dev, sizeof(double) * (size_t)N * n_vars,
+                                            ctx->device))))
         return CO_ERR_DATA;
     ctx->data_N = -1;   // no data set until this upload completes
     if (ctx->on_data) ctx->resident = false;
@@ -645,22 +751,27 @@ extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, c
     CO_HIP(hipSetDevice(ctx->device));
     ctx->resident = false;  // the evaluation reuses the population buffers
     const int M = h->M_prob;
-    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? (size_t)h->total_nodes : 1);
+    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1);
     CO_GROW_HOST(ctx->h_desc, M > 0 ? (size_t)M : 1);
+    Plan plan = {};
     int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
-                               ctx->h_desc.data(), nullptr, nullptr, nullptr);
+                               ctx->h_desc.data(), nullptr, nullptr, nullptr, nullptr, &plan);
     if (rc != CO_OK || M == 0) return rc;
     const int N = h->N, D = h->n_vars, C = h->total_c;
-    const size_t nX = (size_t)N * D, nY = (size_t)M * N;
-    CO_GROW(ctx->prog, sizeof(uint64_t) * h->total_nodes);
+    const size_t nX = (size_t)N * D, nY = (size_t)M * N, words = (size_t)plan.words;
+    // one workgroup per expression: inputs and spill slots of 64 points in LDS
+    const size_t lds = (size_t)(D + plan.max_slots) * kLanes * (precision == CO_PREC_FP64 ? 8 : 4);
+    if (lds + sizeof(double) * CO_MAX_K > ctx->lds_per_block) return CO_ERR_BOUNDS;
+    CO_GROW(ctx->prog, sizeof(uint64_t) * words);
     CO_GROW(ctx->desc, sizeof(ExprDesc) * M);
     CO_GROW(ctx->X, sizeof(double) * nX);
     CO_GROW(ctx->Y, sizeof(double) * nY);
     CO_GROW(ctx->C0, sizeof(double) * C);
     CO_GROW(ctx->stage, sizeof(double) * nX);
     hipStream_t s = ctx->stream;
-    CO_HIP(hipMemcpyAsync(ctx->prog.p, ctx->h_prog.data(), sizeof(uint64_t) * h->total_nodes,
-                          hipMemcpyHostToDevice, s));
+    if (words)
+        CO_HIP(hipMemcpyAsync(ctx->prog.p, ctx->h_prog.data(), sizeof(uint64_t) * words,
+                              hipMemcpyHostToDevice, s));
     CO_HIP(hipMemcpyAsync(ctx->desc.p, ctx->h_desc.data(), sizeof(ExprDesc) * M,
                           hipMemcpyHostToDevice, s));
     if (C) CO_HIP(hipMemcpyAsync(ctx->C0.p, c, 8 * (size_t)C, hipMemcpyHostToDevice, s));
@@ -672,21 +783,29 @@ extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, c
     }
     EvalArgs ea;
     ea.prog = ptr<uint64_t>(ctx->prog);
-    ea.desc = ptr<ExprDesc>(ctx->desc);
     ea.X = ptr<double>(ctx->X);
     ea.C = ptr<double>(ctx->C0);
     ea.Yout = ptr<double>(ctx->Y);
     ea.N = N;
     ea.D = D;
-    int slots = 0;
-    for (int m = 0; m < M; m++)
-        if (ctx->h_desc[m].slots > slots) slots = ctx->h_desc[m].slots;
-    const size_t lds = (size_t)(D + slots) * kLanes * (precision == CO_PREC_FP64 ? 8 : 4);
-    if (precision == CO_PREC_FP64)
-        eval_kernel<double><<<M, kLanes, lds, s>>>(ea);
-    else
-        eval_kernel<float><<<M, kLanes, lds, s>>>(ea);
-    CO_HIP(hipGetLastError());
+    // descriptors in launch order: the wide programs first, then the fast ones
+    const int ng = plan.n_gen, nf = M - plan.n_gen;
+    ea.desc = ptr<ExprDesc>(ctx->desc);
+    if (ng) {
+        if (precision == CO_PREC_FP64)
+            eval_kernel<double, WideFmt><<<ng, kLanes, lds, s>>>(ea);
+        else
+            eval_kernel<float, WideFmt><<<ng, kLanes, lds, s>>>(ea);
+        CO_HIP(hipGetLastError());
+    }
+    ea.desc = ptr<ExprDesc>(ctx->desc) + ng;
+    if (nf) {
+        if (precision == CO_PREC_FP64)
+            eval_kernel<double, FastFmt><<<nf, kLanes, lds, s>>>(ea);
+        else
+            eval_kernel<float, FastFmt><<<nf, kLanes, lds, s>>>(ea);
+        CO_HIP(hipGetLastError());
+    }
     if (nY) CO_HIP(hipMemcpyAsync(y_out, ctx->Y.p, 8 * nY, hipMemcpyDeviceToHost, s));
     CO_HIP(hipStreamSynchronize(s));
     return CO_OK;
@@ -694,16 +813,17 @@ extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, c
 
 extern "C" int co_decode(const PopHeader *h, const int32_t *nt, const float *nv,
                          const int32_t *ci, const TreeMeta *metas, uint64_t *program_out,
-                         int32_t *order_out, int32_t *bin_start_out, int32_t *stack_out) {
+                         int32_t *order_out, int32_t *bin_start_out, int32_t *stack_out,
+                         int32_t *program_off_out, int32_t *route_out) {
     if (!h) return CO_ERR_NULLARG;
     std::vector<uint64_t> tmp;
     uint64_t *prog = program_out;
     if (!prog) {
-        tmp.resize(h->total_nodes > 0 ? h->total_nodes : 1);
+        tmp.resize(h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1);
         prog = tmp.data();
     }
     return decode_population(h, nt, nv, ci, metas, prog, order_out, bin_start_out, nullptr,
-                             stack_out, nullptr, nullptr);
+                             stack_out, nullptr, program_off_out, route_out, nullptr);
 }
 
 extern "C" int co_upload_ex(void *handle, const PopHeader *h, const int32_t *nt,
@@ -734,7 +854,7 @@ extern "C" int co_last_kernel_ms(void *handle, double *fit_ms_out) {
 extern "C" int co_last_bin_ms(void *handle, double *bin_ms_out) {
     if (!handle || !bin_ms_out) return CO_ERR_NULLARG;
     const Ctx *ctx = (const Ctx *)handle;
-    for (int k = 0; k <= CO_MAX_K; ++k) bin_ms_out[k] = ctx->last_bin_ms[k];
+    for (int k = 0; k < CO_BINS; ++k) bin_ms_out[k] = ctx->last_bin_ms[k];
     return CO_OK;
 }
 
@@ -763,7 +883,7 @@ extern "C" void co_teardown(void *handle) {
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_t0) (void)hipEventDestroy(ctx->ev_t0);
     if (ctx->ev_t1) (void)hipEventDestroy(ctx->ev_t1);
-    for (int k = 0; k <= CO_MAX_K; ++k) {
+    for (int k = 0; k < CO_BINS; ++k) {
         if (ctx->ev_b0[k]) (void)hipEventDestroy(ctx->ev_b0[k]);
         if (ctx->ev_b1[k]) (void)hipEventDestroy(ctx->ev_b1[k]);
     }

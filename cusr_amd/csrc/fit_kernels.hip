@@ -1,5 +1,6 @@
 // fit_kernels.hip -- instantiates the fit kernels of one (precision, AD mode)
-// variant for K = 0..CO_MAX_K. Built four times with
+// variant: the fast kernels for K = 0..CO_FAST_MAX_K and the general kernel.
+// Built four times with
 //   -DCUSR_FIT_R=double|float -DCUSR_FIT_AD=0|1 -DCUSR_FIT_LAUNCH=<name>.
 #include "lm_device.h"
 
@@ -9,14 +10,14 @@
 
 namespace cusr {
 
-hipError_t CUSR_FIT_LAUNCH(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa) {
+hipError_t CUSR_FIT_LAUNCH(int bin, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa) {
     if (fa.pwaves < 1 || fa.pwaves > CO_MAX_PARTITIONS || fa.parts % fa.pwaves != 0)
         return hipErrorInvalidValue;
     // a segment that can pause or resume needs the state buffer
     if (fa.it_end < 0 || fa.it_end > fa.max_iter ||
         ((fa.resume || fa.it_end < fa.max_iter) && !fa.state))
         return hipErrorInvalidValue;
-    switch (K) {
+    switch (bin) {
 // the large-N instance where its tables differ (large_n_variant), chosen by N
 #define CUSR_CASE(k)                                                                        \
     case k:                                                                                 \
@@ -33,6 +34,9 @@ hipError_t CUSR_FIT_LAUNCH(int K, unsigned grid, size_t lds, hipStream_t s, cons
         CUSR_CASE(6) CUSR_CASE(7) CUSR_CASE(8) CUSR_CASE(9) CUSR_CASE(10) CUSR_CASE(11)
         CUSR_CASE(12) CUSR_CASE(13) CUSR_CASE(14) CUSR_CASE(15) CUSR_CASE(16)
 #undef CUSR_CASE
+    case CO_GENERAL_BIN:
+        lm_fit_gen_kernel<CUSR_FIT_R, CUSR_FIT_AD><<<grid, kLanes * fa.pwaves, lds, s>>>(fa);
+        break;
     default:
         return hipErrorInvalidValue;
     }

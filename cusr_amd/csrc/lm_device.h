@@ -31,6 +31,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/cusr_math.h"
 #include "program.h"
 
@@ -61,10 +63,10 @@ constexpr float kCexpCap32 = 485165184.0f;         // exp(20) rounded to float
 #define CUSR_P64_LARGE_N_TABLE 4, 4, 4, 4, 4, 2, 2, 4, 4, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
 constexpr int kLargeN = 16384;
-constexpr int kP64[CO_MAX_K + 1] = {CUSR_P64_TABLE};
-constexpr int kP64LargeN[CO_MAX_K + 1] = {CUSR_P64_LARGE_N_TABLE};
-constexpr int kP32[CO_MAX_K + 1] = {CUSR_P32_TABLE};
-constexpr int kPRev[CO_MAX_K + 1] = {CUSR_PREV_TABLE};   // reverse AD (tape in LDS)
+constexpr int kP64[CO_FAST_MAX_K + 1] = {CUSR_P64_TABLE};
+constexpr int kP64LargeN[CO_FAST_MAX_K + 1] = {CUSR_P64_LARGE_N_TABLE};
+constexpr int kP32[CO_FAST_MAX_K + 1] = {CUSR_P32_TABLE};
+constexpr int kPRev[CO_FAST_MAX_K + 1] = {CUSR_PREV_TABLE};   // reverse AD (tape in LDS)
 template <typename R, int K, int AD, int LN = 0>
 constexpr int points_per_pass() {
     return (AD == CO_AD_REVERSE) ? kPRev[K]
@@ -83,6 +85,56 @@ constexpr int audit_points() {
 
 // scalar-cache view of the program (constant address space)
 typedef const __attribute__((address_space(4))) uint64_t *ProgPtr;
+
+// The two program formats of program.h, read by the same interpreter: one
+// 64-bit word per instruction for the fast kernels, two for the general one.
+struct FastFmt {
+    typedef uint64_t W;
+    static __device__ __forceinline__ W load(ProgPtr p, int pc) { return p[pc]; }
+    static __device__ __forceinline__ int fid(W w) { return ins_fid(w); }
+    static __device__ __forceinline__ int binary(W w) { return ins_binary(w); }
+    static __device__ __forceinline__ int akind(W w) { return ins_akind(w); }
+    static __device__ __forceinline__ int aidx(W w) { return ins_aidx(w); }
+    static __device__ __forceinline__ int bkind(W w) { return ins_bkind(w); }
+    static __device__ __forceinline__ int bidx(W w) { return ins_bidx(w); }
+    static __device__ __forceinline__ int toslot(W w) { return ins_toslot(w); }
+    static __device__ __forceinline__ int didx(W w) { return ins_didx(w); }
+    static __device__ __forceinline__ int lo(W w) { return ins_lo(w); }
+    static __device__ __forceinline__ int mid(W w) { return ins_mid(w); }
+    static __device__ __forceinline__ int hi(W w) { return ins_hi(w); }
+    static __device__ __forceinline__ int tape(W w) { return ins_tape(w); }
+    static __device__ __forceinline__ int sel(W w) { return ins_sel(w); }
+    static __device__ __forceinline__ int scale_a(W w) { return ins_scale_a(w); }
+    static __device__ __forceinline__ int scale_b(W w) { return ins_scale_b(w); }
+    static __device__ __forceinline__ int tape_a(W w) { return ins_tape_a(w); }
+    static __device__ __forceinline__ int tape_b(W w) { return ins_tape_b(w); }
+};
+struct WideFmt {
+    typedef Wide W;
+    static __device__ __forceinline__ W load(ProgPtr p, int pc) {
+        W w;
+        w.a = p[2 * pc];
+        w.b = p[2 * pc + 1];
+        return w;
+    }
+    static __device__ __forceinline__ int fid(W w) { return wins_fid(w.a); }
+    static __device__ __forceinline__ int binary(W w) { return wins_binary(w.a); }
+    static __device__ __forceinline__ int akind(W w) { return wins_akind(w.a); }
+    static __device__ __forceinline__ int aidx(W w) { return wins_aidx(w.a); }
+    static __device__ __forceinline__ int bkind(W w) { return wins_bkind(w.a); }
+    static __device__ __forceinline__ int bidx(W w) { return wins_bidx(w.a); }
+    static __device__ __forceinline__ int toslot(W w) { return wins_toslot(w.a); }
+    static __device__ __forceinline__ int didx(W w) { return wins_didx(w.a); }
+    static __device__ __forceinline__ int lo(W w) { return wins_lo(w.b); }
+    static __device__ __forceinline__ int mid(W w) { return wins_mid(w.b); }
+    static __device__ __forceinline__ int hi(W w) { return wins_hi(w.b); }
+    static __device__ __forceinline__ int tape(W w) { return wins_tape(w.b); }
+    static __device__ __forceinline__ int sel(W w) { return wins_sel(w.a); }
+    static __device__ __forceinline__ int scale_a(W w) { return wins_scale_a(w.a); }
+    static __device__ __forceinline__ int scale_b(W w) { return wins_scale_b(w.a); }
+    static __device__ __forceinline__ int tape_a(W w) { return wins_tape_a(w.a); }
+    static __device__ __forceinline__ int tape_b(W w) { return wins_tape_b(w.a); }
+};
 
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ double uni(double v) {
@@ -400,21 +452,37 @@ __device__ __forceinline__ void scale_entries(R *T, const R *d, const uint64_t *
 template <int K, typename R, int P>
 __device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, const bool *z,
                                             bool sel) {
-    const uint32_t mask = ((1u << hi) - 1u) & ~((1u << lo) - 1u);
+    uint32_t mask;
+    if constexpr (K < 32) {
+        mask = ((1u << hi) - 1u) & ~((1u << lo) - 1u);
+    } else {   // hi up to 32: the shift is formed in 64 bits
+        mask = (uint32_t)(((uint64_t)1 << hi) - 1u) & ~(uint32_t)(((uint64_t)1 << lo) - 1u);
+    }
     uint64_t zm[P];
     CUSR_FOR_P zm[p] = __builtin_amdgcn_ballot_w64(z[p]);
     scale_entries<K, 0, R, P>(T, d, zm, mask, sel ? 1u : 0u);
 }
 
 // T[p*K + k] += v[p] for a wave-uniform k (same branch scheme as scale_range).
+// The add sits in the asm of its branch: as plain C++ the compiler merges the
+// K branches into one add at a selected address, which puts T in scratch
+// memory. The arithmetic is the IEEE v_add_f64 / v_add_f32 of a plain add.
+template <typename R> struct AddAsm;
+template <> struct AddAsm<double> {
+    static __device__ __forceinline__ void run(double &t, double v) {
+        __asm__ volatile("v_add_f64 %0, %0, %1" : "+v"(t) : "v"(v));
+    }
+};
+template <> struct AddAsm<float> {
+    static __device__ __forceinline__ void run(float &t, float v) {
+        __asm__ volatile("v_add_f32 %0, %0, %1" : "+v"(t) : "v"(v));
+    }
+};
 template <int K, typename R, int P>
 __device__ __forceinline__ void add_tangent(R *T, int k, const R *v) {
 #pragma unroll
     for (int j = 0; j < K; ++j) {
-        if (j == k) {
-            __asm__ volatile("; add %0" ::"n"(j));
-            CUSR_FOR_P T[p * K + j] = T[p * K + j] + v[p];
-        }
+        if (j == k) CUSR_FOR_P AddAsm<R>::run(T[p * K + j], v[p]);
     }
 }
 
@@ -438,31 +506,31 @@ __device__ __forceinline__ void fetch(int kind, int idx, const R *acc, const Wav
 // JAC: 0 value only, 1 forward AD into T[p*K + j] (which must hold 1.0 on
 // entry: the tangent of constant k with respect to itself), 2 partials to the
 // tape.
-template <int K, typename R, int P, int JAC>
+template <int K, typename R, int P, int JAC, typename F = FastFmt>
 __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<R, P> &w,
                                              const double *cs, int lane, R *acc, R *T) {
     for (int pc = 0; pc < n; ++pc) {
-        const uint64_t ins = prog[pc];
-        const int fid = ins_fid(ins);
-        const int ak = ins_akind(ins), ai = ins_aidx(ins);
+        const typename F::W ins = F::load(prog, pc);
+        const int fid = F::fid(ins);
+        const int ak = F::akind(ins), ai = F::aidx(ins);
         R a[P], b[P], o[P], d1[P], d2[P];
         bool z1[P], z2[P];
         fetch<R, P>(ak, ai, acc, w, cs, lane, a);
-        const int lo = ins_lo(ins), mid = ins_mid(ins), hi = ins_hi(ins);
-        if (ins_binary(ins)) {
-            const int bk = ins_bkind(ins), bi = ins_bidx(ins);
+        const int lo = F::lo(ins), mid = F::mid(ins), hi = F::hi(ins);
+        if (F::binary(ins)) {
+            const int bk = F::bkind(ins), bi = F::bidx(ins);
             fetch<R, P>(bk, bi, acc, w, cs, lane, b);
             binary_p<R, P>(fid, a, b, JAC == 2 || mid < hi, o, d1, d2, z1, z2);
             if constexpr (JAC == 2) {
-                const int t = ins_tape(ins), ta = ins_tape_a(ins);
+                const int t = F::tape(ins), ta = F::tape_a(ins);
                 if (ta) CUSR_FOR_P lds_at<R, P>(w.tape, t, p, lane) = d1[p];
-                if (ins_tape_b(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, t + ta, p, lane) = d2[p];
+                if (F::tape_b(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, t + ta, p, lane) = d2[p];
             }
         } else {
             unary_p<R, P>(fid, a, o, d1, z1);
             CUSR_FOR_P { d2[p] = d1[p]; z2[p] = z1[p]; }   // unused: scale_b is never set
             if constexpr (JAC == 2) {
-                if (ins_tape_a(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, ins_tape(ins), p, lane) = d1[p];
+                if (F::tape_a(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, F::tape(ins), p, lane) = d1[p];
             }
         }
         if constexpr (JAC == 1) {
@@ -471,12 +539,12 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
             // sets scale_a / scale_b only where a partial is not exactly 1
             // (not for ADD, SUB's left operand or the identity) and the
             // range is non-empty, and sel for the flat-branch operators
-            const bool sel = ins_sel(ins);
-            if (ins_scale_a(ins)) scale_range<K, R, P>(T, lo, mid, d1, z1, sel);
-            if (ins_scale_b(ins)) scale_range<K, R, P>(T, mid, hi, d2, z2, sel);
+            const bool sel = F::sel(ins);
+            if (F::scale_a(ins)) scale_range<K, R, P>(T, lo, mid, d1, z1, sel);
+            if (F::scale_b(ins)) scale_range<K, R, P>(T, mid, hi, d2, z2, sel);
         }
-        if (ins_toslot(ins)) {
-            const int di = ins_didx(ins);
+        if (F::toslot(ins)) {
+            const int di = F::didx(ins);
             CUSR_FOR_P lds_at<R, P>(w.slot, di, p, lane) = o[p];
         } else {
             CUSR_FOR_P acc[p] = o[p];
@@ -487,31 +555,31 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
 // Reverse sweep over the tape written by forward_pass<..., 2>:
 // T[p*K + k] = d f / d c_k, T zero on entry (cusr/kernel/revad_interp.cuh:131-156). The
 // adjoints of spilled values live in the slot area (their values are dead).
-template <int K, typename R, int P>
+template <int K, typename R, int P, typename F = FastFmt>
 __device__ __forceinline__ void reverse_pass(ProgPtr prog, int n, const WaveLds<R, P> &w,
                                              int lane, R *T) {
     R accadj[P];
     CUSR_FOR_P accadj[p] = R(1);
     for (int pc = n - 1; pc >= 0; --pc) {
-        const uint64_t ins = prog[pc];
+        const typename F::W ins = F::load(prog, pc);
         R adj[P];
-        if (ins_toslot(ins)) {
-            const int di = ins_didx(ins);
+        if (F::toslot(ins)) {
+            const int di = F::didx(ins);
             CUSR_FOR_P adj[p] = lds_at<R, P>(w.slot, di, p, lane);
         } else {
             CUSR_FOR_P adj[p] = accadj[p];
         }
-        const int t = ins_tape(ins), ta = ins_tape_a(ins);
-        const int nop = ins_binary(ins) ? 2 : 1;
+        const int t = F::tape(ins), ta = F::tape_a(ins);
+        const int nop = F::binary(ins) ? 2 : 1;
         for (int side = 0; side < nop; ++side) {
-            const int kind = side ? ins_bkind(ins) : ins_akind(ins);
-            const int idx = side ? ins_bidx(ins) : ins_aidx(ins);
+            const int kind = side ? F::bkind(ins) : F::akind(ins);
+            const int idx = side ? F::bidx(ins) : F::aidx(ins);
             if (kind == OPD_VAR) continue;
             R g[P];
-            if (side ? ins_tape_b(ins) : ta) {
+            if (side ? F::tape_b(ins) : ta) {
                 const int slot = t + (side ? ta : 0);
                 CUSR_FOR_P g[p] = safe_mul<R>(adj[p], lds_at<R, P>(w.tape, slot, p, lane));
-            } else if (side && ins_fid(ins) == OP_SUB) {
+            } else if (side && F::fid(ins) == OP_SUB) {
                 // safe_mul(adj, -1) without the tape: -adj, and 0 for a zero adjoint
                 CUSR_FOR_P g[p] = (adj[p] == R(0)) ? R(0) : -adj[p];
             } else {
@@ -582,7 +650,7 @@ __device__ __forceinline__ void block_sync(int pwaves) {
 // One pass over all points at constants cs (LDS): sums[0] = sum r^2,
 // sums[1..K] = J^T r, sums[1+K..] = upper triangle of J^T J (row-major),
 // written to out (LDS) by lane 0. JAC: 0 value only, 1 forward, 2 reverse.
-template <int K, typename R, int P, int JAC>
+template <int K, typename R, int P, int JAC, typename F = FastFmt>
 __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P> &w, const double *cs,
                           double *out, int lane) {
     constexpr int W = (JAC == 0) ? 1 : sums_width(K);
@@ -625,8 +693,8 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
         R T[P * KT];
 #pragma unroll
         for (int j = 0; j < P * KT; ++j) T[j] = (JAC == 1) ? R(1) : R(0);
-        forward_pass<K, R, P, JAC>(a.prog, a.n, w, cs, lane, accv, T);
-        if constexpr (JAC == 2) reverse_pass<K, R, P>(a.prog, a.n, w, lane, T);
+        forward_pass<K, R, P, JAC, F>(a.prog, a.n, w, cs, lane, accv, T);
+        if constexpr (JAC == 2) reverse_pass<K, R, P, F>(a.prog, a.n, w, lane, T);
         if constexpr (MX) {
             CUSR_FOR_P {
                 const double r = valid[p] ? (double)accv[p] - yv[p] : 0.0;
@@ -717,6 +785,119 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
     __syncthreads();
 }
 
+// The general kernel's Jacobian pass (runtime K = Kr <= CO_MAX_K, one point
+// per lane): sums[0] = sum r^2, sums[1..Kr] = J^T r, then the upper triangle
+// of J^T J, every entry one fma chain over the partition's points in ascending
+// order. The 64 augmented rows [J | r] of a slice go to LDS (jt, [64][kGenStride],
+// r in column Kr); v_mfma_f64_16x16x4 then folds them four points at a time into
+// the 16 x 16 blocks (a, b), a <= b, of [J | r]^T [J | r]: nb = ceil((Kr+1)/16)
+// column blocks, nb (nb+1) / 2 accumulators. Columns past Kr read column Kr
+// (so every operand is defined); the entries they produce are never read.
+// The accumulators then go straight to the sums vector: register r4 of lane l
+// holds entry (4 r4 + l / 16, l mod 16) of its block.
+constexpr int kGenK = CO_MAX_K;
+constexpr int kGenStride = kGenK + 1;   // doubles per staged row: [J | r]
+constexpr size_t kGenJtBytes = (size_t)kLanes * kGenStride * sizeof(double);
+
+// Entries (i, j), i <= j <= Kr, of the 16 x 16 block (ba, bb) of
+// [J | r]^T [J | r] (accumulator g: register r4 of lane l holds entry
+// (4 r4 + l / 16, l mod 16)) to their places in the sums vector.
+__device__ __forceinline__ void put_block(double *dst, cusr_double4 g, int ba, int bb, int Kr,
+                                          int lane) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+        const int i = 16 * ba + 4 * r4 + (lane >> 4), j = 16 * bb + (lane & 15);
+        if (i > j || j > Kr) continue;
+        const int q = (j == Kr) ? ((i == Kr) ? 0 : 1 + i)
+                                : 1 + Kr + i * Kr - (i * (i - 1)) / 2 + (j - i);
+        dst[q] = g[r4];
+    }
+}
+
+template <typename R, int JAC, typename F>
+__device__ __forceinline__ void data_pass_gen(const PassArgs &a, const WaveLds<R, 1> &w,
+                                              const double *cs, double *out, int lane, int Kr) {
+    constexpr int K = kGenK;
+    const int W = sums_width(Kr);
+    const int nb = (Kr + 16) / 16;
+    const int granules = (a.N + kLanes - 1) / kLanes;
+    const int last = a.N - 1;
+    double *jt = a.jt;
+    const int c16 = lane & 15;
+    const int col0 = c16 < Kr ? c16 : Kr;
+    const int col1 = 16 + c16 < Kr ? 16 + c16 : Kr;
+    const int col2 = 32 + c16 < Kr ? 32 + c16 : Kr;
+    for (int part = a.wave; part < a.parts; part += a.pwaves) {
+        cusr_double4 g0 = {0.0, 0.0, 0.0, 0.0}, g1 = g0, g2 = g0, g3 = g0, g4 = g0, g5 = g0;
+        const int ng = (part < granules) ? (granules - part + a.parts - 1) / a.parts : 0;
+        for (int gi = 0; gi < ng; ++gi) {
+            // points past N read point N-1 (in bounds) and stage a zero row
+            const int i = (part + a.parts * gi) * kLanes + lane;
+            const bool valid = i < a.N;
+            const int ic = valid ? i : last;
+            const double yv = a.y[ic];
+            for (int v = 0; v < a.D; ++v)
+                lds_at<R, 1>(w.x, v, 0, lane) = (R)a.X[(size_t)v * a.N + ic];
+            R accv[1];
+            R T[K];
+#pragma unroll
+            for (int j = 0; j < K; ++j) T[j] = (JAC == 1) ? R(1) : R(0);
+            forward_pass<K, R, 1, JAC, F>(a.prog, a.n, w, cs, lane, accv, T);
+            if constexpr (JAC == 2) reverse_pass<K, R, 1, F>(a.prog, a.n, w, lane, T);
+            const double r = valid ? (double)accv[0] - yv : 0.0;
+            double *row = jt + lane * kGenStride;
+#pragma unroll
+            for (int j = 0; j < K; ++j) row[j] = valid ? (double)T[j] : 0.0;
+            row[Kr] = r;
+            wave_sync_lds();
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                const double *pr = jt + (4 * m + (lane >> 4)) * kGenStride;
+                const double v0 = pr[col0];
+                g0 = __builtin_amdgcn_mfma_f64_16x16x4f64(v0, v0, g0, 0, 0, 0);
+                if (nb > 1) {
+                    const double v1 = pr[col1];
+                    g1 = __builtin_amdgcn_mfma_f64_16x16x4f64(v0, v1, g1, 0, 0, 0);
+                    g2 = __builtin_amdgcn_mfma_f64_16x16x4f64(v1, v1, g2, 0, 0, 0);
+                    if (nb > 2) {
+                        const double v2 = pr[col2];
+                        g3 = __builtin_amdgcn_mfma_f64_16x16x4f64(v0, v2, g3, 0, 0, 0);
+                        g4 = __builtin_amdgcn_mfma_f64_16x16x4f64(v1, v2, g4, 0, 0, 0);
+                        g5 = __builtin_amdgcn_mfma_f64_16x16x4f64(v2, v2, g5, 0, 0, 0);
+                    }
+                }
+            }
+            wave_sync_lds();
+        }
+        double *dst = (a.parts == 1) ? out : a.part + part * W;
+        put_block(dst, g0, 0, 0, Kr, lane);
+        if (nb > 1) {
+            put_block(dst, g1, 0, 1, Kr, lane);
+            put_block(dst, g2, 1, 1, Kr, lane);
+        }
+        if (nb > 2) {
+            put_block(dst, g3, 0, 2, Kr, lane);
+            put_block(dst, g4, 1, 2, Kr, lane);
+            put_block(dst, g5, 2, 2, Kr, lane);
+        }
+    }
+    if (a.parts == 1) {
+        wave_sync_lds();
+        return;
+    }
+    // partition sums added in partition order, sum q by lane q mod 64 of the
+    // first wavefront
+    __syncthreads();
+    if (a.wave == 0) {
+        for (int q = lane; q < W; q += kLanes) {
+            double v = a.part[q];
+            for (int g = 1; g < a.parts; ++g) v = v + a.part[g * W + q];
+            out[q] = v;
+        }
+    }
+    __syncthreads();
+}
+
 // ------------------------------------------------------------ the solve
 
 // Relative-damped Cholesky solve of (J^T J + lambda diag(J^T J)) delta = -J^T r
@@ -773,14 +954,14 @@ __device__ __forceinline__ bool damped_solve(const double *s, double lambda, dou
     return true;
 }
 
-// The same solve with L in LDS (the matrix-sum kernels,
-// where K(K+1)/2 doubles per lane of the register version would set the
-// kernel's register count). Every element gets exactly the arithmetic of
-// damped_solve: column j's pivot is computed by every lane, the entries below
-// it by lane i; the substitutions run on every lane with L read by broadcast.
-template <int K>
-__device__ __forceinline__ bool damped_solve_lds(const double *s, double lambda, double (&delta)[K],
-                                                 double *L, int lane) {
+// The same solve with L in LDS, K at run time (the general kernel, and the
+// fast kernels with matrix sums, where K(K+1)/2 doubles per lane of the
+// register version would set the kernel's register count). Every element gets
+// exactly the arithmetic of damped_solve: column j's pivot is computed by
+// every lane, the entries below it by lane i; the substitutions run on every
+// lane with L read by broadcast. The solution is left in L[K*K .. K*K+K).
+__device__ __forceinline__ bool damped_solve_rt(const double *s, double lambda, int K, double *L,
+                                                int lane) {
     double *b = L + K * K;   // right-hand side, then the solution (LDS, K doubles)
     // L[i][j] = upper-triangle element (j, i) of J^T J for j <= i; diagonal damped
     if (lane < K) {
@@ -827,8 +1008,15 @@ __device__ __forceinline__ bool damped_solve_lds(const double *s, double lambda,
         if (lane == 0) b[i] = t / L[i * K + i];
         wave_sync_lds();
     }
+    return true;
+}
+
+template <int K>
+__device__ __forceinline__ bool damped_solve_lds(const double *s, double lambda, double (&delta)[K],
+                                                 double *L, int lane) {
+    if (!damped_solve_rt(s, lambda, K, L, lane)) return false;
 #pragma unroll
-    for (int i = 0; i < K; ++i) delta[i] = b[i];
+    for (int i = 0; i < K; ++i) delta[i] = L[K * K + i];
     return true;
 }
 
@@ -847,40 +1035,76 @@ struct FitArgs {
     int32_t *iters;         // [M] out
     int N, D, max_iter, guard, lm_order;
     int shared_y;           // 1: Y is one row [N] shared by every expression
+    int f32_range;          // 1: constants and losses held to the fp32 range
     double lambda0, xtol;
     int slots, tape;        // per-wave LDS rows of this launch ([row][P][64] each)
     int parts;              // point partitions per expression (1, 2 or 4)
-    int pwaves;             // wavefronts per workgroup (divides parts)
+    int pwaves;             // wavefronts of the workgroup (divides parts)
     int wave_bytes;         // dynamic LDS of one wavefront; partition sums follow
     // segments of the iteration loop: this launch runs iterations up to it_end
     // (<= max_iter); an expression still running there saves its loop state
-    // to state[y_row] (and its constants to C) for the next launch, which
-    // resumes it (resume = 1) or, for expressions that finished, exits
+    // to state[y_row * state_stride] (and its constants to C) for the next
+    // launch, which resumes it (resume = 1) or, for expressions that
+    // finished, exits
     int it_end, resume;
-    double *state;          // [M][kStateStride], null for single-launch fits
+    int state_stride;       // doubles per state row, >= kStateSums + sums_width(K)
+    double *state;          // [M][state_stride], null for single-launch fits
 };
 
 // loop state of a paused fit, per expression: loss, loss_init, lambda,
 // internal status (kStateDone once the outputs are written), iterations,
 // then the sums at the current constants
-constexpr int kStateStride = 8 + 160;
 constexpr int kStateSums = 8;
 constexpr double kStateDone = -1.0;
-static_assert(sums_width(CO_MAX_K) <= kStateStride - kStateSums, "state row too short");
+constexpr int state_stride_for(int K) { return kStateSums + sums_width(K); }
 
 // internal states, mapped to STATUS_* at the end (lm_core.cuh:46-56)
 enum { ST_RUN = 0, ST_CONV = 1, ST_NAN = 2, ST_K0 = 3, ST_CHOL = 4 };
 
-template <int K, typename R, int AD, int LN>
+// A loss the fit may go on from (batch_lm_ad.cu:437-443): finite, and under
+// f32_range finite in fp32 too, where the reference accumulates it.
+__device__ __forceinline__ bool loss_ok(const FitArgs &fa, double loss) {
+    return isfinite(loss) && (!fa.f32_range || isfinite((float)loss));
+}
+
+// Static LDS of a fit kernel: current and trial constants, current and trial
+// sums, sized for the kernel family's largest K.
+template <bool GEN>
+struct FitStatic {
+    static constexpr int KC = GEN ? CO_MAX_K : CO_FAST_MAX_K;
+    static constexpr int SW = sums_width(KC);
+};
+
+// Points per lane of a fit's passes and of its fp64 audit passes: the
+// general kernel runs one of each.
+template <bool GEN, typename R, int K, int AD, int LN>
+constexpr int fit_points() {
+    if constexpr (GEN) return 1;
+    else return points_per_pass<R, K, AD, LN>();
+}
+template <bool GEN, typename R, int K, int AD, int LN>
+constexpr int fit_audit_points() {
+    if constexpr (GEN) return 1;
+    else return audit_points<R, K, AD, LN>();
+}
+
+template <int K, typename R, int AD, int LN, bool GEN = false>
 __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, double *lds_c, double *lds_s,
                         char *lds_dyn, int lane, int wave) {
-    constexpr int P = points_per_pass<R, K, AD, LN>();
+    typedef typename std::conditional<GEN, WideFmt, FastFmt>::type F;
+    constexpr int P = fit_points<GEN, R, K, AD, LN>();
     constexpr int JAC = (K == 0) ? 0 : (AD == CO_AD_REVERSE ? 2 : 1);
+    constexpr int KC = FitStatic<GEN>::KC;
+    const int Kr = GEN ? e.K : K;   // the expression's K (wave-uniform)
     char *my_lds = lds_dyn + (size_t)wave * fa.wave_bytes;
     const bool lead = wave == 0;     // the wavefront that writes shared state
-    double *jt = (double *)my_lds;   // matrix sums: [64][17] slice tile first
-    double *lds_l = jt + kLanes * kJtStride;   // then the K x K Cholesky factor and rhs
-    if constexpr (matrix_sums<K, AD>()) {
+    double *jt = (double *)my_lds;   // matrix sums: the slice's augmented rows first
+    // then the K x K Cholesky factor and rhs (the general kernel's solve
+    // reuses the rows' bytes: it runs between passes)
+    double *lds_l = GEN ? jt : jt + kLanes * kJtStride;
+    if constexpr (GEN) {
+        my_lds += kGenJtBytes;
+    } else if constexpr (matrix_sums<K, AD>()) {
         // columns K+1.. of every row stay zero for the whole fit
 #pragma unroll
         for (int j = 0; j < kJtStride; ++j) jt[lane * kJtStride + j] = 0.0;
@@ -903,18 +1127,23 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     pa.part = (double *)(lds_dyn + (size_t)fa.pwaves * fa.wave_bytes);
     pa.jt = jt;
 
-    double *c_cur = lds_c, *c_try = lds_c + CO_MAX_K;
-    double *s_cur = lds_s, *s_try = lds_s + sums_width(CO_MAX_K);
-    double *sv = fa.state ? fa.state + (size_t)e.y_row * kStateStride : nullptr;
+    double *c_cur = lds_c, *c_try = lds_c + KC;
+    double *s_cur = lds_s, *s_try = lds_s + FitStatic<GEN>::SW;
+    double *sv = fa.state ? fa.state + (size_t)e.y_row * fa.state_stride : nullptr;
     double loss, loss_init, lambda;
     int st, it;
     if (!fa.resume) {
-        if (lead && lane < K) c_cur[lane] = fa.C0[e.c_off + lane];
+        if (lead && lane < Kr) c_cur[lane] = fa.C0[e.c_off + lane];
         block_sync(fa.pwaves);
-        data_pass<K, R, P, JAC>(pa, wl, c_cur, s_cur, lane);
+        if constexpr (GEN) {
+            if (Kr == 0) data_pass<0, R, 1, 0, F>(pa, wl, c_cur, s_cur, lane);
+            else data_pass_gen<R, JAC, F>(pa, wl, c_cur, s_cur, lane, Kr);
+        } else {
+            data_pass<K, R, P, JAC, F>(pa, wl, c_cur, s_cur, lane);
+        }
         loss = uni(0.5 * s_cur[0]);
         loss_init = loss;
-        st = (K == 0) ? ST_K0 : (isfinite(loss) ? ST_RUN : ST_NAN);
+        st = (Kr == 0) ? ST_K0 : (loss_ok(fa, loss) ? ST_RUN : ST_NAN);
         lambda = fa.lambda0;
         it = 0;
     } else {
@@ -922,8 +1151,8 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
         const double sst = uni(sv[3]);
         if (sst == kStateDone) return;
         if (lead) {
-            if (lane < K) c_cur[lane] = fa.C[e.c_off + lane];
-            for (int j = lane; j < sums_width(K); j += kLanes) s_cur[j] = sv[kStateSums + j];
+            if (lane < Kr) c_cur[lane] = fa.C[e.c_off + lane];
+            for (int j = lane; j < sums_width(Kr); j += kLanes) s_cur[j] = sv[kStateSums + j];
         }
         loss = uni(sv[0]);
         loss_init = uni(sv[1]);
@@ -935,9 +1164,11 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     if constexpr (K > 0) {
         while (uni(st) == ST_RUN && it < fa.it_end) {
             ++it;
-            double delta[K];
+            double delta[GEN ? 1 : K];
             bool solved;
-            if constexpr (matrix_sums<K, AD>())
+            if constexpr (GEN)
+                solved = damped_solve_rt(s_cur, lambda, Kr, lds_l, lane);
+            else if constexpr (matrix_sums<K, AD>())
                 solved = damped_solve_lds<K>(s_cur, lambda, delta, lds_l, lane);
             else
                 solved = damped_solve<K>(s_cur, lambda, delta);
@@ -949,21 +1180,55 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
             // every wavefront is done reading c_try (the norm below) before
             // the lead overwrites it
             if (fa.pwaves > 1) __syncthreads();
-            if (lead && lane < K) {
-#pragma unroll
-                for (int j = 0; j < K; ++j)
-                    if (j == lane) c_try[j] = c_cur[j] + delta[j];
-            }
-            block_sync(fa.pwaves);
-            data_pass<K, R, P, JAC>(pa, wl, c_try, s_try, lane);
-            const double loss_try = uni(0.5 * s_try[0]);
-            if (!isfinite(loss_try)) { st = ST_NAN; continue; }
             double dn2 = 0.0, cn2 = 0.0;
+            if constexpr (GEN) {
+                // the solution sits in the rows' bytes, which the pass
+                // overwrites: the step norms are formed before it
+                const double *db = lds_l + Kr * Kr;
+                if (lead && lane < Kr) {
+                    const double v = c_cur[lane] + db[lane];
+                    c_try[lane] = fa.f32_range ? (double)(float)v : v;
+                }
+                block_sync(fa.pwaves);
+                for (int j = 0; j < Kr; ++j) {
+                    dn2 = fma(db[j], db[j], dn2);
+                    cn2 = fma(c_try[j], c_try[j], cn2);
+                }
+            } else {
+                if (lead && lane < K) {
 #pragma unroll
-            for (int j = 0; j < K; ++j) {
-                dn2 = fma(delta[j], delta[j], dn2);
-                cn2 = fma(c_try[j], c_try[j], cn2);
+                    for (int j = 0; j < K; ++j) {
+                        if (j == lane) {
+                            const double v = c_cur[j] + delta[j];
+                            c_try[j] = fa.f32_range ? (double)(float)v : v;
+                        }
+                    }
+                }
+                block_sync(fa.pwaves);
             }
+            if (fa.f32_range) {
+                // trial constants are held in fp32, as the reference's are; one
+                // beyond the fp32 range makes its trial loss non-finite
+                // (batch_lm_ad.cu:437-443): no pass needed
+                int over = 0;
+                for (int j = 0; j < Kr; ++j) over |= !isfinite(c_try[j]) ? 1 : 0;
+                if (uni(over)) {
+                    st = ST_NAN;
+                    continue;
+                }
+            }
+            if constexpr (GEN) {
+                data_pass_gen<R, JAC, F>(pa, wl, c_try, s_try, lane, Kr);
+            } else {
+                data_pass<K, R, P, JAC, F>(pa, wl, c_try, s_try, lane);
+#pragma unroll
+                for (int j = 0; j < K; ++j) {
+                    dn2 = fma(delta[j], delta[j], dn2);
+                    cn2 = fma(c_try[j], c_try[j], cn2);
+                }
+            }
+            const double loss_try = uni(0.5 * s_try[0]);
+            if (!loss_ok(fa, loss_try)) { st = ST_NAN; continue; }
             const double dn = ::sqrt(dn2), cn = ::sqrt(cn2);
             const bool small = dn < fa.xtol * (cn + fa.xtol);
             bool accept, conv;
@@ -996,8 +1261,8 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     if (st == ST_RUN && it < fa.max_iter) {
         // paused at the end of this launch's segment: save the loop state
         if (lead) {
-            if (lane < K) fa.C[e.c_off + lane] = c_cur[lane];
-            for (int j = lane; j < sums_width(K); j += kLanes) sv[kStateSums + j] = s_cur[j];
+            if (lane < Kr) fa.C[e.c_off + lane] = c_cur[lane];
+            for (int j = lane; j < sums_width(Kr); j += kLanes) sv[kStateSums + j] = s_cur[j];
             if (lane == 0) {
                 sv[0] = loss;
                 sv[1] = loss_init;
@@ -1012,29 +1277,30 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     if constexpr (sizeof(R) == 4) {
         // fp64 losses at the delivered point and at the start; the fp64
         // value pass reuses the same LDS bytes per row and lane (half the
-        // points of the fp32 passes). A lane's points are summed in the same
+        // points of the fp32 passes). A lane sums its points in the same
         // ascending order at any number of points per pass.
-        constexpr int AP = audit_points<R, K, AD, LN>();
+        constexpr int AP = fit_audit_points<GEN, R, K, AD, LN>();
+        constexpr int KA = GEN ? 0 : K;
         WaveLds<double, AP> w64;
         w64.x = (double *)my_lds;
         w64.slot = w64.x + (size_t)fa.D * AP * kLanes;
         w64.tape = w64.slot + (size_t)fa.slots * AP * kLanes;
-        data_pass<K, double, AP, 0>(pa, w64, c_cur, s_try, lane);
+        data_pass<KA, double, AP, 0, F>(pa, w64, c_cur, s_try, lane);
         lf = uni(0.5 * s_try[0]);
         if (fa.pwaves > 1) __syncthreads();
-        if (lead && lane < K) c_try[lane] = fa.C0[e.c_off + lane];
+        if (lead && lane < Kr) c_try[lane] = fa.C0[e.c_off + lane];
         block_sync(fa.pwaves);
-        data_pass<K, double, AP, 0>(pa, w64, c_try, s_try, lane);
+        data_pass<KA, double, AP, 0, F>(pa, w64, c_try, s_try, lane);
         li = uni(0.5 * s_try[0]);
     }
     bool revert = false;
-    if (fa.guard && K > 0) revert = !isfinite(lf) || (isfinite(li) && lf > li);
+    if (fa.guard && Kr > 0) revert = !isfinite(lf) || (isfinite(li) && lf > li);
     if (revert) {
         if (st == ST_CONV) st = ST_RUN;
         lf = li;
     }
     if (!lead) return;
-    if (lane < K) fa.C[e.c_off + lane] = revert ? fa.C0[e.c_off + lane] : c_cur[lane];
+    if (lane < Kr) fa.C[e.c_off + lane] = revert ? fa.C0[e.c_off + lane] : c_cur[lane];
     if (lane == 0) {
         // ST_RUN -> STATUS_MAXITER, ST_CONV -> STATUS_CONVERGED, the rest keep their code
         fa.status[e.y_row] = (st <= ST_CONV) ? (1 - st) : st;
@@ -1063,9 +1329,9 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
 #ifndef CUSR_WAVES_OTHER
 #define CUSR_WAVES_OTHER 1
 #endif
-constexpr int kW64[CO_MAX_K + 1] = {CUSR_W64_TABLE};
-constexpr int kW64LargeN[CO_MAX_K + 1] = {CUSR_W64_LARGE_N_TABLE};
-constexpr int kWRev64[CO_MAX_K + 1] = {CUSR_WREV64_TABLE};
+constexpr int kW64[CO_FAST_MAX_K + 1] = {CUSR_W64_TABLE};
+constexpr int kW64LargeN[CO_FAST_MAX_K + 1] = {CUSR_W64_LARGE_N_TABLE};
+constexpr int kWRev64[CO_FAST_MAX_K + 1] = {CUSR_WREV64_TABLE};
 template <typename R, int K, int AD, int LN = 0>
 constexpr int waves_per_eu() {
     return sizeof(R) == 8 ? (AD == CO_AD_FORWARD ? (LN ? kW64LargeN[K] : kW64[K]) : kWRev64[K])
@@ -1081,13 +1347,36 @@ constexpr bool large_n_variant() {
 template <int K, typename R, int AD, int LN = 0>
 __global__ void __launch_bounds__(kLanes * CO_MAX_PARTITIONS, (waves_per_eu<R, K, AD, LN>()))
 lm_fit_kernel(FitArgs fa) {
-    __shared__ double lds_c[2 * CO_MAX_K];
-    __shared__ double lds_s[2 * sums_width(CO_MAX_K)];
+    __shared__ double lds_c[2 * FitStatic<false>::KC];
+    __shared__ double lds_s[2 * FitStatic<false>::SW];
     extern __shared__ char lds_dyn[];
     const ExprDesc e = fa.desc[blockIdx.x];
     const int lane = (int)threadIdx.x & (kLanes - 1);
     const int wave = uni((int)threadIdx.x >> 6);
     fit_one<K, R, AD, LN>(fa, e, lds_c, lds_s, lds_dyn, lane, wave);
+}
+
+// The general kernel: runtime K <= CO_MAX_K, wide programs, one point per
+// lane; tangents / gradients in 32 fixed registers, sums on the matrix unit.
+#ifndef CUSR_WAVES_GEN
+#define CUSR_WAVES_GEN 2
+#endif
+template <typename R, int AD>
+__global__ void __launch_bounds__(kLanes * CO_MAX_PARTITIONS, CUSR_WAVES_GEN)
+lm_fit_gen_kernel(FitArgs fa) {
+    __shared__ double lds_c[2 * FitStatic<true>::KC];
+    __shared__ double lds_s[2 * FitStatic<true>::SW];
+    extern __shared__ char lds_dyn[];
+    const ExprDesc e = fa.desc[blockIdx.x];
+    const int lane = (int)threadIdx.x & (kLanes - 1);
+    const int wave = uni((int)threadIdx.x >> 6);
+    fit_one<kGenK, R, AD, 0, true>(fa, e, lds_c, lds_s, lds_dyn, lane, wave);
+}
+
+// Static LDS bytes of a fit kernel family (kept out of the dynamic budget).
+constexpr size_t fit_static_lds(bool gen) {
+    return gen ? (2 * FitStatic<true>::KC + 2 * FitStatic<true>::SW) * sizeof(double)
+               : (2 * FitStatic<false>::KC + 2 * FitStatic<false>::SW) * sizeof(double);
 }
 
 // Dynamic LDS bytes one wavefront of a fit launch needs (the mixed-precision
@@ -1101,10 +1390,20 @@ constexpr size_t fit_lds_bytes_t(int D, int slots, int tape) {
            (a > b ? a : b);
 }
 
-hipError_t launch_fit_f64_fwd(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
-hipError_t launch_fit_f64_rev(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
-hipError_t launch_fit_f32_fwd(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
-hipError_t launch_fit_f32_rev(int K, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
+// ... of a general-kernel launch (one point per lane; the fp64 audit at one)
+template <typename R>
+constexpr size_t fit_lds_bytes_gen(int D, int slots, int tape) {
+    const size_t a = (size_t)(D + slots + tape) * kLanes * sizeof(R);
+    const size_t b = (size_t)(D + slots) * kLanes * sizeof(double);
+    return kGenJtBytes + (a > b ? a : b);
+}
+
+// Launch the fit kernel of one bin (k <= CO_FAST_MAX_K: the fast kernel of
+// K = k; CO_GENERAL_BIN: the general kernel) for one (precision, AD mode).
+hipError_t launch_fit_f64_fwd(int bin, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
+hipError_t launch_fit_f64_rev(int bin, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
+hipError_t launch_fit_f32_fwd(int bin, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
+hipError_t launch_fit_f32_rev(int bin, unsigned grid, size_t lds, hipStream_t s, const FitArgs &fa);
 
 // ------------------------------------------------------ plain evaluation
 
@@ -1117,7 +1416,7 @@ struct EvalArgs {
     int N, D;
 };
 
-template <typename R>
+template <typename R, typename F>
 __global__ void __launch_bounds__(kLanes) eval_kernel(EvalArgs ea) {
     constexpr int P = 1;
     __shared__ double cs[CO_MAX_K];
@@ -1135,11 +1434,10 @@ __global__ void __launch_bounds__(kLanes) eval_kernel(EvalArgs ea) {
     for (int bt = 0; bt < batches; ++bt) {
         const int i = lane + kLanes * bt;
         const bool valid = i < ea.N;
-#pragma unroll
-        for (int v = 0; v < CO_MAX_VARS; ++v)
-            if (v < ea.D) lds_at<R, P>(w.x, v, 0, lane) = valid ? (R)ea.X[(size_t)v * ea.N + i] : R(0);
+        for (int v = 0; v < ea.D; ++v)
+            lds_at<R, P>(w.x, v, 0, lane) = valid ? (R)ea.X[(size_t)v * ea.N + i] : R(0);
         R accv[1], T[1];
-        forward_pass<0, R, P, 0>(prog, e.n, w, cs, lane, accv, T);
+        forward_pass<0, R, P, 0, F>(prog, e.n, w, cs, lane, accv, T);
         if (valid) ea.Yout[(size_t)e.y_row * ea.N + i] = (double)accv[0];
     }
 }

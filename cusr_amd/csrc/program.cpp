@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <functional>
 #include <thread>
 #include <vector>
 
@@ -56,19 +57,49 @@ static int op_cost(int f) {
     }
 }
 
-// Forward-AD flags of an instruction (program.h bits 47..49): flat-branch
-// select rule, and which of its rank ranges get scaled. ADD's partials and
-// SUB's left one are exactly 1; the identity has no partial to apply.
-static uint64_t flag_bits(int f, bool bin, int lo, int mid, int hi) {
-    const bool sel = f == OP_MAX || f == OP_MIN || f == OP_LT || f == OP_GT || f == OP_LE ||
-                     f == OP_GE || f == OP_PDIV || f == OP_CEXP;
-    const bool unit_a = bin ? (f == OP_ADD || f == OP_SUB) : (f == OP_IDENT);
-    const bool unit_b = !bin || f == OP_ADD;
-    uint64_t w = 0;
-    if (sel) w |= (uint64_t)1 << 47;
-    if (!unit_a && mid > lo) w |= (uint64_t)1 << 48;
-    if (!unit_b && hi > mid) w |= (uint64_t)1 << 49;
-    return w;
+// Forward-AD and reverse-AD flags of an instruction: flat-branch select
+// rule, which of its rank ranges get scaled (ADD's partials and SUB's left
+// one are exactly 1; the identity has no partial to apply), and which partials
+// keep a reverse-AD tape slot (read, and not exactly +-1).
+struct Ins {
+    int fid, bin, ak, ai, bk, bi, toslot, di, lo, mid, hi, tape;
+    bool sel, sa, sb, ta, tb;
+};
+
+static void set_flags(Ins &w) {
+    const int f = w.fid;
+    w.sel = f == OP_MAX || f == OP_MIN || f == OP_LT || f == OP_GT || f == OP_LE || f == OP_GE ||
+            f == OP_PDIV || f == OP_CEXP;
+    const bool unit_a = w.bin ? (f == OP_ADD || f == OP_SUB) : (f == OP_IDENT);
+    const bool unit_b = !w.bin || f == OP_ADD;
+    w.sa = !unit_a && w.mid > w.lo;
+    w.sb = !unit_b && w.hi > w.mid;
+}
+
+// program.h bit layouts
+static uint64_t encode_fast(const Ins &w) {
+    uint64_t x = (uint64_t)w.fid | (uint64_t)w.bin << 6;
+    x |= (uint64_t)w.ak << 7 | (uint64_t)(w.ai & 15) << 9;
+    x |= (uint64_t)w.bk << 13 | (uint64_t)(w.bi & 15) << 15;
+    x |= (uint64_t)w.toslot << 19 | (uint64_t)(w.di & 15) << 20;
+    x |= (uint64_t)w.lo << 24 | (uint64_t)w.mid << 29 | (uint64_t)w.hi << 34;
+    x |= (uint64_t)w.tape << 39;
+    x |= (uint64_t)w.sel << 47 | (uint64_t)w.sa << 48 | (uint64_t)w.sb << 49;
+    x |= (uint64_t)w.ta << 50 | (uint64_t)w.tb << 51;
+    return x;
+}
+
+static void encode_wide(const Ins &w, uint64_t *out) {
+    uint64_t a = (uint64_t)w.fid | (uint64_t)w.bin << 6;
+    a |= (uint64_t)w.ak << 7 | (uint64_t)(w.ai & 255) << 9;
+    a |= (uint64_t)w.bk << 17 | (uint64_t)(w.bi & 255) << 19;
+    a |= (uint64_t)w.toslot << 27 | (uint64_t)(w.di & 255) << 28;
+    a |= (uint64_t)w.sel << 36 | (uint64_t)w.sa << 37 | (uint64_t)w.sb << 38;
+    a |= (uint64_t)w.ta << 39 | (uint64_t)w.tb << 40;
+    uint64_t b = (uint64_t)w.lo | (uint64_t)w.mid << 8 | (uint64_t)w.hi << 16;
+    b |= (uint64_t)(uint32_t)w.tape << 24;
+    out[0] = a;
+    out[1] = b;
 }
 
 // Integral node value in [0, limit) or -1.
@@ -88,15 +119,17 @@ struct TreeScratch {
     std::vector<int> size, left, cc;
     std::vector<int> depth_stack;
     std::vector<Operand> opd;
+    std::vector<Ins> ins;
 };
 
-// Decode one expression (n nodes) into out[0..n_ins) in execution order.
-// Returns CO_OK, CO_ERR_BOUNDS or CO_ERR_PROGRAM.
-static int decode_tree(const int32_t *nt, const float *nv, const int32_t *ci, int n, int K,
-                       int D, uint64_t *out, int *n_ins, int *stack_depth, int *tape_slots,
-                       int *slots_used, TreeScratch &s) {
+// Validate one expression (n nodes, K constants, D variables): node types,
+// operator ids, variable indices, prefix-order constant ranks and stack moves.
+// Returns CO_OK, CO_ERR_BOUNDS (value stack beyond CO_MAX_STACK) or
+// CO_ERR_PROGRAM, and its value-stack depth. Fills s.size / s.left / s.cc for
+// the emission.
+static int check_tree(const int32_t *nt, const float *nv, const int32_t *ci, int n, int K,
+                      int D, int *stack_depth, TreeScratch &s) {
     if (n <= 0) return CO_ERR_PROGRAM;
-    if (n > CO_MAX_NODES) return CO_ERR_BOUNDS;
     s.size.assign(n, 0);
     s.left.assign(n, 0);
     s.cc.assign(n + 1, 0);
@@ -138,11 +171,19 @@ static int decode_tree(const int32_t *nt, const float *nv, const int32_t *ci, in
         if ((int)s.depth_stack.size() > depth) depth = (int)s.depth_stack.size();
     }
     if (s.depth_stack.size() != 1) return CO_ERR_PROGRAM;
+    *stack_depth = depth;
     if (depth > CO_MAX_STACK) return CO_ERR_BOUNDS;
+    return CO_OK;
+}
 
-    // emission pass: operator instructions over ACC / SLOT / leaf operands
+// Emit the instructions of a checked expression into s.ins in execution
+// order. max_slots: slots the target format can address. Returns CO_OK,
+// CO_ERR_BOUNDS or CO_ERR_PROGRAM; sets the tape and spill-slot counts.
+static int emit_tree(const int32_t *nt, const float *nv, const int32_t *ci, int n, int D,
+                     int max_slots_fmt, int *tape_slots, int *slots_used, TreeScratch &s) {
     s.opd.clear();
-    int nins = 0, tape = 0, live_slots = 0, max_slots = 0;
+    s.ins.clear();
+    int tape = 0, live_slots = 0, max_slots = 0;
     for (int i = n - 1; i >= 0; i--) {
         const int t = nt[i];
         if (t == NODE_VAR) {
@@ -175,113 +216,61 @@ static int decode_tree(const int32_t *nt, const float *nv, const int32_t *ci, in
         // operand stack (at most one) moves to the next free slot instead
         for (Operand &o : s.opd) {
             if (o.kind != OPD_ACC) continue;
-            if (live_slots >= kMaxSlots) return CO_ERR_BOUNDS;
+            if (live_slots >= max_slots_fmt) return CO_ERR_BOUNDS;
             const int slot = live_slots++;
             if (live_slots > max_slots) max_slots = live_slots;
-            out[o.producer] |= (uint64_t)1 << 19 | (uint64_t)slot << 20;
+            s.ins[o.producer].toslot = 1;
+            s.ins[o.producer].di = slot;
             o.kind = OPD_SLOT;
             o.idx = slot;
             o.producer = -1;
         }
-        const int lo = s.cc[i + 1];
-        const int hi = s.cc[i + s.size[i]];
-        const int mid = bin ? s.cc[i + 1 + s.left[i]] : hi;
-        uint64_t w = (uint64_t)f | (uint64_t)(bin ? 1 : 0) << 6;
-        w |= (uint64_t)a.kind << 7 | (uint64_t)(a.idx & 15) << 9;
-        if (bin) w |= (uint64_t)b.kind << 13 | (uint64_t)(b.idx & 15) << 15;
-        w |= (uint64_t)lo << 24 | (uint64_t)mid << 29 | (uint64_t)hi << 34;
-        w |= (uint64_t)tape << 39;
-        w |= flag_bits(f, bin, lo, mid, hi);
+        Ins w = {};
+        w.fid = f;
+        w.bin = bin ? 1 : 0;
+        w.ak = a.kind;
+        w.ai = a.idx;
+        if (bin) {
+            w.bk = b.kind;
+            w.bi = b.idx;
+        }
+        w.lo = s.cc[i + 1];
+        w.hi = s.cc[i + s.size[i]];
+        w.mid = bin ? s.cc[i + 1 + s.left[i]] : w.hi;
+        w.tape = tape;
+        set_flags(w);
         // reverse-AD tape slots only for partials that are read and not exactly +-1
         const bool unit = bin && (f == OP_ADD || f == OP_SUB);
-        const bool ta = a.kind != OPD_VAR && !unit;
-        const bool tb = bin && b.kind != OPD_VAR && !unit;
-        w |= (uint64_t)(ta ? 1 : 0) << 50 | (uint64_t)(tb ? 1 : 0) << 51;
-        tape += (ta ? 1 : 0) + (tb ? 1 : 0);
-        out[nins] = w;
-        s.opd.push_back({OPD_ACC, 0, nins});
-        nins++;
+        w.ta = a.kind != OPD_VAR && !unit;
+        w.tb = bin && b.kind != OPD_VAR && !unit;
+        tape += (w.ta ? 1 : 0) + (w.tb ? 1 : 0);
+        s.opd.push_back({OPD_ACC, 0, (int)s.ins.size()});
+        s.ins.push_back(w);
     }
-    if (nins == 0) {
+    if (s.ins.empty()) {
         // the expression is one leaf: its value is the identity of that leaf
         const Operand a = s.opd.back();
-        const int lo = s.cc[0], hi = s.cc[n];
-        uint64_t w = (uint64_t)OP_IDENT;
-        w |= (uint64_t)a.kind << 7 | (uint64_t)(a.idx & 15) << 9;
-        w |= (uint64_t)lo << 24 | (uint64_t)hi << 29 | (uint64_t)hi << 34;
-        w |= (uint64_t)tape << 39;   // the identity's partial is +1: no tape slot
-        out[nins++] = w;
+        Ins w = {};
+        w.fid = OP_IDENT;
+        w.ak = a.kind;
+        w.ai = a.idx;
+        w.lo = s.cc[0];
+        w.mid = w.hi = s.cc[n];
+        w.tape = tape;     // the identity's partial is +1: no tape slot
+        set_flags(w);
+        s.ins.push_back(w);
     }
-    if (tape > 255) return CO_ERR_BOUNDS;
     if (live_slots != 0) return CO_ERR_PROGRAM;
-    *n_ins = nins;
-    *stack_depth = depth;
     *tape_slots = tape;
     *slots_used = max_slots;
     return CO_OK;
 }
 
-int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
-                      const int32_t *ci, const TreeMeta *metas, uint64_t *prog,
-                      int32_t *order, int32_t *bin_start, ExprDesc *descs,
-                      int32_t *stack, int32_t *n_ins, Plan *plan) {
-    if (!h || !metas) return CO_ERR_NULLARG;
-    if (h->total_nodes > 0 && (!nt || !nv || !ci)) return CO_ERR_NULLARG;
-    if (h->M_prob < 0 || h->N < 0 || h->n_vars < 0 || h->total_nodes < 0 || h->total_c < 0)
-        return CO_ERR_NULLARG;
-    if (h->K_max > CO_MAX_K || h->max_stack > CO_MAX_STACK || h->n_vars > CO_MAX_VARS)
-        return CO_ERR_BOUNDS;
-    const int M = h->M_prob;
-    long ksum = 0, nsum = 0;
-    for (int m = 0; m < M; m++) { ksum += metas[m].K; nsum += metas[m].n_nodes; }
-    if (ksum != (long)h->total_c) return CO_ERR_SUM_C;
-    if (nsum != (long)h->total_nodes) return CO_ERR_SUM_NODES;
-
-    std::vector<uint64_t> tmp;
-    if (!prog) {
-        tmp.assign(h->total_nodes > 0 ? h->total_nodes : 1, 0);
-        prog = tmp.data();
-    }
-    std::vector<int> count(CO_MAX_K + 1, 0);
-    std::vector<int32_t> depth(M), tapes(M), poff(M), nins(M), slots(M), rcs(M, CO_OK);
-    std::vector<int64_t> cost(descs ? M : 0);
-    // programs are laid out expression after expression (prefix sum of
-    // n_nodes), which equals node_offset for well-formed populations and
-    // keeps overlapping metas from aliasing each other's instructions
-    int64_t run = 0;
-    for (int m = 0; m < M; m++) {
-        const TreeMeta &t = metas[m];
-        if (t.K < 0 || t.n_nodes < 0 || t.node_offset < 0 || t.c_offset < 0 ||
-            (long)t.node_offset + t.n_nodes > (long)h->total_nodes ||
-            (long)t.c_offset + t.K > (long)h->total_c)
-            return CO_ERR_PROGRAM;
-        if (t.K > CO_MAX_K) return CO_ERR_BOUNDS;
-        poff[m] = (int32_t)run;
-        run += t.n_nodes;
-    }
-    // expressions decode independently: contiguous chunks on host threads for
-    // large populations (C5's 1.7 M nodes take 32 ms on one thread); the code
-    // returned is that of the first failing expression, as on one thread
-    auto decode_range = [&](int m0, int m1) {
-        TreeScratch s;
-        for (int m = m0; m < m1; m++) {
-            const TreeMeta &t = metas[m];
-            uint64_t *out = prog + poff[m];
-            if (t.n_nodes > 0) memset(out, 0, sizeof(uint64_t) * t.n_nodes);
-            rcs[m] = decode_tree(nt + t.node_offset, nv + t.node_offset, ci + t.node_offset,
-                                 t.n_nodes, t.K, h->n_vars, out, &nins[m], &depth[m], &tapes[m],
-                                 &slots[m], s);
-            if (rcs[m] != CO_OK) return;
-            if (descs) {
-                // launch-order estimate: fixed per-pass cost plus op_cost per instruction
-                int64_t c = 229;
-                for (int i = 0; i < nins[m]; i++) c += op_cost(ins_fid(out[i]));
-                cost[m] = c;
-            }
-        }
-    };
-    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-    const int nthreads = (int)std::min<int64_t>(std::min(16u, hw), run / 65536 + 1);
+// Runs fn(m0, m1) over contiguous chunks of [0, M) on up to nthreads host
+// threads (fewer threads than chunks when the system refuses more: the chunks
+// already started finish, then fn runs over everything on this thread).
+template <typename Fn, typename Redo>
+static void chunked(int M, int nthreads, const Fn &fn, const Redo &redo) {
     bool done = false;
     if (nthreads > 1) {
         std::vector<std::thread> pool;
@@ -289,19 +278,114 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
             const int chunk = (M + nthreads - 1) / nthreads;
             for (int i = 0; i < nthreads; i++) {
                 const int m0 = i * chunk, m1 = std::min(M, m0 + chunk);
-                if (m0 < m1) pool.emplace_back(decode_range, m0, m1);
+                if (m0 < m1) pool.emplace_back(std::cref(fn), m0, m1);
             }
             done = true;
         } catch (...) {
-            // no more threads: the started chunks finish, then all of it again on this one
+            // no more threads
         }
         for (std::thread &th : pool) th.join();
     }
-    if (!done) {
-        std::fill(rcs.begin(), rcs.end(), CO_OK);
-        decode_range(0, M);
+    if (!done) redo(0, M);
+}
+
+int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
+                      const int32_t *ci, const TreeMeta *metas, uint64_t *prog,
+                      int32_t *order, int32_t *bin_start, ExprDesc *descs,
+                      int32_t *stack, int32_t *n_ins, int32_t *prog_off, int32_t *route,
+                      Plan *plan) {
+    if (!h || !metas) return CO_ERR_NULLARG;
+    if (h->total_nodes > 0 && (!nt || !nv || !ci)) return CO_ERR_NULLARG;
+    if (h->M_prob < 0 || h->N < 0 || h->n_vars < 0 || h->total_nodes < 0 || h->total_c < 0)
+        return CO_ERR_NULLARG;
+    if (h->K_max > CO_MAX_K || h->max_stack > CO_MAX_STACK || h->n_vars > CO_MAX_VARS)
+        return CO_ERR_BOUNDS;
+    const int M = h->M_prob, D = h->n_vars;
+    long ksum = 0, nsum = 0;
+    for (int m = 0; m < M; m++) { ksum += metas[m].K; nsum += metas[m].n_nodes; }
+    if (ksum != (long)h->total_c) return CO_ERR_SUM_C;
+    if (nsum != (long)h->total_nodes) return CO_ERR_SUM_NODES;
+
+    std::vector<uint64_t> tmp;
+    if (!prog) {
+        tmp.assign(h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1, 0);
+        prog = tmp.data();
     }
+    for (int m = 0; m < M; m++) {
+        const TreeMeta &t = metas[m];
+        if (t.K < 0 || t.n_nodes < 0 || t.node_offset < 0 || t.c_offset < 0 ||
+            (long)t.node_offset + t.n_nodes > (long)h->total_nodes ||
+            (long)t.c_offset + t.K > (long)h->total_c)
+            return CO_ERR_PROGRAM;
+        if (t.K > CO_MAX_K) return CO_ERR_BOUNDS;
+    }
+    std::vector<int32_t> depth(M, 0), tapes(M, 0), poff(M), nins(M, 0), slots(M, 0);
+    std::vector<int32_t> rcs(M, CO_OK), gen(M, 0);
+    std::vector<int64_t> cost(descs ? M : 0);
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const int nthreads = (int)std::min<int64_t>(std::min(16u, hw), nsum / 65536 + 1);
+    // phase 1: check every expression, its stack depth and so its kernel
+    auto check_range = [&](int m0, int m1) {
+        TreeScratch s;
+        for (int m = m0; m < m1; m++) {
+            const TreeMeta &t = metas[m];
+            rcs[m] = check_tree(nt + t.node_offset, nv + t.node_offset, ci + t.node_offset,
+                                t.n_nodes, t.K, D, &depth[m], s);
+            gen[m] = co_fast_path(t.K, depth[m], t.n_nodes, D) ? 0 : 1;
+        }
+    };
+    chunked(M, nthreads, check_range, check_range);
+    for (int m = 0; m < M; m++)
+        if (rcs[m] != CO_OK) return rcs[m];
+    // programs are laid out expression after expression: n_nodes words in the
+    // fast format, 2 * n_nodes in the wide one (node_offset order would let
+    // overlapping metas alias each other's instructions)
+    int64_t run = 0;
+    int n_gen = 0;
+    for (int m = 0; m < M; m++) {
+        poff[m] = (int32_t)run;
+        run += (int64_t)metas[m].n_nodes * (gen[m] ? 2 : 1);
+        n_gen += gen[m];
+    }
+    // phase 2: emit and encode (expressions decode independently; C5's 1.7 M
+    // nodes take 32 ms on one thread)
+    auto emit_range = [&](int m0, int m1) {
+        TreeScratch s;
+        for (int m = m0; m < m1; m++) {
+            const TreeMeta &t = metas[m];
+            const int32_t *tnt = nt + t.node_offset;
+            const float *tnv = nv + t.node_offset;
+            const int32_t *tci = ci + t.node_offset;
+            uint64_t *out = prog + poff[m];
+            const int words = t.n_nodes * (gen[m] ? 2 : 1);
+            if (words > 0) memset(out, 0, sizeof(uint64_t) * words);
+            int dd = 0;
+            rcs[m] = check_tree(tnt, tnv, tci, t.n_nodes, t.K, D, &dd, s);
+            if (rcs[m] == CO_OK)
+                rcs[m] = emit_tree(tnt, tnv, tci, t.n_nodes, D, gen[m] ? kMaxSlotsWide : kMaxSlots,
+                                   &tapes[m], &slots[m], s);
+            if (rcs[m] != CO_OK) return;
+            nins[m] = (int32_t)s.ins.size();
+            if (!gen[m] && tapes[m] > 255) {   // 8-bit tape field (n <= 255 keeps it below)
+                rcs[m] = CO_ERR_BOUNDS;
+                return;
+            }
+            int64_t c = 229;
+            for (int i = 0; i < nins[m]; i++) {
+                if (gen[m]) encode_wide(s.ins[i], out + 2 * i);
+                else out[i] = encode_fast(s.ins[i]);
+                c += op_cost(s.ins[i].fid);
+            }
+            if (descs) cost[m] = c;
+        }
+    };
+    auto emit_all = [&](int m0, int m1) {
+        std::fill(rcs.begin(), rcs.end(), CO_OK);
+        emit_range(m0, m1);
+    };
+    chunked(M, nthreads, emit_range, emit_all);
     int max_tape = 0, max_n = 0, max_slots = 0;
+    std::vector<int> count(CO_MAX_K + 1, 0);
     for (int m = 0; m < M; m++) {
         if (rcs[m] != CO_OK) return rcs[m];
         if (tapes[m] > max_tape) max_tape = tapes[m];
@@ -319,14 +403,17 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
     if (bin_start) memcpy(bin_start, start.data(), sizeof(int32_t) * (CO_MAX_K + 2));
     if (stack) memcpy(stack, depth.data(), sizeof(int32_t) * M);
     if (n_ins) memcpy(n_ins, nins.data(), sizeof(int32_t) * M);
+    if (prog_off) memcpy(prog_off, poff.data(), sizeof(int32_t) * M);
+    if (route) memcpy(route, gen.data(), sizeof(int32_t) * M);
     if (descs) {
-        // launch positions: K bins largest K first; within a bin the costliest
-        // programs first (fixed per-pass cost plus op_cost of each
-        // instruction), so the longest-running workgroups start earliest and
-        // a bin ends on cheap ones. Ties keep the order of ord reversed.
-        // two stable counting-sort passes over reversed ord: by cost
-        // descending (clamped to kCostBuckets), then by K descending; ties
-        // keep the order of ord reversed
+        // launch positions: the general kernel's bin first, then the fast K
+        // bins, largest K first; within a bin by K descending (the general
+        // bin) and the costliest programs first (fixed per-pass cost plus
+        // op_cost of each instruction), so the longest-running workgroups
+        // start earliest and a bin ends on cheap ones. Three stable counting
+        // sorts over reversed ord: by cost descending (clamped to
+        // kCostBuckets), by K descending, by kernel (general first); ties keep
+        // the order of ord reversed
         constexpr int kCostBuckets = 1 << 15;
         std::vector<int32_t> a(M), launch(M);
         for (int p = 0; p < M; p++) a[p] = ord[M - 1 - p];
@@ -342,7 +429,8 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
         for (int p = 0; p < M; p++) knext[CO_MAX_K - metas[launch[p]].K + 1]++;
         for (int i = 0; i <= CO_MAX_K; i++) knext[i + 1] += knext[i];
         for (int p = 0; p < M; p++) a[knext[CO_MAX_K - metas[launch[p]].K]++] = launch[p];
-        launch.swap(a);
+        int gpos = 0, fpos = n_gen;
+        for (int p = 0; p < M; p++) launch[gen[a[p]] ? gpos++ : fpos++] = a[p];
         for (int p = 0; p < M; p++) {
             const int m = launch[p];
             ExprDesc &d = descs[p];
@@ -353,7 +441,7 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
             d.y_row = m;
             d.tape = tapes[m];
             d.slots = slots[m];
-            d.pad = 0;
+            d.gen = gen[m];
         }
     }
     if (plan) {
@@ -365,6 +453,8 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
         plan->max_tape = max_tape;
         plan->max_n = max_n;
         plan->max_slots = max_slots;
+        plan->words = run;
+        plan->n_gen = n_gen;
     }
     return CO_OK;
 }

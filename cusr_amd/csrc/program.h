@@ -41,6 +41,17 @@
 // Constants are ranked in prefix order (cusr/benchmark/popio.py:87-91), so the
 // constants of a subtree form one contiguous rank range; forward AD scales
 // only those ranks.
+//
+// The general kernel (expressions outside co_fast_path: K up to 32, a value
+// stack up to 64, any number of nodes, up to 255 variables) reads the same
+// fields from two 64-bit words per instruction, wide enough for its ranges:
+//   word 0: bits  0..5   fid         bit 6 binary
+//           bits  7..8   a_kind      bits  9..16 a_idx
+//           bits 17..18  b_kind      bits 19..26 b_idx
+//           bit  27      to_slot     bits 28..35 d_idx
+//           bits 36..40  sel, scale_a, scale_b, tape_a, tape_b
+//   word 1: bits  0..7   lo          bits  8..15 mid      bits 16..23 hi
+//           bits 24..55  tape
 #pragma once
 
 #include <stdint.h>
@@ -51,17 +62,18 @@ namespace cusr {
 
 enum { OPD_ACC = 0, OPD_VAR = 1, OPD_CONST = 2, OPD_SLOT = 3 };
 constexpr int OP_IDENT = 63;
-constexpr int kMaxSlots = 16;
+constexpr int kMaxSlots = 16;                    // fast format (4-bit slot index)
+constexpr int kMaxSlotsWide = CO_MAX_STACK;      // wide format
 
 struct ExprDesc {          // one per expression, device-resident
-    int32_t prog_off;      // first instruction
+    int32_t prog_off;      // first program word
     int32_t n;             // instructions
     int32_t c_off;         // constants offset
     int32_t K;             // constants
     int32_t y_row;         // row of ym / output index (original expression index)
     int32_t tape;          // reverse-mode tape slots
     int32_t slots;         // spill slots
-    int32_t pad;
+    int32_t gen;           // 1: wide program, general kernel
 };
 
 static inline __host__ __device__ int ins_fid(uint64_t w) { return (int)(w & 63u); }
@@ -82,20 +94,48 @@ static inline __host__ __device__ int ins_scale_b(uint64_t w) { return (int)((w 
 static inline __host__ __device__ int ins_tape_a(uint64_t w) { return (int)((w >> 50) & 1u); }
 static inline __host__ __device__ int ins_tape_b(uint64_t w) { return (int)((w >> 51) & 1u); }
 
+// wide-format fields (word 0 a, word 1 b)
+struct Wide {
+    uint64_t a, b;
+};
+static inline __host__ __device__ int wins_fid(uint64_t a) { return (int)(a & 63u); }
+static inline __host__ __device__ int wins_binary(uint64_t a) { return (int)((a >> 6) & 1u); }
+static inline __host__ __device__ int wins_akind(uint64_t a) { return (int)((a >> 7) & 3u); }
+static inline __host__ __device__ int wins_aidx(uint64_t a) { return (int)((a >> 9) & 255u); }
+static inline __host__ __device__ int wins_bkind(uint64_t a) { return (int)((a >> 17) & 3u); }
+static inline __host__ __device__ int wins_bidx(uint64_t a) { return (int)((a >> 19) & 255u); }
+static inline __host__ __device__ int wins_toslot(uint64_t a) { return (int)((a >> 27) & 1u); }
+static inline __host__ __device__ int wins_didx(uint64_t a) { return (int)((a >> 28) & 255u); }
+static inline __host__ __device__ int wins_sel(uint64_t a) { return (int)((a >> 36) & 1u); }
+static inline __host__ __device__ int wins_scale_a(uint64_t a) { return (int)((a >> 37) & 1u); }
+static inline __host__ __device__ int wins_scale_b(uint64_t a) { return (int)((a >> 38) & 1u); }
+static inline __host__ __device__ int wins_tape_a(uint64_t a) { return (int)((a >> 39) & 1u); }
+static inline __host__ __device__ int wins_tape_b(uint64_t a) { return (int)((a >> 40) & 1u); }
+static inline __host__ __device__ int wins_lo(uint64_t b) { return (int)(b & 255u); }
+static inline __host__ __device__ int wins_mid(uint64_t b) { return (int)((b >> 8) & 255u); }
+static inline __host__ __device__ int wins_hi(uint64_t b) { return (int)((b >> 16) & 255u); }
+static inline __host__ __device__ int wins_tape(uint64_t b) { return (int)((b >> 24) & 0xffffffffu); }
+
 struct Plan {
     int32_t M, N, D, total_nodes, total_c;
     int32_t max_tape, max_n, max_slots;
+    int64_t words;         // program words (fast: 1 per instruction, wide: 2)
+    int32_t n_gen;         // expressions of the general kernel
 };
 
 // Check a population and decode it. Returns a CO_* code. On success fills
-// prog[total_nodes] (expression m's instructions start at the prefix sum of
-// n_nodes; entries past its instruction count are 0), order[M] (stable K bins,
-// ascending), bin_start[CO_MAX_K+2], descs[M] (by launch position: largest K
-// first), stack[M] (value-stack depth, by expression), n_ins[M] (instructions
-// per expression). Any output pointer may be null.
+// prog[2 * total_nodes] (expression m's program starts at word prog_off[m]:
+// programs are laid out expression after expression, n_nodes words for the
+// fast format and 2 * n_nodes for the wide one; words past its instructions
+// are 0), order[M] (stable K bins, ascending), bin_start[CO_MAX_K+2],
+// descs[M] (by launch position: the general kernel's bin first, then the fast
+// K bins, largest K first), stack[M] (value-stack depth, by expression),
+// n_ins[M] (instructions per expression), prog_off[M], route[M] (1: general
+// kernel). Any output pointer may be null.
 int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
                       const int32_t *ci, const TreeMeta *metas, uint64_t *prog,
                       int32_t *order, int32_t *bin_start, ExprDesc *descs,
-                      int32_t *stack, int32_t *n_ins, Plan *plan);
+                      int32_t *stack, int32_t *n_ins, int32_t *prog_off, int32_t *route,
+                      Plan *plan);
 
 }  // namespace cusr

@@ -44,7 +44,9 @@ def _eligible(nt, n_vars):
 
     nt = np.asarray(nt)
     K = int(np.sum(nt == popio.NODE_CONST))
-    return (len(nt) <= ci.CO_MAX_NODES and K <= ci.CO_MAX_K and n_vars <= ci.CO_MAX_VARS
+    # the reference bridge's rule (kernel_bridge.py:45-46,66-71): K and the
+    # value stack within the library's bounds
+    return (K <= ci.CO_MAX_K and n_vars <= ci.CO_MAX_VARS
             and popio.stack_depth(nt) <= ci.CO_MAX_STACK and not np.any(nt > popio.NODE_BFUNC))
 
 

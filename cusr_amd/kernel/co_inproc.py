@@ -36,10 +36,15 @@ CO_ERR_OOM = -5
 CO_ERR_PROGRAM = -6
 CO_ERR_DATA = -7
 
-CO_MAX_K = 16
-CO_MAX_STACK = 16
-CO_MAX_VARS = 8
-CO_MAX_NODES = 255
+# bounds (include/cusr_co.h): K and value stack as the reference's
+# (cusr/kernel/ad_interp.cuh:34-39), variables up to 255, any number of nodes
+CO_MAX_K = 32
+CO_MAX_STACK = 64
+CO_MAX_VARS = 255
+# the fast kernels' share (co_fast_path); the general kernel fits the rest
+CO_FAST_MAX_K, CO_FAST_MAX_STACK, CO_FAST_MAX_VARS, CO_FAST_MAX_NODES = 16, 16, 8, 255
+CO_GENERAL_BIN = CO_FAST_MAX_K + 1
+CO_BINS = CO_FAST_MAX_K + 2
 
 CO_AD_FORWARD, CO_AD_REVERSE = 0, 1
 CO_PREC_FP64, CO_PREC_MIXED = 0, 1
@@ -50,7 +55,7 @@ STATUS_CONVERGED, STATUS_MAXITER, STATUS_FAIL_NAN, STATUS_K0_SKIP, STATUS_FAIL_C
 
 _ERR_MSG = {
     CO_ERR_BOUNDS: (f"beyond device bounds (K<={CO_MAX_K}, max_stack<={CO_MAX_STACK}, "
-                    f"n_vars<={CO_MAX_VARS}, n_nodes<={CO_MAX_NODES})"),
+                    f"n_vars<={CO_MAX_VARS}), or LDS rows beyond the device's LDS"),
     CO_ERR_CUDA: "HIP error inside the library",
     CO_ERR_SUM_C: "sum(metas.K) != header.total_c (pop inconsistent)",
     CO_ERR_SUM_NODES: "sum(metas.n_nodes) != header.total_nodes (pop inconsistent)",
@@ -91,7 +96,8 @@ class CoOptions(ctypes.Structure):
                 ("lambda0", ctypes.c_double), ("xtol", ctypes.c_double),
                 ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
                 ("lm_order", ctypes.c_int32), ("tail_iter", ctypes.c_int32),
-                ("tail_partitions", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3)]
+                ("tail_partitions", ctypes.c_int32), ("f32_range", ctypes.c_int32),
+                ("reserved", ctypes.c_int32 * 2)]
 
 
 assert ctypes.sizeof(PopHeader) == 64
@@ -105,7 +111,7 @@ _HERE = Path(__file__).resolve().parent
 EXPORTED = ("co_init", "co_optimize", "co_last_split", "co_teardown", "co_options_default",
             "co_optimize_ex", "co_eval_ex", "co_upload_ex", "co_fit_resident",
             "co_last_kernel_ms", "co_last_bin_ms", "co_decode", "co_data_upload",
-            "co_optimize_data", "co_data_upload_device")
+            "co_optimize_data", "co_data_upload_device", "co_narrow_fp32")
 
 
 def lib_path(variant: str = "ad") -> Path:
@@ -183,8 +189,10 @@ def _bind(lib) -> None:
     lib.co_last_kernel_ms.restype = ctypes.c_int
     lib.co_last_bin_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
     lib.co_last_bin_ms.restype = ctypes.c_int
-    lib.co_decode.argtypes = [ctypes.POINTER(PopHeader)] + [_VP] * 8
+    lib.co_decode.argtypes = [ctypes.POINTER(PopHeader)] + [_VP] * 10
     lib.co_decode.restype = ctypes.c_int
+    lib.co_narrow_fp32.argtypes = [ctypes.POINTER(PopHeader)] + [_VP] * 9
+    lib.co_narrow_fp32.restype = ctypes.c_int
     lib.co_last_split.argtypes = [ctypes.POINTER(dbl), ctypes.POINTER(dbl)]
     lib.co_last_split.restype = ctypes.c_int
     lib.co_teardown.argtypes = [_VP]
@@ -213,9 +221,17 @@ def load_library(variant: str = "ad", path: str | Path | None = None) -> ctypes.
     return _LIBS[key]
 
 
-def decode(pop: dict, variant: str = "ad"):
-    """Host-only decode: (rc, program uint64[T], order int32[M], bin_start int32[K+2],
-    stack int32[M]). Needs no GPU."""
+def co_fast_path(K: int, stack_depth: int, n_nodes: int, n_vars: int) -> bool:
+    """include/cusr_co.h co_fast_path: the fast kernels take the expression."""
+    return (K <= CO_FAST_MAX_K and stack_depth <= CO_FAST_MAX_STACK
+            and n_nodes <= CO_FAST_MAX_NODES and n_vars <= CO_FAST_MAX_VARS)
+
+
+def decode(pop: dict, variant: str = "ad", full: bool = False):
+    """Host-only decode: (rc, program uint64[2T], order int32[M], bin_start
+    int32[CO_MAX_K+2], stack int32[M]); with full, also program_off int32[M]
+    (first word of each program) and route int32[M] (1: general kernel, two
+    words per instruction). Needs no GPU."""
     lib = load_library(variant)
     h = _header(pop)
     T, M = int(pop["total_nodes"]), int(pop["M"])
@@ -223,14 +239,44 @@ def decode(pop: dict, variant: str = "ad"):
     nv, pnv = _arr(pop["nv"], np.float32)
     ci, pci = _arr(pop["ci"], np.int32)
     me, pme = _metas(pop)
-    prog = np.zeros(max(T, 1), np.uint64)
+    prog = np.zeros(max(2 * T, 1), np.uint64)
     order = np.zeros(max(M, 1), np.int32)
     bins = np.zeros(CO_MAX_K + 2, np.int32)
     stack = np.zeros(max(M, 1), np.int32)
+    poff = np.zeros(max(M, 1), np.int32)
+    route = np.zeros(max(M, 1), np.int32)
     rc = lib.co_decode(ctypes.byref(h), pnt, pnv, pci, pme, prog.ctypes.data_as(_VP),
                        order.ctypes.data_as(_VP), bins.ctypes.data_as(_VP),
-                       stack.ctypes.data_as(_VP))
-    return rc, prog[:T], order[:M], bins, stack[:M]
+                       stack.ctypes.data_as(_VP), poff.ctypes.data_as(_VP),
+                       route.ctypes.data_as(_VP))
+    out = (rc, prog[:2 * T], order[:M], bins, stack[:M])
+    return out + (poff[:M], route[:M]) if full else out
+
+
+def narrow_fp32(pop: dict, fit: dict, variant: str = "ad") -> dict:
+    """The fp32 carrier of co_optimize applied to an fp64 fit's results
+    (co_narrow_fp32, host only): {'c_final', 'status', 'loss_init',
+    'loss_final', 'demoted'}; an expression whose finite fp64 constants or loss
+    overflow fp32 gets its c_init back and CONVERGED becomes MAXITER."""
+    lib = load_library(variant)
+    h = _header(pop)
+    M, C = int(pop["M"]), int(pop["total_c"])
+    me, pme = _metas(pop)
+    c0, pc0 = _sized(pop["c_init"], np.float64, C, "c_init")
+    cf, pcf = _sized(fit["c_final"], np.float64, C, "c_final")
+    li, pli = _sized(fit["loss_init"], np.float64, M, "loss_init")
+    lf, plf = _sized(fit["loss_final"], np.float64, M, "loss_final")
+    st = np.array(fit["status"], np.int32, copy=True)
+    c32 = np.zeros(max(C, 1), np.float32)
+    li32 = np.zeros(max(M, 1), np.float32)
+    lf32 = np.zeros(max(M, 1), np.float32)
+    rc = lib.co_narrow_fp32(ctypes.byref(h), pme, pc0, pcf, pli, plf, st.ctypes.data_as(_VP),
+                            c32.ctypes.data_as(_VP), li32.ctypes.data_as(_VP),
+                            lf32.ctypes.data_as(_VP))
+    if rc < 0:
+        raise COError(rc, "co_narrow_fp32")
+    return {"c_final": c32[:C], "status": st, "loss_init": li32[:M], "loss_final": lf32[:M],
+            "demoted": rc}
 
 
 def default_options(**kw) -> CoOptions:
@@ -309,19 +355,21 @@ class InProcessCO:
     def optimize_ex(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                     precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                     fp64_guard: bool = True, partitions: int = 0, lm_order: int | None = None,
-                    tail_iter: int = 0, tail_partitions: int = 0,
+                    tail_iter: int = 0, tail_partitions: int = 0, f32_range: bool = False,
                     c_init=None, xs=None, ym=None) -> dict:
         """fp64 fit; c_init/xs/ym override the pop's (fp32) arrays when given.
         partitions: point partitions per expression (0: by N). lm_order: None
         keeps the library's default (CO_ORDER_IMPROVE_FIRST for the ad
-        library, CO_ORDER_CONVERGE_FIRST for fd)."""
+        library, CO_ORDER_CONVERGE_FIRST for fd). f32_range: trial constants
+        held in fp32 and losses in its range, as co_optimize fits."""
         self._check()
         M, C = int(pop["M"]), int(pop["total_c"])
         h = _header(pop)
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
                             fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
-                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions))
+                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions),
+                            f32_range=1 if f32_range else 0)
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
@@ -437,7 +485,7 @@ class InProcessCO:
     def optimize_data(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                       precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                       fp64_guard: bool = True, partitions: int = 0, lm_order: int | None = None,
-                    tail_iter: int = 0, tail_partitions: int = 0,
+                    tail_iter: int = 0, tail_partitions: int = 0, f32_range: bool = False,
                       c_init=None) -> dict:
         """optimize_ex against the uploaded data set: pop's xs and ym are not
         read or sent; only the programs and constants go to the device."""
@@ -447,7 +495,8 @@ class InProcessCO:
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
                             fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
-                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions))
+                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions),
+                            f32_range=1 if f32_range else 0)
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
@@ -474,7 +523,7 @@ class InProcessCO:
     def fit_resident(self, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                      precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                      fp64_guard: bool = True, outputs: bool = True, partitions: int = 0,
-                     tail_iter: int = 0, tail_partitions: int = 0,
+                     tail_iter: int = 0, tail_partitions: int = 0, f32_range: bool = False,
                      lm_order: int | None = None):
         """Fit the uploaded population again; outputs=False leaves results on the device."""
         self._check()
@@ -482,7 +531,8 @@ class InProcessCO:
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
                             fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
-                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions))
+                            tail_iter=int(tail_iter), tail_partitions=int(tail_partitions),
+                            f32_range=1 if f32_range else 0)
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
         if not outputs:
             rc = self._lib.co_fit_resident(self._handle, ctypes.byref(o), None, None, None, None, None)
@@ -512,8 +562,9 @@ class InProcessCO:
         return v.value
 
     def last_bin_ms(self) -> np.ndarray:
-        """Per-K-bin kernel durations of the last fit (ms, -1 for empty bins)."""
-        v = (ctypes.c_double * (CO_MAX_K + 1))()
+        """Per-bin kernel durations of the last fit (ms, -1 for empty bins):
+        [k] the fast kernel of K = k, [CO_GENERAL_BIN] the general kernel."""
+        v = (ctypes.c_double * CO_BINS)()
         rc = self._lib.co_last_bin_ms(self._handle, v)
         if rc != CO_OK:
             raise COError(rc, "co_last_bin_ms")

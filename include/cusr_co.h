@@ -24,7 +24,8 @@ extern "C" {
 /* Return codes (cusr/kernel/co_lib.h:27-41, plus CO_ERR_PROGRAM and
  * CO_ERR_DATA). */
 #define CO_OK 0
-#define CO_ERR_BOUNDS 2      /* K_max, max_stack, n_vars or n_nodes beyond the device limits */
+#define CO_ERR_BOUNDS 2      /* K_max, max_stack or n_vars beyond the bounds below, or
+                                LDS rows beyond the device's LDS */
 #define CO_ERR_CUDA (-1)     /* HIP runtime error */
 #define CO_ERR_SUM_C (-2)    /* sum(K) != header.total_c */
 #define CO_ERR_SUM_NODES (-3) /* sum(n_nodes) != header.total_nodes */
@@ -37,15 +38,42 @@ extern "C" {
 #define CO_ERR_DATA (-7)     /* co_optimize_data: no data set uploaded, or the header's
                                 N / n_vars differ from the uploaded one;
                                 co_data_upload_device: a pointer that is not
-                                device memory of the handle's device */
+                                device memory of the handle's device, or an
+                                extent that runs past its allocation */
 
-/* Device limits of this build (the reference's are MAX_K=32, MAX_STACK=64,
- * cusr/kernel/ad_interp.cuh:34-39). Populations beyond them get CO_ERR_BOUNDS
- * before anything is copied to the device. */
-#define CO_MAX_K 16
-#define CO_MAX_STACK 16
-#define CO_MAX_VARS 8
-#define CO_MAX_NODES 255
+/* Bounds of this build. K and the value stack are the reference's
+ * (MAX_K = 32, MAX_STACK = 64, cusr/kernel/ad_interp.cuh:34-39, checked on the
+ * header like cusr/kernel/co_lib.cu:211-212 and again per expression); the
+ * reference has no bound on n_vars or on nodes per expression. Populations
+ * beyond them get CO_ERR_BOUNDS before anything is copied to the device, and
+ * so does a launch whose per-wavefront LDS rows (inputs, spill slots, reverse
+ * tape) exceed the device's LDS. */
+#define CO_MAX_K 32
+#define CO_MAX_STACK 64
+#define CO_MAX_VARS 255
+
+/* Two kernel families fit an expression. The fast kernels, one instance per
+ * K (0..CO_FAST_MAX_K), take expressions with K <= CO_FAST_MAX_K, a value
+ * stack <= CO_FAST_MAX_STACK and <= CO_FAST_MAX_NODES nodes, in populations
+ * with n_vars <= CO_FAST_MAX_VARS; the general kernel (runtime K, one point
+ * per lane, matrix-instruction sums) takes every other expression. The
+ * choice is a function of the expression and n_vars only, and part of the
+ * arithmetic order: the general kernel forms every sum of a Jacobian pass
+ * (r^2, J^T r and J^T J) as one fused multiply-add chain per entry over the
+ * points in ascending order (see CO_SUMS_MATRIX_MIN_K), whatever K. */
+#define CO_FAST_MAX_K 16
+#define CO_FAST_MAX_STACK 16
+#define CO_FAST_MAX_VARS 8
+#define CO_FAST_MAX_NODES 255
+static inline int co_fast_path(int K, int stack_depth, int n_nodes, int n_vars) {
+    return K <= CO_FAST_MAX_K && stack_depth <= CO_FAST_MAX_STACK &&
+           n_nodes <= CO_FAST_MAX_NODES && n_vars <= CO_FAST_MAX_VARS;
+}
+
+/* Launches of one fit: the K bins 0..CO_FAST_MAX_K of the fast kernels, then
+ * the general kernel's bin (index CO_GENERAL_BIN). */
+#define CO_GENERAL_BIN (CO_FAST_MAX_K + 1)
+#define CO_BINS (CO_FAST_MAX_K + 2)
 
 /* Jacobian mode and arithmetic of a fit (extension). */
 #define CO_AD_FORWARD 0
@@ -83,7 +111,17 @@ typedef struct CoOptions {
                            at once.
                            0: co_tail_iter_for; -1: one launch, no tail */
     int32_t tail_partitions; /* partitions of the tail (1, 2 or 4; 0: 4) */
-    int32_t reserved[3];
+    int32_t f32_range;  /* 1: constants held in fp32 and losses in its range,
+                           as in the reference's fp32 fit: each trial point is
+                           rounded to fp32 (so the delivered constants are
+                           exactly representable and loss_final is the fp64
+                           loss at them); a trial constant or loss that is
+                           +-inf in fp32 (or a start loss so) counts as a
+                           non-finite trial, FAIL_NAN with the last accepted
+                           constants kept (cusr/kernel/batch_lm_ad.cu:437-443).
+                           co_optimize and the CLI on float32 files set it;
+                           default 0 */
+    int32_t reserved[2];
 } CoOptions;
 
 #define CO_ORDER_IMPROVE_FIRST 0
@@ -151,7 +189,8 @@ int co_init(int device_id, void **handle_out);
  * Inputs are host pointers read during the call. Outputs are caller-allocated
  * and sized to the current header: c_final_out[total_c], status_out[M_prob],
  * loss_init_out / loss_final_out [M_prob] (both may be NULL). The fit itself
- * runs in fp64 with forward AD; outputs are rounded to fp32. */
+ * runs in fp64 with forward AD, with constants and losses held to the fp32
+ * range (CoOptions.f32_range); outputs go through co_narrow_fp32. */
 int co_optimize(void *handle, const PopHeader *header,
                 const int32_t *nt, const float *nv, const int32_t *ci,
                 const TreeMeta *metas,
@@ -232,8 +271,9 @@ int co_data_upload(void *handle, int N, int n_vars, const double *xs, const doub
  * the data-residency half of the zero-copy entry its in-process plan
  * describes as the end state (docs/kernel/INPROCESS_CO_PLAN.md:69-75).
  * Returns as co_data_upload, and CO_ERR_DATA when a pointer is not device
- * memory of the handle's device; then nothing is copied and the previous data
- * set stays. */
+ * memory of the handle's device or its N * n_vars (N) doubles run past the end
+ * of the allocation it points into; then nothing is copied and the previous
+ * data set stays. */
 int co_data_upload_device(void *handle, int N, int n_vars, const double *xs_dev,
                           const double *y_dev);
 
@@ -253,27 +293,49 @@ int co_optimize_data(void *handle, const CoOptions *opt, const PopHeader *header
  * handle's stream before the first and after the last fit kernel. */
 int co_last_kernel_ms(void *handle, double *fit_ms_out);
 
-/* Per-launch device time of the last fit: bin_ms_out[k] (CO_MAX_K + 1
- * entries) is the duration of the fit kernel of the K = k bin, from HIP events
- * recorded around that launch on the stream it ran on; -1 for bins with no
+/* Per-launch device time of the last fit: bin_ms_out[k] (CO_BINS entries)
+ * is the duration of the fit launches of bin k (k <= CO_FAST_MAX_K: the fast
+ * kernel of K = k; CO_GENERAL_BIN: the general kernel), from HIP events
+ * recorded around them on the stream they ran on; -1 for bins with no
  * expressions. No counterpart in the reference (measurement only). */
 int co_last_bin_ms(void *handle, double *bin_ms_out);
+
+/* Host-only narrowing of an fp64 fit's results to the fp32 carrier of
+ * co_optimize (extension; co_optimize and the CLI's float32 blobs use it).
+ * Writes c_out[total_c], loss_init_out / loss_final_out [M_prob]; status[M_prob]
+ * is updated in place. The reference fits in fp32, so a constant it commits
+ * is representable there; an fp64 fit can leave a finite constant or loss
+ * beyond FLT_MAX. Such an expression (K > 0, a finite fp64 constant or final
+ * loss that is +-inf in fp32) is treated as the fp64 guard treats a
+ * non-finite loss (cusr/kernel/lm_core.cuh:299-351): its c_init is delivered,
+ * loss_final_out = loss_init_out, and CONVERGED becomes MAXITER. No device
+ * needed. Returns the number of expressions so treated (>= 0), or
+ * CO_ERR_NULLARG / CO_ERR_PROGRAM (metas beyond total_c). */
+int co_narrow_fp32(const PopHeader *header, const TreeMeta *metas, const double *c_init,
+                   const double *c_final, const double *loss_init, const double *loss_final,
+                   int32_t *status, float *c_out, float *loss_init_out, float *loss_final_out);
 
 /* Host-only decode of a population, no device needed: runs every check
  * co_optimize runs before touching the device and returns its code
  * (0, 2, -2, -3, -4, -6). When it returns 0 and the pointers are non-NULL:
- *   program_out[total_nodes]  one 64-bit instruction per node, in the order
- *                             the device executes it (last node first);
+ *   program_out[2*total_nodes] the device programs: expression m's
+ *                             instructions in the order the device executes
+ *                             them (last node first) from word
+ *                             program_off_out[m], one 64-bit word each for the
+ *                             fast kernels, two for the general kernel;
  *   order_out[M_prob]         expressions grouped by K ascending (stable);
- *                             the fit launches these bins largest K first;
  *   bin_start_out[CO_MAX_K+2] start of each K bin in order_out, with
  *                             bin_start_out[CO_MAX_K+1] == M_prob;
- *   stack_out[M_prob]         value-stack depth each expression needs. */
+ *   stack_out[M_prob]         value-stack depth each expression needs;
+ *   program_off_out[M_prob]   first word of expression m's program;
+ *   route_out[M_prob]         1 where the general kernel fits expression m
+ *                             (co_fast_path false), else 0. */
 int co_decode(const PopHeader *header,
               const int32_t *nt, const float *nv, const int32_t *ci,
               const TreeMeta *metas,
               uint64_t *program_out, int32_t *order_out,
-              int32_t *bin_start_out, int32_t *stack_out);
+              int32_t *bin_start_out, int32_t *stack_out,
+              int32_t *program_off_out, int32_t *route_out);
 
 #ifdef __cplusplus
 }

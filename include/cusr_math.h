@@ -21,8 +21,11 @@
  *         doubles subtracted by fma (Cody-Waite); Taylor series on
  *         [-pi/4, pi/4] to r^17 / r^18 (fp32: r^11 / r^12); cos uses the
  *         compensated 1 - z/2 step of fdlibm k_cos.c; quadrant by k mod 4.
- *         For |x| >= 2^50 (fp32: 2^21) the argument carries no phase
- *         information in the format and the functions return sin = 0, cos = 1.
+ *         For |x| >= 2^50 the reduction is Payne and Hanek's ("Radian
+ *         reduction for trigonometric functions", SIGNUM Newsletter 18,
+ *         1983): x = M 2^E, and only the 192 bits of 2/pi from weight
+ *         2^-(E-1) on matter for x 2/pi mod 4, a 53 x 192-bit integer
+ *         product. fp32 arguments from 2^21 are reduced in fp64.
  *   tan   sin/cos of the same reduction.
  *   sinh, cosh, tanh  Taylor series for |x| < 1 (sinh), exp otherwise.
  *   pow   integral |y| <= 64: binary powering (x^2, x^3 exact when
@@ -54,6 +57,7 @@
 #if defined(__HIP_DEVICE_COMPILE__) && !defined(CUSR_MATH_FOLD_TABLES)
 typedef const __attribute__((address_space(4))) double *cm_dtab;
 typedef const __attribute__((address_space(4))) float *cm_ftab;
+typedef const __attribute__((address_space(4))) uint64_t *cm_utab;
 #define CM_TABLE static __constant__ const
 #define CM_ACCESSOR(T, name)                                              \
     static __device__ __forceinline__ T name##_ptr() {                    \
@@ -65,6 +69,7 @@ typedef const __attribute__((address_space(4))) float *cm_ftab;
 #else
 typedef const double *cm_dtab;
 typedef const float *cm_ftab;
+typedef const uint64_t *cm_utab;
 #if defined(__HIP_DEVICE_COMPILE__)
 #define CM_TABLE static __constant__ const
 #else
@@ -290,28 +295,95 @@ CM_FN double cm_cos_kernel(double r, cm_dtab t) {
     return w + (((1.0 - w) - hz) + z * (z * p));
 }
 
-/* sin and cos of x from one argument reduction. Branch-free: NaN and +-inf
- * give NaN, |x| >= 2^50 gives sin 0 and cos 1, both through the reduction of
- * 0 and a final select; the quadrant k mod 4 swaps and negates. */
+/* The bits of 2/pi (cusr_amd/csrc/gen_two_over_pi.py, exact integer
+ * arithmetic): word 0 is zero, word j >= 1 holds the bits of weight
+ * 2^-(64(j-1)+1) .. 2^-64j, most significant first. */
+CM_TABLE uint64_t cm_two_over_pi[24] = {
+    0x0000000000000000ull, 0xA2F9836E4E441529ull, 0xFC2757D1F534DDC0ull,
+    0xDB6295993C439041ull, 0xFE5163ABDEBBC561ull, 0xB7246E3A424DD2E0ull,
+    0x06492EEA09D1921Cull, 0xFE1DEB1CB129A73Eull, 0xE88235F52EBB4484ull,
+    0xE99C7026B45F7E41ull, 0x3991D639835339F4ull, 0x9C845F8BBDF9283Bull,
+    0x1FF897FFDE05980Full, 0xEF2F118B5A0A6D1Full, 0x6D367ECF27CB09B7ull,
+    0x4F463F669E5FEA2Dull, 0x7527BAC7EBE5F17Bull, 0x3D0739F78A5292EAull,
+    0x6BFB5FB11F8D5D08ull, 0x56033046FC7B6BABull, 0xF0CFBC209AF4361Dull,
+    0xA9E391615EE61B08ull, 0x6599855F14A06840ull, 0x8DFFD8804D732731ull,
+};
+CM_ACCESSOR(cm_utab, cm_two_over_pi)
+
+/* Payne-Hanek reduction of a finite ax >= 2^50: returns r with |r| <= pi/4
+ * and sets *q so that ax = (4n + *q) pi/2 + r. ax = M 2^E with M the 53-bit
+ * integer significand (E >= -2). Bits of 2/pi of weight 2^-i with i <= E - 2
+ * add multiples of 4 to ax 2/pi; the 192 bits W from weight 2^-(E-1) on give
+ * ax 2/pi = M W 2^-190 (mod 4) with an error below 2^-137. Bits 190..191 of
+ * the product are the quadrant, the 128 below the fraction; a fraction
+ * >= 1/2 rounds the quadrant up and turns negative. The fraction goes to
+ * double-double and is multiplied by pi/2 (two doubles) with one fma for
+ * the product's rounding error. Integer steps are exact, so host and device
+ * agree to the bit. */
+CM_FN double cm_rem_pio2_huge(double ax, int *q, cm_dtab t) {
+    const uint64_t b = cm_bits(ax);
+    const int E = (int)((b >> 52) & 0x7ff) - 1075;
+    const uint64_t M = (b & 0xfffffffffffffull) | 0x10000000000000ull;
+    cm_utab w = CM_TAB(cm_utab, cm_two_over_pi);
+    const int bit = E + 62;                     /* stream position of weight 2^-(E-1) */
+    const int j = bit >> 6, sh = bit & 63;
+    const uint64_t a0 = w[j], a1 = w[j + 1], a2 = w[j + 2], a3 = w[j + 3];
+    const uint64_t w2 = sh ? (a0 << sh) | (a1 >> (64 - sh)) : a0;
+    const uint64_t w1 = sh ? (a1 << sh) | (a2 >> (64 - sh)) : a1;
+    const uint64_t w0 = sh ? (a2 << sh) | (a3 >> (64 - sh)) : a2;
+    typedef unsigned __int128 u128;
+    const u128 p0 = (u128)M * w0, p1 = (u128)M * w1, p2 = (u128)M * w2;
+    const uint64_t lo = (uint64_t)p0;
+    const u128 t1 = (p0 >> 64) + (u128)(uint64_t)p1;
+    const uint64_t mid = (uint64_t)t1;
+    const uint64_t hi = (uint64_t)(t1 >> 64) + (uint64_t)(p1 >> 64) + (uint64_t)p2;
+    const u128 g = ((u128)hi << 66) | ((u128)mid << 2) | (u128)(lo >> 62);
+    *q = (int)((hi >> 62) + (uint64_t)(g >> 127)) & 3;
+    const int64_t gh = (int64_t)(uint64_t)(g >> 64);   /* signed fraction, 2^-64 units */
+    const double fh = (double)gh;
+    const double fl = (double)(gh - (int64_t)fh) + (double)(uint64_t)g * 5.421010862427522e-20;
+    const double a = fh * 5.421010862427522e-20, bq = fl * 5.421010862427522e-20; /* 2^-64 */
+    const double rh = a * t[17];
+    const double rl = CM_FMA(a, t[17], -rh) + CM_FMA(a, t[18], bq * t[17]);
+    return rh + rl;
+}
+
+/* x - k pi/2 with k = rint(x 2/pi) for |x| < 2^50 (Cody-Waite, pi/2 in three
+ * doubles subtracted by fma); *q = k mod 4. */
+CM_FN double cm_rem_pio2_cw(double x, int *q, cm_dtab t) {
+    double kf = cm_rint_small(x * t[16]);
+    double r = CM_FMA(-kf, t[17], x);
+    r = CM_FMA(-kf, t[18], r);
+    r = CM_FMA(-kf, t[19], r);
+    double q4 = kf - 4.0 * cm_rint_small(kf * 0.25 - 0.375); /* kf mod 4, in 0..3 */
+    *q = (int)q4;
+    return r;
+}
+
+/* sin and cos of x from one argument reduction: NaN and +-inf give NaN
+ * (through the reduction of 0 and a final select); |x| >= 2^50 takes the
+ * Payne-Hanek reduction; the quadrant swaps and negates. */
 CM_FN void cm_sincos(double x, double *s, double *c) {
     const double ax = cm_fabs(x);
     const int bad = !(ax < CM_INF);
     const int huge = !bad && ax >= 1125899906842624.0; /* 2^50 */
     const double xr = (bad || huge) ? 0.0 : x;
     cm_dtab t = CM_TAB(cm_dtab, cm_trig_tab);
-    double kf = cm_rint_small(xr * t[16]);
-    double r = CM_FMA(-kf, t[17], xr);
-    r = CM_FMA(-kf, t[18], r);
-    r = CM_FMA(-kf, t[19], r);
-    double q4 = kf - 4.0 * cm_rint_small(kf * 0.25 - 0.375); /* kf mod 4, in 0..3 */
-    int q = (int)q4;
+    int q;
+    double r = cm_rem_pio2_cw(xr, &q, t);
+    if (huge) {
+        int qh;
+        const double rh = cm_rem_pio2_huge(ax, &qh, t);
+        r = x < 0.0 ? -rh : rh;
+        q = (x < 0.0 ? -qh : qh) & 3;
+    }
     double sr = cm_sin_kernel(r, t), cr = cm_cos_kernel(r, t);
     double so = (q & 1) ? cr : sr;
     double co = (q & 1) ? sr : cr;
     so = (q & 2) ? -so : so;
     co = ((q + 1) & 2) ? -co : co;
-    *s = bad ? CM_NAN : (huge ? 0.0 : so);
-    *c = bad ? CM_NAN : (huge ? 1.0 : co);
+    *s = bad ? CM_NAN : so;
+    *c = bad ? CM_NAN : co;
 }
 
 CM_FN double cm_sin(double x) { double s, c; cm_sincos(x, &s, &c); return s; }
@@ -344,6 +416,9 @@ CM_FN float cm_cos_kernelf(float r, cm_ftab t) {
     return w + (((1.0f - w) - hz) + z * (z * p));
 }
 
+/* fp32 sin and cos; arguments from 2^21 on are reduced in fp64 (exact
+ * widening, then the fp64 reduction) and the reduced argument rounded to
+ * fp32. */
 CM_FN void cm_sincosf(float x, float *s, float *c) {
     const float ax = cm_fabsf(x);
     const int bad = !(ax < CM_INFF);
@@ -356,13 +431,22 @@ CM_FN void cm_sincosf(float x, float *s, float *c) {
     r = CM_FMAF(-kf, t[13], r);
     float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
     int q = (int)q4;
+    if (huge) {
+        cm_dtab td = CM_TAB(cm_dtab, cm_trig_tab);
+        const double axd = (double)ax;
+        int qh;
+        const double rd = axd >= 1125899906842624.0 ? cm_rem_pio2_huge(axd, &qh, td)
+                                                    : cm_rem_pio2_cw(axd, &qh, td);
+        r = (float)(x < 0.0f ? -rd : rd);
+        q = (x < 0.0f ? -qh : qh) & 3;
+    }
     float sr = cm_sin_kernelf(r, t), cr = cm_cos_kernelf(r, t);
     float so = (q & 1) ? cr : sr;
     float co = (q & 1) ? sr : cr;
     so = (q & 2) ? -so : so;
     co = ((q + 1) & 2) ? -co : co;
-    *s = bad ? CM_NANF : (huge ? 0.0f : so);
-    *c = bad ? CM_NANF : (huge ? 1.0f : co);
+    *s = bad ? CM_NANF : so;
+    *c = bad ? CM_NANF : co;
 }
 
 CM_FN float cm_sinf(float x) { float s, c; cm_sincosf(x, &s, &c); return s; }

@@ -43,7 +43,7 @@
 #define CEXP_CAP64 485165195.4097903
 #define CEXP_CAP32 485165184.0f
 #define ORC_MAXK 64
-#define ORC_MAXS 256
+#define ORC_MAXD 256   /* variables per point */
 
 /* ------------------------------------------------------------------ decode */
 
@@ -301,14 +301,33 @@ typedef struct {
     const float *nv;
     const int32_t *ci;
     int n, K;
+    int general;   /* fitted by the device's general kernel (co_fast_path false) */
+    /* per-point scratch, n entries each (tree_init) */
+    double *st, *t1, *t2, *sa;
+    float *st32, *t132, *t232, *sa32;
+    int *lo, *hi;
 } Tree;
+
+static int tree_init(Tree *t, const int32_t *nt, const float *nv, const int32_t *ci, int n,
+                     int K, int general) {
+    t->nt = nt; t->nv = nv; t->ci = ci; t->n = n; t->K = K; t->general = general;
+    const size_t m = n > 0 ? (size_t)n : 1;
+    char *b = (char *)malloc(m * (4 * sizeof(double) + 4 * sizeof(float) + 2 * sizeof(int)));
+    if (!b) return CO_ERR_OOM;
+    t->st = (double *)b; t->t1 = t->st + m; t->t2 = t->t1 + m; t->sa = t->t2 + m;
+    t->st32 = (float *)(t->sa + m); t->t132 = t->st32 + m; t->t232 = t->t132 + m;
+    t->sa32 = t->t232 + m;
+    t->lo = (int *)(t->sa32 + m); t->hi = t->lo + m;
+    return CO_OK;
+}
+
+static void tree_free(Tree *t) { free(t->st); t->st = NULL; }
 
 /* Value and (optionally) gradient at one point, fp64.
  * jac: 0 none, 1 forward (range scaling), 2 reverse (tape + adjoint stack). */
 static double point64(const Tree *t, const double *x, const double *c, int jac, double *g) {
-    double st[ORC_MAXS];
-    int lo[ORC_MAXS], hi[ORC_MAXS];
-    double tape1[ORC_MAXS * 2], tape2[ORC_MAXS * 2];
+    double *st = t->st, *tape1 = t->t1, *tape2 = t->t2;
+    int *lo = t->lo, *hi = t->hi;
     int sp = 0;
     for (int i = t->n - 1; i >= 0; i--) {
         int ty = t->nt[i];
@@ -352,7 +371,7 @@ static double point64(const Tree *t, const double *x, const double *c, int jac, 
     }
     if (jac == 2) {
         /* backward sweep in prefix order, revad_interp.cuh:131-156 */
-        double sa[ORC_MAXS];
+        double *sa = t->sa;
         int asp = 0;
         for (int k = 0; k < t->K; k++) g[k] = 0.0;
         sa[asp++] = 1.0;
@@ -373,9 +392,8 @@ static double point64(const Tree *t, const double *x, const double *c, int jac, 
 }
 
 static float point32(const Tree *t, const double *x, const double *c, int jac, float *g) {
-    float st[ORC_MAXS];
-    int lo[ORC_MAXS], hi[ORC_MAXS];
-    float tape1[ORC_MAXS * 2], tape2[ORC_MAXS * 2];
+    float *st = t->st32, *tape1 = t->t132, *tape2 = t->t232;
+    int *lo = t->lo, *hi = t->hi;
     int sp = 0;
     for (int i = t->n - 1; i >= 0; i--) {
         int ty = t->nt[i];
@@ -417,7 +435,7 @@ static float point32(const Tree *t, const double *x, const double *c, int jac, f
         }
     }
     if (jac == 2) {
-        float sa[ORC_MAXS];
+        float *sa = t->sa32;
         int asp = 0;
         for (int k = 0; k < t->K; k++) g[k] = 0.0f;
         sa[asp++] = 1.0f;
@@ -445,30 +463,34 @@ typedef struct {
     double jtr[ORC_MAXK];
 } PassOut;
 
-/* Sums over points in the canonical lane order (see the file header). */
-/* One pass in the device's order (cusr_amd/csrc/lm_device.h data_pass):
- * 64-point granule g belongs to partition g mod G; the partitions' sums are
- * added in order 0, 1, ..., G-1 at the end. Within a partition:
- *   - otherwise (smaller K, reverse AD, value-only passes): point i goes to
- *     lane i mod 64, which sums its points in ascending order from 0.0 with
- *     fma; the lanes combine with strides 32..1;
- *   - forward AD with K >= CO_SUMS_MATRIX_MIN_K: every entry of [J | r]^T [J | r]
- *     is one fma chain over the partition's points in ascending order (the
- *     matrix instruction's order); for K = 16, r^2 and J^T r keep the lane
- *     order above. */
+/* One pass in the device's order (cusr_amd/csrc/lm_device.h data_pass and
+ * data_pass_gen): 64-point granule g belongs to partition g mod G; the
+ * partitions' sums are added in order 0, 1, ..., G-1 at the end. Within a
+ * partition:
+ *   - value-only passes, and Jacobian passes of the fast kernels with smaller
+ *     K or reverse AD: point i goes to lane i mod 64, which sums its points
+ *     in ascending order from 0.0 with fma; the lanes combine with strides
+ *     32..1;
+ *   - Jacobian passes of the fast kernels in forward AD with
+ *     K >= CO_SUMS_MATRIX_MIN_K: every entry of [J | r]^T [J | r] is one fma
+ *     chain over the partition's points in ascending order (the matrix
+ *     instruction's order); for K = 16, r^2 and J^T r keep the lane order;
+ *   - Jacobian passes of the general kernel (either AD mode, any K): every
+ *     entry of [J | r]^T [J | r], r^2 and J^T r included, is one such chain. */
 static void orc_pass(const Tree *t, int N, int D, const double *xs, const double *y,
                      const double *c, int prec, int jac, int G, PassOut *out) {
     int K = t->K;
     int nq = K * (K + 1) / 2;
     int width = 1 + K + nq;
-    const int mx = jac == 1 && K >= CO_SUMS_MATRIX_MIN_K;   /* forward AD only */
-    const int ncol = K < 16 ? K + 1 : 16;   /* columns of the matrix product */
-    const int lane_w = mx ? (K < 16 ? 0 : 1 + K) : width;
+    const int mx = jac != 0 && (t->general || (jac == 1 && K >= CO_SUMS_MATRIX_MIN_K));
+    const int full = t->general || K < 16;  /* r is a column of the product */
+    const int ncol = full ? K + 1 : 16;     /* columns of the matrix product */
+    const int lane_w = mx ? (full ? 0 : 1 + K) : width;
     double *acc = (double *)calloc((size_t)G * ORC_LANES * (lane_w ? lane_w : 1), sizeof(double));
-    double *gm = mx ? (double *)calloc((size_t)G * 256, sizeof(double)) : NULL;
+    double *gm = mx ? (double *)calloc((size_t)G * ncol * ncol, sizeof(double)) : NULL;
     double g64[ORC_MAXK];
     float g32[ORC_MAXK];
-    double x[64], aug[17];
+    double x[ORC_MAXD], aug[ORC_MAXK + 1];
     for (int i = 0; i < N; i++) {
         int part = (i / ORC_LANES) % G;
         double *a = acc + ((size_t)part * ORC_LANES + (size_t)(i % ORC_LANES)) * (lane_w ? lane_w : 1);
@@ -484,12 +506,12 @@ static void orc_pass(const Tree *t, int N, int D, const double *xs, const double
         double r = f - y[i];
         if (mx) {
             for (int k = 0; k < K; k++) aug[k] = g64[k];
-            if (K < 16) aug[K] = r;
-            double *gp = gm + (size_t)part * 256;
+            if (full) aug[K] = r;
+            double *gp = gm + (size_t)part * ncol * ncol;
             for (int i1 = 0; i1 < ncol; i1++)
                 for (int i2 = 0; i2 < ncol; i2++)
-                    gp[i1 * 16 + i2] = fma(aug[i1], aug[i2], gp[i1 * 16 + i2]);
-            if (K == 16) {
+                    gp[i1 * ncol + i2] = fma(aug[i1], aug[i2], gp[i1 * ncol + i2]);
+            if (!full) {
                 a[0] = fma(r, r, a[0]);
                 for (int j = 0; j < K; j++) a[1 + j] = fma(g64[j], r, a[1 + j]);
             }
@@ -520,14 +542,14 @@ static void orc_pass(const Tree *t, int N, int D, const double *xs, const double
             for (int w = 0; w < lane_w; w++) ps[w] = pacc[w];
         }
         if (mx) {
-            const double *gp = gm + (size_t)part * 256;
-            if (K < 16) {
-                ps[0] = gp[K * 16 + K];
-                for (int j = 0; j < K; j++) ps[1 + j] = gp[j * 16 + K];
+            const double *gp = gm + (size_t)part * ncol * ncol;
+            if (full) {
+                ps[0] = gp[K * ncol + K];
+                for (int j = 0; j < K; j++) ps[1 + j] = gp[j * ncol + K];
             }
             int q = 1 + K;
             for (int j1 = 0; j1 < K; j1++)
-                for (int j2 = j1; j2 < K; j2++, q++) ps[q] = gp[j1 * 16 + j2];
+                for (int j2 = j1; j2 < K; j2++, q++) ps[q] = gp[j1 * ncol + j2];
         }
     }
     /* partition sums added in partition order */
@@ -606,6 +628,12 @@ void orc_options_default(CoOptions *o) {
     o->fp64_guard = 1;
 }
 
+/* A loss the fit may go on from: finite, and with f32_range finite in fp32
+ * too (the reference accumulates it in fp32). */
+static int orc_finite(const CoOptions *o, double loss) {
+    return isfinite(loss) && (!o->f32_range || isfinite((float)loss));
+}
+
 /* One expression (batch_lm_ad.cu:295-495 restricted to tree m, with the
  * Jacobian evaluated at every accepted point and reused after a reject). */
 static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const double *xs,
@@ -628,7 +656,7 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
     orc_pass(t, N, D, xs, y, c, o->precision, K > 0 ? jac : 0, G, cur);
     double li = cur->loss;
     if (K == 0) st = 3;
-    else if (!isfinite(cur->loss)) st = 2;
+    else if (!orc_finite(o, cur->loss)) st = 2;
     double lambda = o->lambda0;
     while (st == 0 && it < o->max_iter) {
         it++;
@@ -639,8 +667,19 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
             continue;
         }
         for (int k = 0; k < K; k++) ct[k] = c[k] + delta[k];
+        if (o->f32_range) {
+            /* trial constants held in fp32 like the reference's; one the fp32
+             * fit cannot hold makes its trial loss non-finite there
+             * (batch_lm_ad.cu:437-443); no pass needed */
+            int over = 0;
+            for (int k = 0; k < K; k++) {
+                ct[k] = (double)(float)ct[k];
+                over |= !isfinite(ct[k]);
+            }
+            if (over) { st = 2; continue; }
+        }
         orc_pass(t, N, D, xs, y, ct, o->precision, jac, G, tri);
-        if (!isfinite(tri->loss)) { st = 2; continue; }
+        if (!orc_finite(o, tri->loss)) { st = 2; continue; }
         double dn2 = 0.0, cn2 = 0.0;
         for (int k = 0; k < K; k++) {
             dn2 = fma(delta[k], delta[k], dn2);
@@ -700,74 +739,104 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
     free(tri);
 }
 
+/* Checks a population and sets up expression m's tree and its kernel family
+ * (co_fast_path on K, stack depth, nodes and n_vars, as the device decode
+ * routes it). */
+static int *orc_depths(const PopHeader *h, const int32_t *nt, const float *nv,
+                       const int32_t *ci, const TreeMeta *metas, int *rc) {
+    int *depth = (int *)malloc(sizeof(int) * (h && h->M_prob > 0 ? (size_t)h->M_prob : 1));
+    if (!depth) { *rc = CO_ERR_OOM; return NULL; }
+    *rc = orc_check_pop(h, nt, nv, ci, metas, depth);
+    if (*rc == CO_OK && h->n_vars > ORC_MAXD) *rc = CO_ERR_BOUNDS;
+    for (int m = 0; *rc == CO_OK && m < h->M_prob; m++)
+        if (metas[m].K > CO_MAX_K || depth[m] > CO_MAX_STACK) *rc = CO_ERR_BOUNDS;
+    if (*rc != CO_OK) { free(depth); return NULL; }
+    return depth;
+}
+
+static int orc_tree(const PopHeader *h, const int32_t *nt, const float *nv, const int32_t *ci,
+                    const TreeMeta *metas, const int *depth, int m, Tree *t) {
+    const TreeMeta *mt = &metas[m];
+    const int general = !co_fast_path(mt->K, depth[m], mt->n_nodes, h->n_vars);
+    return tree_init(t, nt + mt->node_offset, nv + mt->node_offset, ci + mt->node_offset,
+                     mt->n_nodes, mt->K, general);
+}
+
 /* Whole-population fit; same arguments as co_optimize_ex minus the handle. */
 int orc_fit(const CoOptions *o, const PopHeader *h, const int32_t *nt, const float *nv,
             const int32_t *ci, const TreeMeta *metas, const double *c_init,
             const double *xs, const double *ym, double *c_final, int32_t *status,
             double *loss_init, double *loss_final, int32_t *iters) {
-    int rc = orc_check_pop(h, nt, nv, ci, metas, NULL);
-    if (rc) return rc;
-    if (h->n_vars > 64) return CO_ERR_BOUNDS;
+    int rc;
+    int *depth = orc_depths(h, nt, nv, ci, metas, &rc);
+    if (!depth) return rc;
     for (int m = 0; m < h->M_prob; m++) {
         const TreeMeta *mt = &metas[m];
-        if (mt->K > ORC_MAXK || mt->n_nodes > ORC_MAXS) return CO_ERR_BOUNDS;
-        Tree t = {nt + mt->node_offset, nv + mt->node_offset, ci + mt->node_offset,
-                  mt->n_nodes, mt->K};
+        Tree t;
+        if ((rc = orc_tree(h, nt, nv, ci, metas, depth, m, &t)) != CO_OK) break;
         double li, lf;
         int32_t st, itn;
         const double *yrow = (pop_flags(h) & POP_FLAG_SHARED_Y) ? ym : ym + (size_t)m * h->N;
         orc_fit_one(o, &t, h->N, h->n_vars, xs, yrow, c_init + mt->c_offset,
                     c_final + mt->c_offset, &st, &li, &lf, &itn);
+        tree_free(&t);
         status[m] = st;
         if (loss_init) loss_init[m] = li;
         if (loss_final) loss_final[m] = lf;
         if (iters) iters[m] = itn;
     }
-    return CO_OK;
+    free(depth);
+    return rc;
 }
 
 /* Values y[m*N+i] (prec CO_PREC_FP64 or CO_PREC_MIXED). */
 int orc_eval(const PopHeader *h, const int32_t *nt, const float *nv, const int32_t *ci,
              const TreeMeta *metas, const double *c, const double *xs, int prec,
              double *y) {
-    int rc = orc_check_pop(h, nt, nv, ci, metas, NULL);
-    if (rc) return rc;
-    double x[64];
+    int rc;
+    int *depth = orc_depths(h, nt, nv, ci, metas, &rc);
+    if (!depth) return rc;
+    double x[ORC_MAXD];
     for (int m = 0; m < h->M_prob; m++) {
         const TreeMeta *mt = &metas[m];
-        Tree t = {nt + mt->node_offset, nv + mt->node_offset, ci + mt->node_offset,
-                  mt->n_nodes, mt->K};
+        Tree t;
+        if ((rc = orc_tree(h, nt, nv, ci, metas, depth, m, &t)) != CO_OK) break;
         for (int i = 0; i < h->N; i++) {
             for (int k = 0; k < h->n_vars; k++) x[k] = xs[(size_t)i * h->n_vars + k];
             y[(size_t)m * h->N + i] = (prec == CO_PREC_FP64)
                 ? point64(&t, x, c + mt->c_offset, 0, NULL)
                 : (double)point32(&t, x, c + mt->c_offset, 0, NULL);
         }
+        tree_free(&t);
     }
-    return CO_OK;
+    free(depth);
+    return rc;
 }
 
 /* Jacobian rows J[(m*N + i)*K_max + j] (fp64), ad_mode 0 forward / 1 reverse. */
 int orc_jacobian(const PopHeader *h, const int32_t *nt, const float *nv, const int32_t *ci,
                  const TreeMeta *metas, const double *c, const double *xs, int ad_mode,
                  double *J) {
-    int rc = orc_check_pop(h, nt, nv, ci, metas, NULL);
-    if (rc) return rc;
-    double x[64], g[ORC_MAXK];
+    int rc;
+    int *depth = orc_depths(h, nt, nv, ci, metas, &rc);
+    if (!depth) return rc;
+    double x[ORC_MAXD], g[ORC_MAXK];
     int KM = h->K_max;
     for (int m = 0; m < h->M_prob; m++) {
         const TreeMeta *mt = &metas[m];
-        if (mt->K > ORC_MAXK || mt->K > KM) return CO_ERR_BOUNDS;
-        Tree t = {nt + mt->node_offset, nv + mt->node_offset, ci + mt->node_offset,
-                  mt->n_nodes, mt->K};
+        if (mt->K > KM) { rc = CO_ERR_BOUNDS; break; }
+        Tree t;
+        if ((rc = orc_tree(h, nt, nv, ci, metas, depth, m, &t)) != CO_OK) break;
         for (int i = 0; i < h->N; i++) {
             for (int k = 0; k < h->n_vars; k++) x[k] = xs[(size_t)i * h->n_vars + k];
             if (mt->K > 0) point64(&t, x, c + mt->c_offset, ad_mode == CO_AD_REVERSE ? 2 : 1, g);
             for (int j = 0; j < KM; j++)
                 J[((size_t)m * h->N + i) * KM + j] = (j < mt->K) ? g[j] : 0.0;
         }
+        tree_free(&t);
     }
-    return CO_OK;
+    free(depth);
+    return rc;
 }
 
 /* The damped solve alone, for tests against a textbook Cholesky. */
@@ -783,12 +852,15 @@ int orc_pass_api(const PopHeader *h, const int32_t *nt, const float *nv, const i
                  const TreeMeta *metas, int m, const double *c, const double *xs,
                  const double *y, int prec, int ad_mode, int partitions, double *loss,
                  double *jtj, double *jtr) {
-    int rc = orc_check_pop(h, nt, nv, ci, metas, NULL);
-    if (rc) return rc;
+    int rc;
+    int *depth = orc_depths(h, nt, nv, ci, metas, &rc);
+    if (!depth) return rc;
+    if (m < 0 || m >= h->M_prob) { free(depth); return CO_ERR_NULLARG; }
     const TreeMeta *mt = &metas[m];
-    if (mt->K > ORC_MAXK) return CO_ERR_BOUNDS;
-    Tree t = {nt + mt->node_offset, nv + mt->node_offset, ci + mt->node_offset,
-              mt->n_nodes, mt->K};
+    Tree t;
+    rc = orc_tree(h, nt, nv, ci, metas, depth, m, &t);
+    free(depth);
+    if (rc != CO_OK) return rc;
     PassOut *p = (PassOut *)malloc(sizeof(PassOut));
     const int G = partitions ? partitions : co_partitions_for_n(h->N);
     orc_pass(&t, h->N, h->n_vars, xs, y, c, prec, mt->K > 0 ? (ad_mode ? 2 : 1) : 0, G, p);
@@ -799,6 +871,7 @@ int orc_pass_api(const PopHeader *h, const int32_t *nt, const float *nv, const i
             jtj[j * mt->K + k] = (j <= k) ? p->jtj[j * mt->K + k] : p->jtj[k * mt->K + j];
     }
     free(p);
+    tree_free(&t);
     return CO_OK;
 }
 

@@ -31,7 +31,8 @@ class CoOptions(ctypes.Structure):
                 ("lambda0", ctypes.c_double), ("xtol", ctypes.c_double),
                 ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
                 ("lm_order", ctypes.c_int32), ("tail_iter", ctypes.c_int32),
-                ("tail_partitions", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3)]
+                ("tail_partitions", ctypes.c_int32), ("f32_range", ctypes.c_int32),
+                ("reserved", ctypes.c_int32 * 2)]
 
 
 def build() -> None:
@@ -74,7 +75,7 @@ def _prog(pop):
 
 def options(ad_mode=CO_AD_FORWARD, precision=CO_PREC_FP64, max_iter=50,
             lambda0=1e-3, xtol=1e-6, fp64_guard=1, partitions=0, lm_order=0,
-            tail_iter=0, tail_partitions=0) -> CoOptions:
+            tail_iter=0, tail_partitions=0, f32_range=0) -> CoOptions:
     o = CoOptions()
     o.struct_size = ctypes.sizeof(CoOptions)
     o.ad_mode, o.precision, o.max_iter = ad_mode, precision, max_iter
@@ -82,6 +83,7 @@ def options(ad_mode=CO_AD_FORWARD, precision=CO_PREC_FP64, max_iter=50,
     o.partitions = partitions
     o.lm_order = lm_order
     o.tail_iter, o.tail_partitions = tail_iter, tail_partitions
+    o.f32_range = f32_range
     return o
 
 

@@ -27,10 +27,10 @@ def _candidates(n, seed=3):
 
 def test_ineligible_without_fallback_raises():
     nat, inits = _candidates(3)
-    nt = np.asarray([3] * 17 + [1] * 18, np.int32)                  # 18 constants
-    nat.append((nt, np.asarray([1.0] * 17 + [0.0] * 18, np.float32),
-                np.asarray([-1] * 17 + list(range(18)), np.int32)))
-    inits.append(np.zeros(18))
+    nt = np.asarray([3] * 32 + [1] * 33, np.int32)                  # 33 constants > 32
+    nat.append((nt, np.asarray([1.0] * 32 + [0.0] * 33, np.float32),
+                np.asarray([-1] * 32 + list(range(33)), np.int32)))
+    inits.append(np.zeros(33))
     X = np.zeros((8, 2))
     with pytest.raises(ValueError):
         co_backend.fit_natives(None, inits, nat, X, np.zeros(8))
@@ -50,8 +50,11 @@ def test_kernel_pop_and_cli_pop():
     assert np.array_equal(a.c_final, o["c_final"])
     assert np.array_equal(a.n_iter, o["iters"])
     assert np.array_equal(a.status, backends._map_status(o["status"]))
-    assert np.array_equal(b.status, a.status)
-    assert np.array_equal(b.c_final, a.c_final.astype(np.float32).astype(np.float64))
+    # the CLI writes float32 blobs of a fit with constants held in fp32
+    from cusr_amd.kernel import co_inproc
+    n = co_inproc.narrow_fp32(pop, lm_oracle.fit(pop, max_iter=20, f32_range=1))
+    assert np.array_equal(b.status, backends._map_status(n["status"]))
+    assert np.array_equal(b.c_final, n["c_final"].astype(np.float64))
     assert np.isfinite(b.wall_core) and b.wall_core >= 0 and np.all(b.n_iter == -1)
 
 
@@ -61,10 +64,10 @@ def test_kernel_lm_fit_batch_aligned_with_fallback():
     rng = np.random.default_rng(9)
     X = rng.uniform(-2, 2, size=(300, 2))
     y = 1.5 * X[:, 0] - 0.25 + 0.01 * rng.normal(size=300)
-    big = np.asarray([3] * 17 + [1] * 18, np.int32)
-    nat.insert(5, (big, np.asarray([1.0] * 17 + [0.0] * 18, np.float32),
-                   np.asarray([-1] * 17 + list(range(18)), np.int32)))
-    inits.insert(5, np.zeros(18))
+    big = np.asarray([3] * 32 + [1] * 33, np.int32)                 # 33 constants > 32
+    nat.insert(5, (big, np.asarray([1.0] * 32 + [0.0] * 33, np.float32),
+                   np.asarray([-1] * 32 + list(range(33)), np.int32)))
+    inits.insert(5, np.zeros(33))
 
     class Stub:
         def fit_batch(self, skeletons, inits, X, y, *, max_iter=100, native=None):

@@ -26,8 +26,35 @@ def fields(w):
                 lo=(w >> 24) & 31, mid=(w >> 29) & 31, hi=(w >> 34) & 31, tape=(w >> 39) & 255)
 
 
+def wfields(a, b):
+    """Fields of a wide (general-kernel) instruction, words a and b."""
+    a, b = int(a), int(b)
+    return dict(fid=a & 63, bin=(a >> 6) & 1, ak=(a >> 7) & 3, ai=(a >> 9) & 255,
+                bk=(a >> 17) & 3, bi=(a >> 19) & 255, ts=(a >> 27) & 1, di=(a >> 28) & 255,
+                sel=(a >> 36) & 1, sa=(a >> 37) & 1, sb=(a >> 38) & 1, ta=(a >> 39) & 1,
+                tb=(a >> 40) & 1, lo=b & 255, mid=(b >> 8) & 255, hi=(b >> 16) & 255,
+                tape=(b >> 24) & 0xffffffff)
+
+
+def instructions(prog, off, n, wide):
+    """Field dicts of one expression's program (n words, or 2n for wide)."""
+    out = []
+    for i in range(n):
+        if wide:
+            a, b = prog[off + 2 * i], prog[off + 2 * i + 1]
+            if a == 0 and b == 0:
+                break
+            out.append(wfields(a, b))
+        else:
+            if prog[off + i] == 0:
+                break
+            out.append(fields(prog[off + i]))
+    return out
+
+
 def rebuild(prog):
-    """Prefix node list [(nt, nv, ci)] from a decoded program, checking ranges."""
+    """Prefix node list [(nt, nv, ci)] from a decoded program (field dicts
+    or fast-format words), checking ranges."""
     acc = None
     slots = {}
 
@@ -45,7 +72,7 @@ def rebuild(prog):
         return (min(r), max(r) + 1) if r else None
 
     for w in prog:
-        f = fields(w)
+        f = w if isinstance(w, dict) else fields(w)
         a = operand(f["ak"], f["ai"])
         if f["fid"] == OP_IDENT:
             sub = a
@@ -105,7 +132,7 @@ def test_stack_depth_and_k_bins(idx):
     assert rc == 0
     K = pop["metas"][:, 3]
     assert np.array_equal(order, np.argsort(K, kind="stable"))
-    assert np.array_equal(bins, np.concatenate([[0], np.cumsum(np.bincount(K, minlength=17))]))
+    assert np.array_equal(bins, np.concatenate([[0], np.cumsum(np.bincount(K, minlength=33))]))
     for m in range(pop["M"]):
         o, n, _, _ = (int(v) for v in pop["metas"][m])
         assert stack[m] == popio.stack_depth(pop["nt"][o:o + n])
@@ -194,19 +221,83 @@ def test_error_codes():
     assert _code(bad) == ci.CO_ERR_PROGRAM
     bad = dict(good); bad["nt"] = good["nt"].copy(); bad["nt"][1] = 2      # MUL as unary: stack
     assert _code(bad) == ci.CO_ERR_PROGRAM
-    bad = dict(good); bad["K_max"] = 17
-    assert _code(bad) == ci.CO_ERR_BOUNDS
-    bad = dict(good); bad["n_vars"] = 9
-    assert _code(bad) == ci.CO_ERR_BOUNDS
+    # header bounds, checked first like co_lib.cu:211-212: K_max 32 and
+    # max_stack 64 are the reference's; n_vars up to 255
+    for key, ok, beyond in (("K_max", 32, 33), ("max_stack", 64, 65), ("n_vars", 255, 256)):
+        bad = dict(good); bad[key] = beyond
+        assert _code(bad) == ci.CO_ERR_BOUNDS, key
+        fine = dict(good); fine[key] = ok
+        assert _code(fine) in (0, ci.CO_ERR_PROGRAM), key   # n_vars changes nothing valid
 
 
-def test_bounds_k17():
-    nt = [3] * 16 + [1] * 17
-    nv = [1.0] * 16 + [0.0] * 17
-    cis = [-1] * 16 + list(range(17))
-    pop = popio.build_pop([(nt, nv, cis, np.zeros(17))], np.zeros((4, 1)), np.zeros((1, 4)))
-    assert pop["K_max"] == 17
-    assert _code(pop) == ci.CO_ERR_BOUNDS
+def _sum_tree(K):
+    """c0 + c1 + ... + c_{K-1} + x0 as a left spine: stack 2, K constants."""
+    nt = [3] * K + [0] + [1] * K
+    nv = [1.0] * K + [0.0] * (K + 1)
+    cis = [-1] * (K + 1) + list(range(K))
+    return nt, nv, cis
+
+
+def test_bounds_per_expression():
+    """K 17..32 decodes (general kernel), K 33 is refused even when the header
+    understates it; a value stack of 64 decodes, 65 is refused."""
+    for K, want in ((17, 0), (28, 0), (32, 0), (33, ci.CO_ERR_BOUNDS)):
+        nt, nv, cis = _sum_tree(K)
+        pop = popio.build_pop([(nt, nv, cis, np.zeros(K))], np.zeros((4, 1)), np.zeros((1, 4)))
+        assert pop["K_max"] == K
+        assert _code(pop) == want, K
+        under = dict(pop); under["K_max"] = 8
+        assert _code(under) == want, K
+    from tests.general_pops import deep_tree
+    rng = np.random.default_rng(0)
+    for S, want in ((63, 0), (64, ci.CO_ERR_BOUNDS)):    # stack S + 1
+        nt, nv, cis, K = deep_tree(rng, S, 2, 8)
+        pop = popio.build_pop([(nt, nv, cis, np.zeros(K))], np.zeros((4, 2)), np.zeros((1, 4)))
+        assert pop["max_stack"] == S + 1
+        under = dict(pop); under["max_stack"] = 10
+        assert _code(under) == want, S
+
+
+@pytest.mark.parametrize("kind", ["highk", "deep", "long", "wide", "mixed"])
+def test_general_programs_round_trip_and_route(kind):
+    """Expressions outside co_fast_path get wide programs (two words per
+    instruction, laid out after the previous expression's words) that
+    rebuild to their nodes exactly; the route is co_fast_path's answer."""
+    from tests.general_pops import general_pop
+    pop, _ = general_pop(kind, 24, 64)
+    rc, prog, order, bins, stack, poff, route = ci.decode(pop, full=True)
+    assert rc == 0
+    D = pop["n_vars"]
+    off = 0
+    for m in range(pop["M"]):
+        o, n, _, K = (int(v) for v in pop["metas"][m])
+        fast = ci.co_fast_path(K, int(stack[m]), n, D)
+        assert route[m] == (0 if fast else 1)
+        assert poff[m] == off
+        ins = instructions(prog, off, n, not fast)
+        nodes = rebuild(ins)
+        assert [t for t, _, _ in nodes] == pop["nt"][o:o + n].tolist()
+        nv = pop["nv"][o:o + n].astype(float)
+        nv[pop["nt"][o:o + n] == 1] = 0.0
+        assert [v for _, v, _ in nodes] == nv.tolist()
+        assert [c for _, _, c in nodes] == pop["ci"][o:o + n].tolist()
+        if not fast:
+            # the wide fields: dense tape slots and the AD flags of the fast format
+            nxt = 0
+            for f in ins:
+                assert f["tape"] == nxt
+                nxt += f["ta"] + f["tb"]
+                unit = f["fid"] in (1, 2) or f["fid"] == OP_IDENT
+                assert f["ta"] == int(f["ak"] != 1 and not unit)
+                assert f["sel"] == int(f["fid"] in SELECT_OPS)
+                if f["bin"]:
+                    assert f["sa"] == int(f["mid"] > f["lo"] and f["fid"] not in (1, 2))
+                    assert f["sb"] == int(f["hi"] > f["mid"] and f["fid"] != 1)
+        off += n if fast else 2 * n
+    if kind != "mixed":
+        assert route.all()
+    else:
+        assert 0 < route.sum() < pop["M"]
 
 
 @pytest.mark.parametrize("variant,order", [("ad", 0), ("fd", 1)])

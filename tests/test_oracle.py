@@ -5,6 +5,7 @@ truth fixtures, and the reference's own interpreter where it builds.
 """
 import ctypes
 import json
+from fractions import Fraction
 import math
 from pathlib import Path
 
@@ -239,6 +240,102 @@ def test_pass_sums_match_textbook():
         assert np.allclose(jtj, J.T @ J, rtol=1e-10, atol=1e-10 * np.abs(J.T @ J).max())
 
 
+def _fma(a, b, c):
+    """fma(a, b, c) rounded once (exact rational product and sum, then the
+    correctly rounded double)."""
+    return float(Fraction(a) * Fraction(b) + Fraction(c))
+
+
+@pytest.mark.parametrize("kind,ad_mode,G", [("highk", 0, 1), ("highk", 1, 2), ("deep", 0, 2),
+                                            ("long", 1, 1), ("wide", 0, 1)])
+def test_general_sums_are_one_chain_per_entry(kind, ad_mode, G):
+    """Expressions of the general kernel: every sum of a Jacobian pass (r^2,
+    J^T r, J^T J) is one fused multiply-add chain over each partition's
+    points in ascending order, and the partition sums are added in order --
+    restated here with exact rational arithmetic, so a dropped term, a wrong
+    index or the lane order of the fast kernels fails it bit for bit."""
+    from tests.general_pops import general_pop
+    pop, _ = general_pop(kind, 6, 150)
+    x = pop["xs"].astype(np.float64)
+    checked = 0
+    for m in range(pop["M"]):
+        K = int(pop["metas"][m][3])
+        if K == 0:
+            continue
+        off = int(pop["metas"][m][2])
+        c = pop["c_init"][off:off + K].astype(np.float64)
+        y = pop["ym"][m].astype(np.float64)
+        sub = popio.select_pop(pop, [m])
+        J = lm_oracle.jacobian(sub, c=c, xs=x, ad_mode=ad_mode)[0]
+        r = lm_oracle.eval_pop(sub, c=c, xs=x)[0] - y
+        aug = np.concatenate([J, r[:, None]], axis=1)
+        want = np.zeros((K + 1, K + 1))
+        for g in range(G):
+            pts = [i for i in range(len(r)) if (i // 64) % G == g]
+            part = np.zeros((K + 1, K + 1))
+            for a_ in range(K + 1):
+                for b_ in range(a_, K + 1):
+                    acc = 0.0
+                    for i in pts:
+                        acc = _fma(aug[i, a_], aug[i, b_], acc)
+                    part[a_, b_] = acc
+            want = want + part if g else part
+        loss, jtj, jtr = lm_oracle.pass_sums(pop, m, c, xs=x, y=y, ad_mode=ad_mode,
+                                             partitions=G)
+        assert loss == 0.5 * want[K, K]
+        assert np.array_equal(jtr, want[:K, K])
+        assert np.array_equal(np.triu(jtj), np.triu(want[:K, :K]))
+        checked += 1
+    assert checked >= 4
+
+
+def test_general_sums_match_textbook():
+    """The same sums against numpy's J^T J and J^T r, K up to 32."""
+    from tests.general_pops import general_pop
+    pop, _ = general_pop("highk", 8, 300)
+    x = pop["xs"].astype(np.float64)
+    for m in range(pop["M"]):
+        K = int(pop["metas"][m][3])
+        off = int(pop["metas"][m][2])
+        c = pop["c_init"][off:off + K].astype(np.float64)
+        y = pop["ym"][m].astype(np.float64)
+        for ad_mode in (0, 1):
+            loss, jtj, jtr = lm_oracle.pass_sums(pop, m, c, xs=x, y=y, ad_mode=ad_mode)
+            sub = popio.select_pop(pop, [m])
+            J = lm_oracle.jacobian(sub, c=c, xs=x, ad_mode=ad_mode)[0]
+            r = lm_oracle.eval_pop(sub, c=c, xs=x)[0] - y
+            assert loss == pytest.approx(0.5 * np.sum(r * r), rel=1e-12)
+            assert np.allclose(jtr, J.T @ r, rtol=1e-10, atol=1e-10 * np.abs(J.T @ r).max())
+            assert np.allclose(jtj, J.T @ J, rtol=1e-10, atol=1e-10 * np.abs(J.T @ J).max())
+
+
+def test_general_jacobians_forward_equals_reverse():
+    """K up to 32 and stacks up to 64: forward- and reverse-mode Jacobians of
+    the oracle agree to rounding, and both agree with central differences."""
+    from tests.general_pops import general_pop
+    for kind in ("highk", "deep", "long"):
+        pop, _ = general_pop(kind, 6, 16)
+        x = pop["xs"].astype(np.float64)
+        c = pop["c_init"].astype(np.float64)
+        Jf = lm_oracle.jacobian(pop, c=c, xs=x, ad_mode=0)
+        Jr = lm_oracle.jacobian(pop, c=c, xs=x, ad_mode=1)
+        scale = np.maximum(np.abs(Jf).max(axis=2, keepdims=True), 1e-300)
+        assert np.max(np.abs(Jf - Jr) / scale) < 1e-12, kind
+        for m in range(pop["M"]):
+            off, K = int(pop["metas"][m][2]), int(pop["metas"][m][3])
+            for j in range(0, K, max(1, K // 4)):
+                h = 1e-6 * max(1.0, abs(c[off + j]))
+                cp, cm = c.copy(), c.copy()
+                cp[off + j] += h
+                cm[off + j] -= h
+                sub = popio.select_pop(pop, [m])
+                cs = lambda cc: cc[off:off + K]   # noqa: E731
+                d = (lm_oracle.eval_pop(sub, c=cs(cp), xs=x)[0]
+                     - lm_oracle.eval_pop(sub, c=cs(cm), xs=x)[0]) / (2 * h)
+                assert np.allclose(d, Jf[m, :, j], rtol=1e-5,
+                                   atol=1e-6 * max(1.0, np.abs(Jf[m]).max())), (kind, m, j)
+
+
 # -------------------------------------------- the LM loop on reference fixtures
 
 def test_truth_fixture_recovered():
@@ -384,49 +481,6 @@ def test_reference_loader_reads_what_popio_reads():
     assert np.array_equal(arr(pd.xs, ctypes.c_float, N * D), pop["xs"].ravel())
     assert np.array_equal(arr(pd.ym, ctypes.c_float, M * N), pop["ym"].ravel())
     lib.free_pop_data(ctypes.byref(pd))
-
-
-def test_reference_interpreters_agree_with_oracle():
-    """The reference's fp32 value / forward / reverse interpreters
-    (ad_interp.cuh, revad_interp.cuh) against the oracle's fp64 values and
-    Jacobians on the real population (reference operators only)."""
-    lib = _ref_lib("libref_ad.so")
-    pop = ref_pop("pop1000.bin")
-    f32p = ctypes.POINTER(ctypes.c_float)
-    i32p = ctypes.POINTER(ctypes.c_int32)
-    lib.ref_value.restype = ctypes.c_float
-    lib.ref_jvp.restype = ctypes.c_float
-    xs = pop["xs"][:16]
-    sub = popio.select_pop(pop, range(0, 1000, 20))
-    sub = dict(sub, xs=xs, N=16, ym=np.zeros((sub["M"], 16), np.float32))
-    c64 = sub["c_init"].astype(np.float64)
-    yo = lm_oracle.eval_pop(sub, c=c64, xs=xs.astype(np.float64))
-    Jo = lm_oracle.jacobian(sub, c=c64, xs=xs.astype(np.float64))
-    agree = total = 0
-    for m in range(sub["M"]):
-        off, n, c_off, K = (int(v) for v in sub["metas"][m])
-        nt = np.ascontiguousarray(sub["nt"][off:off + n], np.int32)
-        nv = np.ascontiguousarray(sub["nv"][off:off + n], np.float32)
-        ci_ = np.ascontiguousarray(sub["ci"][off:off + n], np.int32)
-        c = np.ascontiguousarray(sub["c_init"][c_off:c_off + K], np.float32)
-        for i in range(16):
-            x = np.ascontiguousarray(xs[i], np.float32)
-            g = np.zeros(max(K, 1), np.float32)
-            gr = np.zeros(max(K, 1), np.float32)
-            args = (nt.ctypes.data_as(i32p), nv.ctypes.data_as(f32p), n, ci_.ctypes.data_as(i32p),
-                    x.ctypes.data_as(f32p), c.ctypes.data_as(f32p))
-            v = lib.ref_jvp(*args, K, g.ctypes.data_as(f32p))
-            lib.ref_vjp(*args, K, gr.ctypes.data_as(f32p))
-            if not (np.isfinite(v) and np.isfinite(yo[m, i])):
-                continue
-            total += 1
-            ok = abs(v - yo[m, i]) <= 1e-4 * max(1.0, abs(yo[m, i]))
-            for gg in (g[:K], gr[:K]):
-                fin = np.isfinite(gg) & np.isfinite(Jo[m, i, :K])
-                ok &= bool(np.all(np.abs(gg[fin] - Jo[m, i, :K][fin])
-                                  <= 1e-3 * np.maximum(1.0, np.abs(Jo[m, i, :K][fin]))))
-            agree += ok
-    assert total > 500 and agree / total > 0.99
 
 
 def test_partitioned_sums_agree():
