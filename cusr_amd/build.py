@@ -39,8 +39,8 @@ DEVICE_FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-ffp-co
                 "-fno-fast-math", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                 f"-I{REPO / 'include'}", "-Wall", "-Wno-unused-function"]
 
-FIT_VARIANTS = [("double", 0, "launch_fit_f64_fwd"), ("double", 1, "launch_fit_f64_rev"),
-                ("float", 0, "launch_fit_f32_fwd"), ("float", 1, "launch_fit_f32_rev")]
+FIT_VARIANTS = [("double", 0, "f64_fwd"), ("double", 1, "f64_rev"),
+                ("float", 0, "f32_fwd"), ("float", 1, "f32_rev")]
 
 
 def _run(cmd):
@@ -68,9 +68,10 @@ def build(jobs: int | None = None, verbose: bool = False, defines=(), out: Path 
     jobs = jobs or min(8, os.cpu_count() or 4)
     compiles = []
     for rtype, ad, name in FIT_VARIANTS:
-        obj = bdir / f"fit_{name}.o"
+        obj = bdir / f"fit_launch_fit_{name}.o"
         compiles.append([HIPCC, *DEVICE_FLAGS, *extra, "-x", "hip", f"-DCUSR_FIT_R={rtype}",
-                         f"-DCUSR_FIT_AD={ad}", f"-DCUSR_FIT_LAUNCH={name}", "-c",
+                         f"-DCUSR_FIT_AD={ad}", f"-DCUSR_FIT_LAUNCH=launch_fit_{name}",
+                         f"-DCUSR_PASS_LAUNCH=launch_pass_{name}", "-c",
                          str(CSRC / "fit_kernels.hip"), "-o", str(obj)])
     compiles.append([HIPCC, *DEVICE_FLAGS, *extra, "-x", "hip", "-c", str(CSRC / "co_lib.hip"),
                      "-o", str(bdir / "co_lib.o")])

@@ -18,6 +18,8 @@
 #include <vector>
 
 #include "lm_device.h"
+#define CUSR_SPLIT_STEP_KERNELS
+#include "lm_split.h"
 #include "program.h"
 
 namespace cusr {
@@ -85,10 +87,18 @@ struct HostBuf {
 constexpr int kExtraStreams = 3;
 constexpr int kStreams = kExtraStreams + 1;
 
-// one launcher per (precision, AD mode), each built from fit_kernels.hip in
-// its own translation unit so the four variants compile in parallel
-typedef hipError_t (*FitLauncher)(int K, unsigned grid, size_t lds, hipStream_t s,
-                                  const FitArgs &fa);
+// launchers per (precision, AD mode) come from fit_kernels.hip, each variant
+// in its own translation unit so the four compile in parallel
+
+// Device memory of a fit beyond its inputs and outputs: the loop state of
+// paused (tail) or split fits, then the split path's partition sums. Either
+// the handle's buffer, grown as needed, or a fixed region that is never grown.
+struct Scratch {
+    void *p = nullptr;
+    size_t cap = 0;
+    bool fixed = false;
+};
+
 
 struct Ctx {
     int device = -1;
@@ -109,7 +119,7 @@ struct Ctx {
     size_t lds_per_block = 0;  // LDS one workgroup may use on this device
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
     DevBuf data_X, data_Y;   // co_data_upload: X [D][N] column-major, y [N]
-    DevBuf state;            // loop state of fits paused between segments
+    DevBuf state;            // scratch of tail and split fits (run_fit)
     HostBuf<uint64_t> h_prog;
     HostBuf<ExprDesc> h_desc;
     std::vector<double> h_c, h_li, h_lf, h_c0;   // co_optimize: fp64 results, c_init
@@ -312,9 +322,12 @@ struct LaunchPlan {
 
 // Fit the resident population; copy results to the host pointers that are
 // non-null (c_out and status_out too may be null: results then stay on the
-// device). Returns after the device work and copies are complete.
+// device). sc: where the fit's scratch goes (null: the handle's buffer, grown
+// as needed; a fixed region is never grown, and a fit that needs more is
+// refused with CO_ERR_BOUNDS before anything is launched). Returns after the
+// device work and copies are complete.
 int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, double *li_out,
-            double *lf_out, int32_t *iters_out) {
+            double *lf_out, int32_t *iters_out, const Scratch *sc = nullptr) {
     if (!ctx->resident) return CO_ERR_NULLARG;
     if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
     if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
@@ -332,7 +345,10 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         ctx->bin_launched[k] = false;
         ctx->last_bin_ms[k] = -1.0;
     }
+    const int parts = co_partitions_resolve(&opt, plan.N);
+    if (parts == 0) return CO_ERR_NULLARG;
     if (M == 0) return CO_OK;
+    const bool split = parts > CO_MAX_PARTITIONS;
     hipStream_t s = ctx->stream;
     FitArgs fa;
     fa.prog = ptr<uint64_t>(ctx->prog);
@@ -354,10 +370,10 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
     fa.lm_order = opt.lm_order;
     fa.lambda0 = opt.lambda0;
     fa.xtol = opt.xtol;
+    fa.psum = nullptr;
+    fa.psum_width = 0;
     const bool rev = opt.ad_mode == CO_AD_REVERSE;
     const bool mixed = opt.precision == CO_PREC_MIXED;
-    const int parts = opt.partitions ? opt.partitions : co_partitions_for_n(plan.N);
-    if (parts != 1 && parts != 2 && parts != 4) return CO_ERR_NULLARG;
     // segments of the iteration loop: all expressions up to tail_it, then the
     // ones still running with tail_parts partitions (one launch each per bin)
     int tail_parts = parts;
@@ -404,13 +420,15 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         load[li] += cost;
         b.stream = li;
         // per-wavefront areas, then the partition sums; fewer wavefronts per
-        // workgroup (each summing several partitions) when LDS is short
+        // workgroup (each summing several partitions) when LDS is short. The
+        // split path's pass workgroups are one wavefront with no partition
+        // sums in LDS.
         b.wave_bytes =
             (fit_lds_bytes(mixed, rev, bin, plan.N, plan.D, b.slots, b.tape) + 15) & ~(size_t)15;
         const size_t cap = max_dyn_lds(ctx, gen);
         const int ks = gen ? b.kmax : bin;
-        for (int g = 0; g < (b.kmax == 0 ? 1 : nseg); ++g) {
-            const int sp = seg[g].parts;
+        for (int g = 0; g < (b.kmax == 0 || split ? 1 : nseg); ++g) {
+            const int sp = split ? 1 : seg[g].parts;
             const size_t part_bytes = sp > 1 ? (size_t)sp * sums_width(ks) * 8 : 0;
             int pw = sp;
             while (pw > 1 && pw * b.wave_bytes + part_bytes > cap) pw /= 2;
@@ -420,12 +438,33 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         }
         lp[nl++] = b;
     }
-    const int stride = state_stride_for(kmax);
-    if (tail_it > 0) CO_GROW(ctx->state, sizeof(double) * stride * (size_t)M);
-    fa.state = tail_it > 0 ? ptr<double>(ctx->state) : nullptr;
+    // scratch: loop-state rows by expression, then the split path's partition
+    // sums by launch position
+    const int stride = split ? kSplitStride : state_stride_for(kmax);
+    const int pwidth = sums_width(kmax);
+    const size_t state_bytes =
+        (split || tail_it > 0) ? (((sizeof(double) * stride * (size_t)M) + 255) & ~(size_t)255) : 0;
+    const size_t psum_bytes = split ? sizeof(double) * (size_t)parts * pwidth * M : 0;
+    Scratch own;
+    if (!sc) {
+        if (state_bytes + psum_bytes) CO_GROW(ctx->state, state_bytes + psum_bytes);
+        own.p = ctx->state.p;
+        own.cap = ctx->state.cap;
+        sc = &own;
+    } else if (state_bytes + psum_bytes > sc->cap) {
+        return CO_ERR_BOUNDS;   // a fixed region is never grown
+    }
+    fa.state = state_bytes ? (double *)sc->p : nullptr;
     fa.state_stride = stride;
-    const FitLauncher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
-                                     : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
+    if (split) {
+        fa.psum = (double *)((char *)sc->p + state_bytes);
+        fa.psum_width = pwidth;
+    }
+    typedef hipError_t (*Launcher)(int, unsigned, size_t, hipStream_t, const FitArgs &);
+    const Launcher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
+                                  : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
+    const Launcher launch_pass = mixed ? (rev ? launch_pass_f32_rev : launch_pass_f32_fwd)
+                                       : (rev ? launch_pass_f64_rev : launch_pass_f64_fwd);
     bool lane_used[kExtraStreams] = {};
     // after the first launch an error must not return with work still running
     // on the lanes: they are joined first
@@ -443,7 +482,16 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
         if (e_ != hipSuccess) return fail(e_, __LINE__); \
     } while (0)
     CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t0, s));
+    if (split) {
+        // every expression starts with a pass at c_init pending
+        FitArgs fi = fa;
+        lm_split_init_kernel<<<M, kLanes, 0, s>>>(fi);
+        CO_LAUNCH_HIP(hipGetLastError());
+    }
     CO_LAUNCH_HIP(hipEventRecord(ctx->ev_start, s));
+    // the split path's (pass, step) rounds: the pass at c_init, one per
+    // iteration, two fp64 audit passes for mixed precision
+    const int rounds = 1 + opt.max_iter + (mixed ? 2 : 0);
     for (int i = 0; i < nl; ++i) {
         const LaunchPlan &b = lp[i];
         hipStream_t ks = b.stream < kExtraStreams ? ctx->lanes[b.stream] : s;
@@ -452,18 +500,36 @@ int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, 
             CO_LAUNCH_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
         }
         CO_LAUNCH_HIP(hipEventRecord(ctx->ev_b0[b.bin], ks));
-        // K = 0 expressions have no iterations, so no tail either
-        for (int g = 0; g < (b.kmax == 0 ? 1 : nseg); ++g) {
+        if (split) {
             FitArgs fk = fa;
             fk.desc = fa.desc + b.pos;
+            fk.psum = fa.psum + (size_t)b.pos * parts * pwidth;
             fk.slots = b.slots;
             fk.tape = b.tape;
-            fk.parts = seg[g].parts;
-            fk.pwaves = b.pwaves[g];
+            fk.parts = parts;
+            fk.pwaves = 1;
             fk.wave_bytes = (int)b.wave_bytes;
-            fk.it_end = seg[g].it_end;
-            fk.resume = seg[g].resume;
-            CO_LAUNCH_HIP(launch(b.bin, (unsigned)b.cnt, b.lds[g], ks, fk));
+            fk.it_end = opt.max_iter;
+            fk.resume = 0;
+            for (int r = 0; r < rounds; ++r) {
+                CO_LAUNCH_HIP(launch_pass(b.bin, (unsigned)b.cnt * parts, b.lds[0], ks, fk));
+                lm_step_kernel<<<b.cnt, kLanes, 0, ks>>>(fk, mixed ? 1 : 0);
+                CO_LAUNCH_HIP(hipGetLastError());
+            }
+        } else {
+            // K = 0 expressions have no iterations, so no tail either
+            for (int g = 0; g < (b.kmax == 0 ? 1 : nseg); ++g) {
+                FitArgs fk = fa;
+                fk.desc = fa.desc + b.pos;
+                fk.slots = b.slots;
+                fk.tape = b.tape;
+                fk.parts = seg[g].parts;
+                fk.pwaves = b.pwaves[g];
+                fk.wave_bytes = (int)b.wave_bytes;
+                fk.it_end = seg[g].it_end;
+                fk.resume = seg[g].resume;
+                CO_LAUNCH_HIP(launch(b.bin, (unsigned)b.cnt, b.lds[g], ks, fk));
+            }
         }
         CO_LAUNCH_HIP(hipEventRecord(ctx->ev_b1[b.bin], ks));
         ctx->bin_launched[b.bin] = true;

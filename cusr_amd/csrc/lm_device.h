@@ -608,8 +608,13 @@ struct PassArgs {
     int parts;          // point partitions G (64-point granule g -> partition g mod G)
     int pwaves;         // wavefronts of the workgroup; wave w sums partitions w, w+pwaves, ...
     int wave;           // this wavefront
-    double *part;       // LDS [parts][sums_width(K)] partition sums (parts > 1)
+    double *part;       // [parts][sums_width(K)] partition sums (parts > 1): LDS, or
+                        // HBM on the split path
     double *jt;         // LDS [64][17] augmented Jacobian rows of one slice (matrix sums)
+    int split;          // 1: this workgroup sums one partition into part (HBM) and the
+                        // step kernel adds the partitions; no combine here
+    int part_stride;    // split: doubles between partitions in part (the launch's
+                        // widest sums row, which the step kernel reads by)
 };
 
 // Matrix sums (forward AD, K >= CO_SUMS_MATRIX_MIN_K): v_mfma_f64_16x16x4 takes A[i][k]
@@ -736,7 +741,7 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
             }
         }
     }
-    double *dst = (a.parts == 1) ? out : a.part + part * W;
+    double *dst = (a.parts == 1) ? out : a.part + part * (a.split ? a.part_stride : W);
     if constexpr (MX) {
         // the accumulator to LDS as G[16][16], then the sums vector by lane 0
         double *gt = a.jt;
@@ -768,7 +773,7 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
         }
     }
     }
-    if (a.parts == 1) {
+    if (a.parts == 1 || a.split) {
         wave_sync_lds();
         return;
     }
@@ -869,7 +874,7 @@ __device__ __forceinline__ void data_pass_gen(const PassArgs &a, const WaveLds<R
             }
             wave_sync_lds();
         }
-        double *dst = (a.parts == 1) ? out : a.part + part * W;
+        double *dst = (a.parts == 1) ? out : a.part + part * (a.split ? a.part_stride : W);
         put_block(dst, g0, 0, 0, Kr, lane);
         if (nb > 1) {
             put_block(dst, g1, 0, 1, Kr, lane);
@@ -881,7 +886,7 @@ __device__ __forceinline__ void data_pass_gen(const PassArgs &a, const WaveLds<R
             put_block(dst, g5, 2, 2, Kr, lane);
         }
     }
-    if (a.parts == 1) {
+    if (a.parts == 1 || a.split) {
         wave_sync_lds();
         return;
     }
@@ -1049,6 +1054,10 @@ struct FitArgs {
     int it_end, resume;
     int state_stride;       // doubles per state row, >= kStateSums + sums_width(K)
     double *state;          // [M][state_stride], null for single-launch fits
+    // the split path: partition sums of the launch's expressions in HBM,
+    // [launch position][parts][psum_width]
+    double *psum;
+    int psum_width;
 };
 
 // loop state of a paused fit, per expression: loss, loss_init, lambda,
@@ -1126,6 +1135,8 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     pa.wave = wave;
     pa.part = (double *)(lds_dyn + (size_t)fa.pwaves * fa.wave_bytes);
     pa.jt = jt;
+    pa.split = 0;
+    pa.part_stride = 0;
 
     double *c_cur = lds_c, *c_try = lds_c + KC;
     double *s_cur = lds_s, *s_try = lds_s + FitStatic<GEN>::SW;

@@ -45,6 +45,19 @@ CO_MAX_VARS = 255
 CO_FAST_MAX_K, CO_FAST_MAX_STACK, CO_FAST_MAX_VARS, CO_FAST_MAX_NODES = 16, 16, 8, 255
 CO_GENERAL_BIN = CO_FAST_MAX_K + 1
 CO_BINS = CO_FAST_MAX_K + 2
+# point partitions (include/cusr_co.h co_partitions_for_n): beyond
+# CO_MAX_PARTITIONS each partition is a workgroup (the split path)
+CO_MAX_PARTITIONS, CO_MAX_SPLIT, CO_SPLIT_MIN_N = 4, 256, 262144
+
+
+def co_partitions_for_n(N: int) -> int:
+    """include/cusr_co.h co_partitions_for_n."""
+    if N >= CO_SPLIT_MIN_N:
+        g = 8
+        while g < CO_MAX_SPLIT and g * 2 * 4096 <= N:
+            g *= 2
+        return g
+    return 4 if N >= 16384 else (2 if N >= 1024 else 1)
 
 CO_AD_FORWARD, CO_AD_REVERSE = 0, 1
 CO_PREC_FP64, CO_PREC_MIXED = 0, 1
@@ -528,6 +541,7 @@ class InProcessCO:
         """Fit the uploaded population again; outputs=False leaves results on the device."""
         self._check()
         M, C = self._resident
+        fn, name = self._lib.co_fit_resident, "co_fit_resident"
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
                             fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
@@ -535,19 +549,18 @@ class InProcessCO:
                             f32_range=1 if f32_range else 0)
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
         if not outputs:
-            rc = self._lib.co_fit_resident(self._handle, ctypes.byref(o), None, None, None, None, None)
+            rc = fn(self._handle, ctypes.byref(o), None, None, None, None, None)
             if rc != CO_OK:
-                raise COError(rc, "co_fit_resident")
+                raise COError(rc, name)
             return None
         out = {"c_final": np.zeros(max(C, 1)), "status": np.zeros(max(M, 1), np.int32),
                "loss_init": np.zeros(max(M, 1)), "loss_final": np.zeros(max(M, 1)),
                "iters": np.zeros(max(M, 1), np.int32)}
-        rc = self._lib.co_fit_resident(
-            self._handle, ctypes.byref(o),
-            *(out[k].ctypes.data_as(_VP) for k in
-              ("c_final", "status", "loss_init", "loss_final", "iters")))
+        rc = fn(self._handle, ctypes.byref(o),
+                *(out[k].ctypes.data_as(_VP) for k in
+                  ("c_final", "status", "loss_init", "loss_final", "iters")))
         if rc != CO_OK:
-            raise COError(rc, "co_fit_resident")
+            raise COError(rc, name)
         out["c_final"] = out["c_final"][:C]
         for k in ("status", "loss_init", "loss_final", "iters"):
             out[k] = out[k][:M]

@@ -95,10 +95,13 @@ typedef struct CoOptions {
     double xtol;
     int32_t fp64_guard; /* 1: deliver c_init where the fp64 loss at c_final is
                            non-finite or worse (cusr/kernel/lm_core.cuh:299-351) */
-    int32_t partitions; /* point partitions per expression (1, 2 or 4; 0: by N,
-                           co_partitions_for_n). Part of the arithmetic order:
-                           the sums of each partition are formed separately and
-                           added in partition order. */
+    int32_t partitions; /* point partitions per expression (a power of two up to
+                           CO_MAX_SPLIT; 0: by N, co_partitions_for_n). Part of
+                           the arithmetic order: the sums of each partition are
+                           formed separately and added in partition order. Up
+                           to CO_MAX_PARTITIONS the wavefronts of one
+                           workgroup sum them; beyond, each partition is a
+                           workgroup of its own (the split path) */
     int32_t lm_order;   /* CO_ORDER_IMPROVE_FIRST (the AD variant,
                            cusr/kernel/batch_lm_ad.cu:456-473) or
                            CO_ORDER_CONVERGE_FIRST (the FD variant: a small step
@@ -133,11 +136,30 @@ typedef struct CoOptions {
  * A function of N only, so an expression fits the same alone or in any
  * population. Measured on MI355X: two partitions from N = 1,024 shorten the
  * slowest expressions of a K bin, which set its duration (C2 -11 %, C3
- * -20 %, C5 even); four pay off only for long expressions. */
+ * -20 %, C5 even); four pay off only for long expressions. From
+ * CO_SPLIT_MIN_N points an expression's passes spread over G = N / 4,096
+ * (a power of two, at most CO_MAX_SPLIT) workgroups, whose partition sums
+ * meet in HBM and are added in partition order by a step kernel that runs
+ * the LM update (the split path): a population of a few long expressions
+ * then still fills the GPU. */
+#define CO_MAX_PARTITIONS 4
+#define CO_MAX_SPLIT 256
+#define CO_SPLIT_MIN_N 262144
 static inline int co_partitions_for_n(int N) {
+    if (N >= CO_SPLIT_MIN_N) {
+        int g = 8;
+        while (g < CO_MAX_SPLIT && (long)g * 2 * 4096 <= (long)N) g *= 2;
+        return g;
+    }
     return N >= 16384 ? 4 : (N >= 1024 ? 2 : 1);
 }
-#define CO_MAX_PARTITIONS 4
+
+/* The partitions options o give for N points (0 if o->partitions is not a
+ * power of two up to CO_MAX_SPLIT). */
+static inline int co_partitions_resolve(const CoOptions *o, int N) {
+    const int g = o->partitions ? o->partitions : co_partitions_for_n(N);
+    return (g >= 1 && g <= CO_MAX_SPLIT && (g & (g - 1)) == 0) ? g : 0;
+}
 
 /* Iterations before the tail when CoOptions.tail_iter is 0, CO_TAIL_ITER_DEFAULT
  * (0: no tail). The tail targets the spread of iteration counts (a few
@@ -159,9 +181,12 @@ static inline int co_tail_iter_for(int N, int max_iter) {
 }
 
 /* The tail options o give for N points: returns the iterations before the
- * tail (0: no tail) and sets *tail_parts to its partitions. */
+ * tail (0: no tail) and sets *tail_parts to its partitions. The split path
+ * (more than CO_MAX_PARTITIONS partitions) has no tail: its step kernel
+ * already runs iteration by iteration. */
 static inline int co_tail_resolve(const CoOptions *o, int N, int *tail_parts) {
     *tail_parts = o->tail_partitions ? o->tail_partitions : CO_MAX_PARTITIONS;
+    if (co_partitions_resolve(o, N) > CO_MAX_PARTITIONS) return 0;
     const int t = o->tail_iter < 0 ? 0
                   : (o->tail_iter > 0 ? o->tail_iter : co_tail_iter_for(N, o->max_iter));
     return (t > 0 && t < o->max_iter) ? t : 0;

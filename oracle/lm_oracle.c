@@ -571,8 +571,7 @@ static void orc_pass(const Tree *t, int N, int D, const double *xs, const double
 
 /* Partitions of an N-point expression under options o. */
 static int orc_partitions(const CoOptions *o, int N) {
-    int G = o->partitions ? o->partitions : co_partitions_for_n(N);
-    return G;
+    return co_partitions_resolve(o, N);
 }
 
 /* ------------------------------------------------------------- the solve */
@@ -768,6 +767,7 @@ int orc_fit(const CoOptions *o, const PopHeader *h, const int32_t *nt, const flo
             const double *xs, const double *ym, double *c_final, int32_t *status,
             double *loss_init, double *loss_final, int32_t *iters) {
     int rc;
+    if (co_partitions_resolve(o, h->N) == 0) return CO_ERR_NULLARG;
     int *depth = orc_depths(h, nt, nv, ci, metas, &rc);
     if (!depth) return rc;
     for (int m = 0; m < h->M_prob; m++) {
