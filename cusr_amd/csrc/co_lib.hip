@@ -14,6 +14,7 @@
 #include <time.h>
 
 #include <cmath>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -39,6 +40,12 @@ __global__ void widen_kernel(const float *src, double *dst, size_t n) {
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t < n) dst[t] = (double)src[t];
 }
+
+// The scratch of co_fit_resident_static: a fixed array in device memory, one
+// copy per GPU the library runs on, held until the process ends. In host code
+// the name is a stand-in, not a device address: every use goes through the
+// per-device address hipGetSymbolAddress gives at co_init.
+static __device__ __align__(256) unsigned char scratch[CO_STATIC_SCRATCH_BYTES];
 
 }  // namespace cusr
 
@@ -92,13 +99,19 @@ constexpr int kStreams = kExtraStreams + 1;
 
 // Device memory of a fit beyond its inputs and outputs: the loop state of
 // paused (tail) or split fits, then the split path's partition sums. Either
-// the handle's buffer, grown as needed, or a fixed region that is never grown.
+// the handle's buffer, grown as needed, or a fixed region that is never grown
+// (the static array of co_fit_resident_static).
 struct Scratch {
     void *p = nullptr;
     size_t cap = 0;
     bool fixed = false;
 };
 
+// Per-device address of the static scratch array (hipGetSymbolAddress with
+// the device current), resolved once per device at co_init.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
 
 struct Ctx {
     int device = -1;
@@ -120,6 +133,7 @@ struct Ctx {
     DevBuf prog, desc, X, Y, C0, C, status, li, lf, iters, stage;
     DevBuf data_X, data_Y;   // co_data_upload: X [D][N] column-major, y [N]
     DevBuf state;            // scratch of tail and split fits (run_fit)
+    void *static_scratch = nullptr;   // this device's address of `scratch`
     HostBuf<uint64_t> h_prog;
     HostBuf<ExprDesc> h_desc;
     std::vector<double> h_c, h_li, h_lf, h_c0;   // co_optimize: fp64 results, c_init
@@ -605,6 +619,24 @@ extern "C" int co_init(int device_id, void **handle_out) {
     Ctx *ctx = new (std::nothrow) Ctx();
     if (!ctx) return CO_ERR_OOM;
     ctx->device = device_id;
+    {
+        // this device's address of the static scratch array, once per device
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (device_id >= 0 && device_id < kMaxDevices) {
+            if (!g_scratch_ptr[device_id]) {
+                void *p = nullptr;
+                const hipError_t es = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+                if (es != hipSuccess) {
+                    fprintf(stderr, "[cusr_co] hipGetSymbolAddress(scratch): %s\n",
+                            hipGetErrorString(es));
+                    delete ctx;
+                    return CO_ERR_CUDA;
+                }
+                g_scratch_ptr[device_id] = p;
+            }
+            ctx->static_scratch = g_scratch_ptr[device_id];
+        }
+    }
     int lds_per_block = 0;
     hipError_t e = hipDeviceGetAttribute(&lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock,
                                          device_id);
@@ -906,6 +938,24 @@ extern "C" int co_fit_resident(void *handle, const CoOptions *opt, double *c_fin
     const double t0 = now_ms();
     int rc = run_fit((Ctx *)handle, *opt, c_final_out, status_out, loss_init_out, loss_final_out,
                      iters_out);
+    g_setup_ms = 0.0;
+    g_loop_ms = now_ms() - t0;
+    return rc;
+}
+
+extern "C" int co_fit_resident_static(void *handle, const CoOptions *opt, double *c_final_out,
+                                      int32_t *status_out, double *loss_init_out,
+                                      double *loss_final_out, int32_t *iters_out) {
+    if (!handle || !opt || opt->struct_size != (int32_t)sizeof(CoOptions)) return CO_ERR_NULLARG;
+    Ctx *ctx = (Ctx *)handle;
+    if (!ctx->static_scratch) return CO_ERR_CUDA;   // device id beyond kMaxDevices
+    Scratch sc;
+    sc.p = ctx->static_scratch;
+    sc.cap = CO_STATIC_SCRATCH_BYTES;
+    sc.fixed = true;
+    const double t0 = now_ms();
+    int rc = run_fit(ctx, *opt, c_final_out, status_out, loss_init_out, loss_final_out,
+                     iters_out, &sc);
     g_setup_ms = 0.0;
     g_loop_ms = now_ms() - t0;
     return rc;

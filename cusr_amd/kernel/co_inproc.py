@@ -48,6 +48,7 @@ CO_BINS = CO_FAST_MAX_K + 2
 # point partitions (include/cusr_co.h co_partitions_for_n): beyond
 # CO_MAX_PARTITIONS each partition is a workgroup (the split path)
 CO_MAX_PARTITIONS, CO_MAX_SPLIT, CO_SPLIT_MIN_N = 4, 256, 262144
+CO_STATIC_SCRATCH_BYTES = 64 << 20
 
 
 def co_partitions_for_n(N: int) -> int:
@@ -124,7 +125,8 @@ _HERE = Path(__file__).resolve().parent
 EXPORTED = ("co_init", "co_optimize", "co_last_split", "co_teardown", "co_options_default",
             "co_optimize_ex", "co_eval_ex", "co_upload_ex", "co_fit_resident",
             "co_last_kernel_ms", "co_last_bin_ms", "co_decode", "co_data_upload",
-            "co_optimize_data", "co_data_upload_device", "co_narrow_fp32")
+            "co_optimize_data", "co_data_upload_device", "co_narrow_fp32",
+            "co_fit_resident_static")
 
 
 def lib_path(variant: str = "ad") -> Path:
@@ -192,6 +194,8 @@ def _bind(lib) -> None:
     lib.co_upload_ex.restype = ctypes.c_int
     lib.co_fit_resident.argtypes = [_VP, ctypes.POINTER(CoOptions)] + [_VP] * 5
     lib.co_fit_resident.restype = ctypes.c_int
+    lib.co_fit_resident_static.argtypes = [_VP, ctypes.POINTER(CoOptions)] + [_VP] * 5
+    lib.co_fit_resident_static.restype = ctypes.c_int
     lib.co_data_upload.argtypes = [_VP, ctypes.c_int, ctypes.c_int, _VP, _VP]
     lib.co_data_upload.restype = ctypes.c_int
     lib.co_data_upload_device.argtypes = [_VP, ctypes.c_int, ctypes.c_int, _VP, _VP]
@@ -537,11 +541,14 @@ class InProcessCO:
                      precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                      fp64_guard: bool = True, outputs: bool = True, partitions: int = 0,
                      tail_iter: int = 0, tail_partitions: int = 0, f32_range: bool = False,
-                     lm_order: int | None = None):
-        """Fit the uploaded population again; outputs=False leaves results on the device."""
+                     lm_order: int | None = None, static_scratch: bool = False):
+        """Fit the uploaded population again; outputs=False leaves results on the
+        device. static_scratch: co_fit_resident_static, the same fit with its
+        scratch in the library's fixed device array (no device allocation)."""
         self._check()
         M, C = self._resident
-        fn, name = self._lib.co_fit_resident, "co_fit_resident"
+        fn = self._lib.co_fit_resident_static if static_scratch else self._lib.co_fit_resident
+        name = "co_fit_resident_static" if static_scratch else "co_fit_resident"
         o = default_options(ad_mode=int(ad_mode), precision=int(precision),
                             max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
                             fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),

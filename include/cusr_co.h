@@ -277,6 +277,23 @@ int co_fit_resident(void *handle, const CoOptions *opt,
                     double *loss_init_out, double *loss_final_out,
                     int32_t *iters_out);
 
+/* co_fit_resident without device allocation. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under graph
+ * capture, tight serving loops, harnesses that forbid it). Fits the resident
+ * population exactly as co_fit_resident does (same kernels, same results),
+ * with the fit's scratch -- the loop state of tail segments and of the split
+ * path, and the split path's partition sums -- in a fixed device array of
+ * CO_STATIC_SCRATCH_BYTES that each GPU holds from co_init until the process
+ * ends, instead of handle buffers. A fit needing more gets CO_ERR_BOUNDS
+ * before anything is launched. Every call on one GPU shares that GPU's array,
+ * which keeps the last call's contents (each value a fit reads there it has
+ * written first): calls that overlap on one GPU race. */
+#define CO_STATIC_SCRATCH_BYTES (64u << 20)
+int co_fit_resident_static(void *handle, const CoOptions *opt,
+                           double *c_final_out, int32_t *status_out,
+                           double *loss_init_out, double *loss_final_out,
+                           int32_t *iters_out);
+
 /* Upload one data set, xs [N][n_vars] row-major and one target y [N], into
  * buffers of the handle reserved for it. It stays on the device across calls
  * until the next co_data_upload or co_teardown; the other entry points do not
