@@ -631,12 +631,101 @@ constexpr bool matrix_sums() { return AD == CO_AD_FORWARD && K >= CO_SUMS_MATRIX
 
 constexpr int sums_width(int K) { return 1 + K + K * (K + 1) / 2; }
 
+// Cross-lane exchange of a double with lane ^ S (S = 32, 16, 8, 4, 2, 1):
+// ds_bpermute for 32, ds_swizzle (xor mask) for 16, DPP moves below: row_ror:8
+// is the xor-8 partner within a row of 16, row_half_mirror then the reversed
+// quad permutation is xor 4, quad_perm [2,3,0,1] / [1,0,3,2] are xor 2 / 1.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int S>
+__device__ __forceinline__ int xchg_i32(int v, int lane) {
+    if constexpr (S == 32) return __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, v);
+    else if constexpr (S == 16) return __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1F);
+    else if constexpr (S == 8) return dpp_i32<0x128>(v);
+    else if constexpr (S == 4) return dpp_i32<0x1B>(dpp_i32<0x141>(v));
+    else if constexpr (S == 2) return dpp_i32<0x4E>(v);
+    else return dpp_i32<0xB1>(v);
+}
+template <int S>
+__device__ __forceinline__ double xchg(double v, int lane) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)xchg_i32<S>((int)(uint32_t)u, lane);
+    const uint32_t hi = (uint32_t)xchg_i32<S>((int)(uint32_t)(u >> 32), lane);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// The butterfly of the sums over the 64 lanes: at strides 32, 16, ..., 1 lane
+// l adds lane l ^ s, so every lane ends with the same sums, the ones the CPU
+// oracle forms (p[l] + p[l ^ s]).
 template <int W>
-__device__ __forceinline__ void wave_allreduce(double (&a)[W]) {
+__device__ __forceinline__ void wave_allreduce(double (&a)[W], int lane) {
 #pragma unroll
-    for (int s = kLanes / 2; s >= 1; s >>= 1) {
+    for (int w = 0; w < W; ++w) a[w] = a[w] + xchg<32>(a[w], lane);
 #pragma unroll
-        for (int w = 0; w < W; ++w) a[w] = a[w] + __shfl_xor(a[w], s, kLanes);
+    for (int w = 0; w < W; ++w) a[w] = a[w] + xchg<16>(a[w], lane);
+#pragma unroll
+    for (int w = 0; w < W; ++w) a[w] = a[w] + xchg<8>(a[w], lane);
+#pragma unroll
+    for (int w = 0; w < W; ++w) a[w] = a[w] + xchg<4>(a[w], lane);
+#pragma unroll
+    for (int w = 0; w < W; ++w) a[w] = a[w] + xchg<2>(a[w], lane);
+#pragma unroll
+    for (int w = 0; w < W; ++w) a[w] = a[w] + xchg<1>(a[w], lane);
+}
+
+// One reduce-scatter step of the butterfly at stride S: a lane keeps the lower
+// half of its entries when bit S of its index is clear, the upper half when
+// set, and adds the partner's copy of the half it keeps -- the value the
+// butterfly has in that lane for those entries.
+template <int S, int H>
+__device__ __forceinline__ void scatter_step(const double (&a)[2 * H], double (&b)[H], int lane) {
+    const bool up = (lane & S) != 0;
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+        const double keep = up ? a[H + j] : a[j];
+        const double send = up ? a[j] : a[H + j];
+        b[j] = keep + xchg<S>(send, lane);
+    }
+}
+
+// The same sums written to dst[0..W): strides 32, 16 and 8 reduce-scatter
+// (W padded to a multiple of 8; each lane ends with an eighth of the entries),
+// strides 4, 2 and 1 finish the butterfly on those; lanes 0, 8, ..., 56 store.
+// Every stored value is the butterfly's, bit for bit.
+template <int W>
+__device__ __forceinline__ void wave_reduce_store(const double (&acc)[W], double *dst, int lane) {
+    if constexpr (W < 8) {
+        double a[W];
+#pragma unroll
+        for (int q = 0; q < W; ++q) a[q] = acc[q];
+        wave_allreduce<W>(a, lane);
+        if (lane == 0) {
+#pragma unroll
+            for (int q = 0; q < W; ++q) dst[q] = a[q];
+        }
+    } else {
+        constexpr int W8 = (W + 7) / 8 * 8;
+        constexpr int H1 = W8 / 2, H2 = W8 / 4, H3 = W8 / 8;
+        double a0[W8], a1[H1], a2[H2], a3[H3];
+#pragma unroll
+        for (int q = 0; q < W8; ++q) a0[q] = q < W ? acc[q] : 0.0;
+        scatter_step<32, H1>(a0, a1, lane);
+        scatter_step<16, H2>(a1, a2, lane);
+        scatter_step<8, H3>(a2, a3, lane);
+#pragma unroll
+        for (int j = 0; j < H3; ++j) a3[j] = a3[j] + xchg<4>(a3[j], lane);
+#pragma unroll
+        for (int j = 0; j < H3; ++j) a3[j] = a3[j] + xchg<2>(a3[j], lane);
+#pragma unroll
+        for (int j = 0; j < H3; ++j) a3[j] = a3[j] + xchg<1>(a3[j], lane);
+        if ((lane & 7) == 0) {
+            const int start = ((lane & 32) ? H1 : 0) + ((lane & 16) ? H2 : 0) + ((lane & 8) ? H3 : 0);
+#pragma unroll
+            for (int j = 0; j < H3; ++j)
+                if (start + j < W) dst[start + j] = a3[j];
+        }
     }
 }
 
@@ -747,16 +836,13 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
         double *gt = a.jt;
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) gt[(4 * r4 + (lane >> 4)) * 16 + (lane & 15)] = g4[r4];
-        if constexpr (K == 16) wave_allreduce<WL>(acc);
+        if constexpr (K == 16) wave_reduce_store<WL>(acc, dst, lane);
         wave_sync_lds();
         if (lane == 0) {
             if constexpr (K < 16) {
                 dst[0] = gt[K * 16 + K];
 #pragma unroll
                 for (int j = 0; j < K; ++j) dst[1 + j] = gt[j * 16 + K];
-            } else {
-#pragma unroll
-                for (int q = 0; q < WL; ++q) dst[q] = acc[q];
             }
             int q = 1 + K;
 #pragma unroll
@@ -766,11 +852,7 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
         }
         wave_sync_lds();
     } else {
-        wave_allreduce<WL>(acc);
-        if (lane == 0) {
-#pragma unroll
-            for (int q = 0; q < W; ++q) dst[q] = acc[q];
-        }
+        wave_reduce_store<WL>(acc, dst, lane);
     }
     }
     if (a.parts == 1 || a.split) {
