@@ -15,20 +15,28 @@ end to end from host buffers (upload, 10 mixed-precision iterations,
 read-back), the per-round latency being the step; the round's one target goes
 over as a shared row (pop.bin v2), or tiled per expression with --tiled.
 
-roofline: the dominant launch is the fit kernel of the K bin that runs
-longest; its algorithmic HBM bytes (cusr_amd/benchmark/accounting.py: per LM
-iteration of each active expression two point-passes that each read y, X once
-per pass, the bytecode) over its duration from HIP events recorded around
-that launch on the stream it runs on. The same object carries the VALU figures,
-the roof this kernel is actually under: algorithmic flops over the same
-duration (a lower bound: a transcendental counts 2 flops), and, when the
-committed rocprofv3 counter summary (profiles/lm_fit_<config>_valu.json) was taken on
-this workload, the measured VALU busy fraction of the whole fit and of the
-dominant kernel running alone. traffic: measured HBM bytes of that launch, from the rocprofv3
-FETCH_SIZE / WRITE_SIZE summary committed under profiles/, when it was taken
-on this workload. cpu_baseline: the reference CPU path (scipy LM per
-expression over a process pool) on a sample of the same population sized to
-10-30 s, on this host's cores.
+roofline: the roof that binds the dominant launch (the K bin whose fit
+kernel runs longest) is VALU issue ("bound": "valu"): its algorithmic flops
+(cusr_amd/benchmark/accounting.py; a lower bound, a transcendental counts 2)
+over its duration running ALONE, against the MI355X fp64 vector peak. That
+duration comes from a leg after the timed steps that fits only the dominant
+bin's expressions (the same launch: the same expressions and iterations, no
+other bin beside it), timed with HIP events recorded around the launch on the
+stream it runs on; the contended duration inside the timed steps (the bins
+share the GPU over 4 streams) is reported beside it. `measured_valu_busy`
+gives SQ_ACTIVE_INST_VALU over the machine's VALU cycles for that kernel alone
+and for the whole fit, from the committed rocprofv3 counter summary
+(profiles/lm_fit_<config>_valu.json) when it was taken on this workload. The
+`hbm` block keeps the HBM figure: algorithmic bytes (per LM iteration of each
+active expression two point-passes that each read y, X once per pass, the
+bytecode) over the same alone duration against 8 TB/s, and `traffic` the
+measured HBM bytes of that launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+summary under profiles/. cpu_baseline: the reference CPU path (scipy LM per
+expression over a process pool, oracle/scipy_pop.py) on a sample of the same
+population, on every core granted to this process (within its cgroup CPU
+quota), the median of >= 3 repeats; with the host (lscpu, versions) and the
+quality of the CPU and GPU constants against the serial scipy oracle (tier-A/B
+of cusr_amd/benchmark/runner.py) on a prefix of the sample.
 """
 from __future__ import annotations
 
@@ -56,40 +64,103 @@ def _say(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(pop, target_s=15.0, min_s=10.0, max_s=30.0):
+def cpu_cores():
+    """(cores used, host description): every core in this process's affinity
+    mask, within its cgroup CPU quota when one is set."""
+    import platform
+    import subprocess
+
+    import scipy
+
+    granted = len(os.sched_getaffinity(0))
+    info = {"affinity_cores": granted, "os_cpu_count": os.cpu_count(),
+            "python": platform.python_version(), "numpy": np.__version__,
+            "scipy": scipy.__version__}
+    quota = None
+    try:
+        q, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        info["cgroup_cpu_max"] = f"{q} {period}"
+        if q != "max":
+            quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        keep = ("Model name", "CPU(s)", "Thread(s) per core", "Core(s) per socket",
+                "Socket(s)", "NUMA node(s)", "CPU max MHz")
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in keep:
+                info["lscpu " + k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    cores = min(granted, quota) if quota else granted
+    return cores, info
+
+
+def cpu_baseline(pop, gpu_c_final, repeats=3, target_s=15.0, quality_s=8.0):
     """scipy LM (the reference CPU path, restated in oracle/scipy_pop.py) on
     the first expressions of the population: a warm-up slice measures the
-    rate, the sample is sized to about target_s, and repeated until min_s of
-    wall time (never starting a repeat that would pass max_s)."""
-    from cusr_amd.benchmark import popio
+    rate, the sample is sized so `repeats` fits of it take about target_s,
+    and the value is the median rate of the repeats. Quality: the serial
+    scipy oracle (cached by population hash) on a prefix of the sample sized
+    to about quality_s, and tier-A/B of the pool's and the GPU's constants
+    against it, all rescored by the numpy fp64 scorer (oracle/interp.py)."""
+    import statistics
+
+    from cusr_amd.benchmark import popio, runner
+    from oracle import interp
     from oracle.scipy_pop import ScipyPop
 
-    nproc = min(16, os.cpu_count() or 1)
-    sp = ScipyPop(nproc=nproc)
+    cores, host = cpu_cores()
+    sp = ScipyPop(nproc=cores)
     try:
-        warm = popio.slice_pop(pop, min(2 * nproc, pop["M"]))
+        warm = popio.slice_pop(pop, min(2 * cores, pop["M"]))
         sp.fit_pop(warm)                       # pool start-up + imports
         t0 = time.perf_counter()
         r = sp.fit_pop(warm)
         rate = max(r["n_fit"], 1) / max(time.perf_counter() - t0, 1e-3)
-        n = int(min(pop["M"], max(nproc, rate * target_s)))
+        n = int(min(pop["M"], max(cores, rate * target_s / repeats)))
         sub = popio.slice_pop(pop, n)
-        fits, wall, reps = 0, 0.0, 0
-        while True:
+        rates, walls = [], []
+        for _ in range(repeats):
             t0 = time.perf_counter()
             r = sp.fit_pop(sub)
             dt = time.perf_counter() - t0
-            fits += r["n_fit"]
-            wall += dt
-            reps += 1
-            if wall >= min_s or wall + dt > max_s:
-                break
+            rates.append(r["n_fit"] / dt)
+            walls.append(dt)
     finally:
         sp.close()
-    return {"value": fits / wall, "unit": "fits/s", "cores": nproc, "kind": "port",
+    value = statistics.median(rates)
+    # quality on a prefix of the sample (the serial oracle runs on one core)
+    q = int(min(n, max(16, value / cores * quality_s)))
+    qpop = popio.slice_pop(pop, q)
+    nc = int(np.sum(qpop["metas"][:, 3]))
+    serial = ScipyPop(nproc=1)
+    try:
+        cache = REPO / "gpurun_out" / "oracle_cache"
+        orc = runner.cached_oracle(qpop, lambda p: serial.fit_pop(p)["c_final"],
+                                   lambda c: interp.loss_pop(qpop, c), cache)
+    finally:
+        serial.close()
+    K = qpop["metas"][:, 3]
+    quality = {"expressions": q, "oracle": "serial scipy least_squares lm (the same settings), "
+               f"{orc['wall']:.1f} s" + (" (cached)" if orc["cached"] else "")}
+    for name, c in (("cpu", r["c_final"][:nc]), ("gpu", np.asarray(gpu_c_final)[:nc])):
+        loss = interp.loss_pop(qpop, c)
+        ta, tb, el = runner.classify_tiers(loss, orc["loss_star"], K)
+        quality[name] = {"tier_a": runner.tier_rate(ta, el), "tier_b": runner.tier_rate(tb, el),
+                         "eligible": int(np.sum(el)),
+                         "spearman": runner.selection_fidelity(loss, orc["loss_star"],
+                                                               el)["spearman"]}
+    return {"value": value, "unit": "fits/s", "cores": cores, "kind": "port",
             "sample": (f"first {sub['M']} expressions of the same population "
-                       f"({r['n_fit']} with K>0) x {reps}, scipy least_squares lm "
-                       f"xtol=ftol=1e-10 max_nfev=200, {wall:.1f} s wall on {nproc} processes")}
+                       f"({r['n_fit']} with K>0), {repeats} repeats (median; rates "
+                       + ", ".join(f"{x:.1f}" for x in rates) + " fits/s; "
+                       + ", ".join(f"{w:.1f}" for w in walls) + " s wall) on "
+                       f"{cores} processes, scipy least_squares lm xtol=ftol=1e-10 "
+                       "max_nfev=200"),
+            "host": host, "quality": quality}
 
 
 def copy_calibration(co, pop):
@@ -173,35 +244,76 @@ def workload_text(cfg, pop):
             f"{'mixed fp32/fp64' if cfg.precision else 'fp64'}")
 
 
-def roofline(pop, cfg, iters, bins, kname_of, device_ms=None):
-    """Dominant launch (longest K bin) against HBM, with its VALU figures."""
+def launch_bins(pop):
+    """The launch bin of every expression: its K on the fast kernels, or
+    CO_GENERAL_BIN (include/cusr_co.h co_fast_path)."""
+    from cusr_amd.kernel import co_inproc
+
+    rc, *_, route = co_inproc.decode(pop, "ad", full=True)
+    if rc != 0:
+        raise RuntimeError(f"co_decode failed ({rc})")
+    K = np.asarray(pop["metas"])[:, 3]
+    return np.where(route != 0, co_inproc.CO_GENERAL_BIN, K)
+
+
+def kernel_name(cfg, pop, k):
+    """Kernel name (as rocprofv3 shows it, without the last template
+    arguments) of bin k's fit: lm_fit_kernel / lm_fit_gen_kernel, or the
+    split path's lm_pass_kernel, which the step kernel follows."""
+    from cusr_amd.kernel import co_inproc
+
+    rname = "double" if cfg.precision == 0 else "float"
+    gen = k == co_inproc.CO_GENERAL_BIN
+    if co_inproc.co_partitions_for_n(int(pop["N"])) > co_inproc.CO_MAX_PARTITIONS:
+        return (f"lm_pass_kernel<{co_inproc.CO_MAX_K if gen else k}, {rname}, "
+                f"{cfg.ad_mode}")
+    if gen:
+        return f"lm_fit_gen_kernel<{rname}, {cfg.ad_mode}"
+    return f"lm_fit_kernel<{k}, {rname}, {cfg.ad_mode}"
+
+
+def alone_leg(fit_alone, pop, bin_of, kdom, reps):
+    """Duration of bin kdom's launch with no other bin beside it: fit only
+    its expressions, `reps` times, and read the bin's HIP-event time."""
+    from cusr_amd.benchmark import popio
+
+    sub = popio.select_pop(pop, np.flatnonzero(bin_of == kdom))
+    ms = [float(fit_alone(sub)[kdom]) for _ in range(reps)]
+    return float(np.mean(ms)), ms
+
+
+def roofline(pop, cfg, iters, bins, kdom, alone_ms, alone_runs, bin_of, device_ms=None):
+    """Dominant launch against the fp64 (fp32 for mixed) vector peak, with
+    the HBM figure as a secondary block."""
     from cusr_amd.benchmark import accounting
 
-    K = pop["metas"][:, 3]
-    kdom = int(np.argmax(bins))
-    w = accounting.algorithmic_work(pop, iters, cfg.ad_mode, subset=(K == kdom))
-    dom_s = bins[kdom] / 1e3
-    achieved = w["bytes"] / dom_s / 1e9
+    w = accounting.algorithmic_work(pop, iters, cfg.ad_mode, subset=(bin_of == kdom))
+    dom_s = alone_ms / 1e3
     vpeak = FP64_VECTOR_PEAK_TFLOPS if cfg.precision == 0 else FP32_VECTOR_PEAK_TFLOPS
     tflops = w["flops"] / dom_s / 1e12
-    kname = kname_of(kdom)
+    gbs = w["bytes"] / dom_s / 1e9
+    kname = kernel_name(cfg, pop, kdom)
     key = f"{cfg.name}:{pop['M']}x{pop['N']}:seed{cfg.seed}:it{cfg.max_iter}"
-    valu = {"achieved": tflops, "peak": vpeak, "unit": "TFLOP/s", "frac": tflops / vpeak,
-            "algorithmic_flops_per_launch": w["flops"]}
+    out = {"bound": "valu", "achieved": tflops, "peak": vpeak, "unit": "TFLOP/s",
+           "frac": tflops / vpeak, "traffic": load_traffic(key, kname),
+           "kernel": kname + ", ...>", "bin": int(kdom),
+           "expressions_in_launch": int(np.sum(bin_of == kdom)),
+           "launch_ms": alone_ms, "launch_ms_runs": alone_runs,
+           "launch_ms_concurrent": float(bins[kdom]),
+           "algorithmic_flops_per_launch": w["flops"],
+           "hbm": {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                   "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": w["bytes"]}}
     if device_ms:
-        valu["measured_issue"] = valu_issue(key, kname_of, bins, device_ms, kdom)
-    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(key, kname),
-            "kernel": kname, "expressions_in_launch": int(np.sum(K == kdom)),
-            "launch_ms": float(bins[kdom]), "algorithmic_bytes_per_launch": w["bytes"],
-            "valu": valu}
+        out["measured_valu_busy"] = valu_issue(key, lambda k: kernel_name(cfg, pop, k), bins,
+                                               device_ms, kdom)
+    return out
 
 
 def run_resident(args, cfg, co, pop):
     """C1-C4: fit the HBM-resident population `steps` times."""
     from cusr_amd.benchmark import accounting
 
-    fit_kw = dict(ad_mode=cfg.ad_mode, precision=cfg.precision)
+    fit_kw = dict(ad_mode=cfg.ad_mode, precision=cfg.precision, partitions=args.partitions)
     if args.copy_calibration:
         copy_calibration(co, pop)
     co.upload(pop)
@@ -227,14 +339,24 @@ def run_resident(args, cfg, co, pop):
     value = n_fit / (ms_per_step / 1e3)
     kms = float(np.mean(fit_ms))
     bins = np.mean(np.asarray(bin_ms), axis=0)
-    rname = "double" if cfg.precision == 0 else "float"
-    roof = roofline(pop, cfg, res["iters"], bins,
-                    lambda k: f"lm_fit_kernel<{k}, {rname}, {cfg.ad_mode}>", device_ms=kms)
+    bin_of = launch_bins(pop)
+    kdom = int(np.argmax(bins))
+
+    def fit_alone(sub):
+        co.upload(sub)
+        co.fit_resident(cfg.max_iter, outputs=False, **fit_kw)
+        return co.last_bin_ms()
+
+    alone_ms, alone_runs = alone_leg(fit_alone, pop, bin_of, kdom, args.alone_reps)
+    roof = roofline(pop, cfg, res["iters"], bins, kdom, alone_ms, alone_runs, bin_of,
+                    device_ms=kms)
     whole = accounting.algorithmic_work(pop, res["iters"], cfg.ad_mode)
     status_counts = np.bincount(res["status"], minlength=5).tolist()
     _say(f"{args.steps} steps: {ms_per_step:.2f} ms/step, device {kms:.2f} ms/fit, "
          f"{value:.0f} fits/s, statuses {status_counts}, mean iters {res['iters'].mean():.1f}")
     _say("per-bin kernel ms: " + " ".join(f"K{k}={v:.2f}" for k, v in enumerate(bins) if v >= 0))
+    _say(f"dominant bin {kdom} alone: {alone_ms:.3f} ms ({len(alone_runs)} launches), "
+         f"{bins[kdom]:.3f} ms beside the other bins")
     fit = {"status_counts": status_counts, "mean_iters": float(res["iters"].mean()),
            "device_ms_per_fit": kms, "fits_per_s_device": n_fit / (kms / 1e3),
            "hbm_gbs_whole_fit": whole["bytes"] / (kms / 1e3) / 1e9,
@@ -242,7 +364,7 @@ def run_resident(args, cfg, co, pop):
            "e2e_ms_from_host": None if np.isnan(e2e_ms) else e2e_ms,
            "fits_per_s_from_host": None if np.isnan(e2e_ms) else n_fit / (e2e_ms / 1e3),
            "bin_ms": {str(k): float(v) for k, v in enumerate(bins) if v >= 0}}
-    return value, ms_per_step, roof, fit
+    return value, ms_per_step, roof, fit, res
 
 
 def run_rounds(args, cfg, co, gen):
@@ -273,12 +395,21 @@ def run_rounds(args, cfg, co, gen):
         last = (pop, res, co.last_bin_ms())
     value = fits / (sum(lat) / 1e3)
     pop, res, bins = last
-    roof = roofline(pop, cfg, res["iters"], bins, lambda k: f"lm_fit_kernel<{k}, float, 0>",
+    bin_of = launch_bins(pop)
+    kdom = int(np.argmax(bins))
+
+    def fit_alone(sub):
+        co.optimize_ex(sub, cfg.max_iter, ad_mode=cfg.ad_mode, precision=cfg.precision)
+        return co.last_bin_ms()
+
+    alone_ms, alone_runs = alone_leg(fit_alone, pop, bin_of, kdom, args.alone_reps)
+    _say(f"dominant bin {kdom} alone: {alone_ms:.3f} ms, {bins[kdom]:.3f} ms beside the others")
+    roof = roofline(pop, cfg, res["iters"], bins, kdom, alone_ms, alone_runs, bin_of,
                     device_ms=rounds[-1]["device_ms"])
     fit = {"rounds": rounds, "mean_round_ms": float(np.mean(lat)),
            "p50_round_ms": float(np.median(lat)),
            "target": "tiled [M][N]" if args.tiled else "shared row [N] (pop.bin v2)"}
-    return value, float(np.mean(lat)), roof, fit, pop
+    return value, float(np.mean(lat)), roof, fit, pop, res
 
 
 def main():
@@ -297,6 +428,11 @@ def main():
                     help="C5: send the target tiled per expression, as the reference does")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one copy kernel of known size (for rocprofv3 --pmc scaling)")
+    ap.add_argument("--alone-reps", type=int, default=3,
+                    help="launches of the dominant bin alone (the roofline's duration)")
+    ap.add_argument("--partitions", type=int, default=0,
+                    help="point partitions per expression (0: by N, co_partitions_for_n; "
+                         "above 4 the split path)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build measures "
@@ -321,17 +457,18 @@ def main():
         return pop
 
     if cfg.rounds > 1:
-        value, ms_per_step, roof, fit, pop = run_rounds(args, cfg, co, gen)
+        value, ms_per_step, roof, fit, pop, res = run_rounds(args, cfg, co, gen)
         steps, warmup = args.rounds, 1
     else:
         pop = gen()
-        value, ms_per_step, roof, fit = run_resident(args, cfg, co, pop)
+        value, ms_per_step, roof, fit, res = run_resident(args, cfg, co, pop)
         steps, warmup = args.steps, args.warmup
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(pop)
-        _say(f"cpu baseline {cpu['value']:.1f} fits/s on {cpu['cores']} cores")
+        cpu = cpu_baseline(pop, res["c_final"])
+        _say(f"cpu baseline {cpu['value']:.1f} fits/s on {cpu['cores']} cores; quality "
+             + json.dumps(cpu["quality"]))
 
     metric = HEADLINE_METRIC if cfg.name == "C2" else \
         f"expressions fitted/sec ({cfg.name}) + achieved HBM GB/s"

@@ -18,6 +18,7 @@ scipy oracle, a numpy scorer) are supplied by whoever runs it.
 """
 from __future__ import annotations
 
+import hashlib
 import json
 import socket
 import time
@@ -71,6 +72,44 @@ def selection_fidelity(loss_b, loss_star, eligible) -> dict:
         best_b = set(idx[np.argsort(loss_b[idx])[:k]].tolist())
         out[key] = len(best_o & best_b) / k
     return out
+
+
+def pop_sha(pop: dict) -> str:
+    """sha1 (16 hex digits) of everything a fit reads: programs, metas,
+    starting constants, X and the target rows."""
+    h = hashlib.sha1()
+    for a in (pop["nt"], pop["nv"], pop["ci"], pop["metas"], pop["c_init"], pop["xs"],
+              popio.y_rows(pop)):
+        a = np.ascontiguousarray(a)
+        h.update(str((a.dtype.str, a.shape)).encode())
+        h.update(a.tobytes())
+    return h.hexdigest()[:16]
+
+
+def cached_oracle(pop: dict, fit_serial, score, cache_dir, limit: int | None = None) -> dict:
+    """The tight serial oracle of a population, cached by (population sha1,
+    limit) as the reference caches it by file sha1 (cusr/benchmark/runner.py:
+    111-128): fit_serial(pop) -> c_final (a serial fit, reproducible bit for
+    bit, which a process pool is not on degenerate expressions), score(c) ->
+    per-expression fp64 loss. Returns loss_star, c_star, wall (of the fit that
+    filled the cache) and cached."""
+    if limit is not None:
+        pop = popio.slice_pop(pop, limit)
+    cache_dir = Path(cache_dir)
+    path = cache_dir / f"oracle_{pop_sha(pop)}_L{limit or 'all'}_serial.npz"
+    if path.exists():
+        z = np.load(path)
+        return {"loss_star": z["loss_star"], "c_star": z["c_star"], "wall": float(z["wall"]),
+                "cached": True}
+    t0 = time.perf_counter()
+    c_star = np.asarray(fit_serial(pop), np.float64)
+    loss_star = np.asarray(score(c_star), np.float64)
+    wall = time.perf_counter() - t0
+    cache_dir.mkdir(parents=True, exist_ok=True)
+    tmp = path.with_suffix(".tmp.npz")
+    np.savez(tmp, loss_star=loss_star, c_star=c_star, wall=wall)
+    tmp.replace(path)
+    return {"loss_star": loss_star, "c_star": c_star, "wall": wall, "cached": False}
 
 
 def run_quality(pop: dict, backends: dict, loss_star: np.ndarray, score, *, repeats: int = 3,

@@ -47,7 +47,7 @@ CO_GENERAL_BIN = CO_FAST_MAX_K + 1
 CO_BINS = CO_FAST_MAX_K + 2
 # point partitions (include/cusr_co.h co_partitions_for_n): beyond
 # CO_MAX_PARTITIONS each partition is a workgroup (the split path)
-CO_MAX_PARTITIONS, CO_MAX_SPLIT, CO_SPLIT_MIN_N = 4, 256, 262144
+CO_MAX_PARTITIONS, CO_MAX_SPLIT, CO_SPLIT_MIN_N = 4, 256, 65536
 CO_STATIC_SCRATCH_BYTES = 64 << 20
 
 

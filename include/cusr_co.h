@@ -138,13 +138,15 @@ typedef struct CoOptions {
  * slowest expressions of a K bin, which set its duration (C2 -11 %, C3
  * -20 %, C5 even); four pay off only for long expressions. From
  * CO_SPLIT_MIN_N points an expression's passes spread over G = N / 4,096
- * (a power of two, at most CO_MAX_SPLIT) workgroups, whose partition sums
- * meet in HBM and are added in partition order by a step kernel that runs
- * the LM update (the split path): a population of a few long expressions
- * then still fills the GPU. */
+ * (rounded down to a power of two, 16 to CO_MAX_SPLIT) workgroups, whose
+ * partition sums meet in HBM and are added in partition order by a step
+ * kernel that runs the LM update (the split path): the waves of many
+ * workgroups hide the loads of long passes, and a population of a few long
+ * expressions still fills the GPU (C4, N = 100,000: 16 partitions, 266 ->
+ * 189 ms per fit against four wavefronts of one workgroup). */
 #define CO_MAX_PARTITIONS 4
 #define CO_MAX_SPLIT 256
-#define CO_SPLIT_MIN_N 262144
+#define CO_SPLIT_MIN_N 65536
 static inline int co_partitions_for_n(int N) {
     if (N >= CO_SPLIT_MIN_N) {
         int g = 8;
