@@ -2,6 +2,7 @@
 // (cusr/kernel/batch_lm_ad.cu:196-551):
 //
 //   batch_lm_ad <pop.bin> [out_dir] [--max-iter N] [--quiet] [--rev] [--mixed]
+//               [--profile]
 //
 // Reads pop.bin v1 and the v2 extension (float64 payloads, shared target;
 // include/pop_format.h).
@@ -11,6 +12,12 @@
 //   [batch-lm] 总耗时 <seconds> 秒 (<trees/s> trees/s, M_prob=<M>)
 // Exit status: 0 ok, 1 load or device failure, 2 beyond device bounds.
 // --rev / --mixed select reverse AD / mixed precision (extensions).
+// --profile prints one machine-readable line whatever --quiet says, with the
+// fields of the reference's -DPROFILE build that a caller compares against
+// (batch_lm_ad.cu:553-575): PROFILE_JSON {"M","N","load_ms","setup_ms",
+// "loop_ms","total_ms","gpu_sum_ms"}; setup/loop are co_last_split's (upload
+// and checks / device fit until the results are on the host), gpu_sum_ms the
+// device time of the fit (co_last_kernel_ms).
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -124,12 +131,13 @@ int main(int argc, char **argv) {
     const double t0 = seconds();
     const char *pop_path = argv[1];
     std::string out_dir;
-    int max_iter = 50, quiet = 0, rev = 0, mixed = 0;
+    int max_iter = 50, quiet = 0, rev = 0, mixed = 0, profile = 0;
     for (int i = 2; i < argc; i++) {
         if (!strcmp(argv[i], "--max-iter") && i + 1 < argc) max_iter = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--quiet")) quiet = 1;
         else if (!strcmp(argv[i], "--rev")) rev = 1;
         else if (!strcmp(argv[i], "--mixed")) mixed = 1;
+        else if (!strcmp(argv[i], "--profile")) profile = 1;
         else if (argv[i][0] != '-') out_dir = argv[i];
     }
     if (out_dir.empty()) {
@@ -141,6 +149,7 @@ int main(int argc, char **argv) {
         fprintf(stderr, "load failed.\n");
         return 1;
     }
+    const double t_load = seconds();
     const PopHeader &h = p.h;
     if (!quiet)
         printf("[batch-lm] loaded %s: M_prob=%d total_nodes=%d total_c=%d N=%d n_vars=%d "
@@ -177,6 +186,9 @@ int main(int argc, char **argv) {
     int rc = co_optimize_ex(handle, &opt, &h, p.nt.data(), p.nv.data(), p.ci.data(),
                             p.metas.data(), p.c_init.data(), p.xs.data(), p.ym.data(), cf.data(),
                             status.data(), li.data(), lf.data(), iters.data());
+    double setup_ms = -1.0, loop_ms = -1.0, gpu_ms = -1.0;
+    co_last_split(&setup_ms, &loop_ms);
+    co_last_kernel_ms(handle, &gpu_ms);
     co_teardown(handle);
     if (rc != CO_OK) {
         fprintf(stderr, "[batch-lm] fit failed (code %d)\n", rc);
@@ -206,5 +218,9 @@ int main(int argc, char **argv) {
                cnt[0], M ? 100.0 * cnt[0] / M : 0.0, cnt[1], cnt[2], cnt[4], cnt[3], h.M_prob);
         printf("[batch-lm] 总耗时 %.3f 秒 (%.0f trees/s, M_prob=%d)\n", el, M / el, h.M_prob);
     }
+    if (profile)
+        printf("PROFILE_JSON {\"M\":%d,\"N\":%d,\"load_ms\":%.4f,\"setup_ms\":%.4f,"
+               "\"loop_ms\":%.4f,\"total_ms\":%.4f,\"gpu_sum_ms\":%.4f}\n",
+               h.M_prob, h.N, 1e3 * (t_load - t0), setup_ms, loop_ms, 1e3 * el, gpu_ms);
     return 0;
 }

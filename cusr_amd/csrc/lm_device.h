@@ -163,6 +163,12 @@ template <> struct Fn<double> {
     static __device__ __forceinline__ double abs_(double a) { return ::fabs(a); }
     static __device__ __forceinline__ double max_(double a, double b) { return ::fmax(a, b); }
     static __device__ __forceinline__ double min_(double a, double b) { return ::fmin(a, b); }
+    template <int P>
+    static __device__ __forceinline__ void sincos_v(const double *a, double *s, double *c) { cm_sincos_v<P>(a, s, c); }
+    template <int P>
+    static __device__ __forceinline__ void log_v(const double *a, double *r) { cm_log_v<P>(a, r); }
+    template <int P>
+    static __device__ __forceinline__ void exp_v(const double *a, double *r) { cm_exp_v<P>(a, r); }
     static constexpr double cexp_cap = kCexpCap64;
     static constexpr double eps9 = 1e-9;
 };
@@ -179,6 +185,12 @@ template <> struct Fn<float> {
     static __device__ __forceinline__ float abs_(float a) { return ::fabsf(a); }
     static __device__ __forceinline__ float max_(float a, float b) { return ::fmaxf(a, b); }
     static __device__ __forceinline__ float min_(float a, float b) { return ::fminf(a, b); }
+    template <int P>
+    static __device__ __forceinline__ void sincos_v(const float *a, float *s, float *c) { cm_sincosf_v<P>(a, s, c); }
+    template <int P>
+    static __device__ __forceinline__ void log_v(const float *a, float *r) { cm_logf_v<P>(a, r); }
+    template <int P>
+    static __device__ __forceinline__ void exp_v(const float *a, float *r) { cm_expf_v<P>(a, r); }
     static constexpr float cexp_cap = kCexpCap32;
     static constexpr float eps9 = 1e-9f;
 };
@@ -193,16 +205,40 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
     typedef Fn<R> F;
     const R one = R(1), zero = R(0), two = R(2);
     CUSR_FOR_P z[p] = false;
+    // sin, cos, tan, log and exp take the P-wide forms of include/cusr_math.h
+    // (the scalar functions' bits, the P points interleaved)
     switch (f) {
-    case OP_SIN: CUSR_FOR_P F::sincos_(a[p], &r[p], &d[p]); break;
-    case OP_COS: CUSR_FOR_P { R s; F::sincos_(a[p], &s, &r[p]); d[p] = -s; } break;
-    case OP_TAN: CUSR_FOR_P { r[p] = F::tan_(a[p]); d[p] = one + r[p] * r[p]; } break;
+    case OP_SIN: F::template sincos_v<P>(a, r, d); break;
+    case OP_COS: {
+        R s[P];
+        F::template sincos_v<P>(a, s, r);
+        CUSR_FOR_P d[p] = -s[p];
+        break;
+    }
+    case OP_TAN: {
+        R s[P], c[P];
+        F::template sincos_v<P>(a, s, c);
+        CUSR_FOR_P { r[p] = s[p] / c[p]; d[p] = one + r[p] * r[p]; }
+        break;
+    }
     case OP_SINH: CUSR_FOR_P { r[p] = F::sinh_(a[p]); d[p] = F::cosh_(a[p]); } break;
     case OP_COSH: CUSR_FOR_P { r[p] = F::cosh_(a[p]); d[p] = F::sinh_(a[p]); } break;
     case OP_TANH: CUSR_FOR_P { r[p] = F::tanh_(a[p]); d[p] = one - r[p] * r[p]; } break;
-    case OP_LOG: CUSR_FOR_P { r[p] = F::log_(a[p]); d[p] = one / a[p]; } break;
-    case OP_LOOSE_LOG: CUSR_FOR_P { r[p] = F::log_(F::abs_(a[p])); d[p] = one / a[p]; } break;
-    case OP_EXP: CUSR_FOR_P { r[p] = F::exp_(a[p]); d[p] = r[p]; } break;
+    case OP_LOG:
+        F::template log_v<P>(a, r);
+        CUSR_FOR_P d[p] = one / a[p];
+        break;
+    case OP_LOOSE_LOG: {
+        R aa[P];
+        CUSR_FOR_P aa[p] = F::abs_(a[p]);
+        F::template log_v<P>(aa, r);
+        CUSR_FOR_P d[p] = one / a[p];
+        break;
+    }
+    case OP_EXP:
+        F::template exp_v<P>(a, r);
+        CUSR_FOR_P d[p] = r[p];
+        break;
     case OP_INV: case OP_LOOSE_INV: CUSR_FOR_P { r[p] = one / a[p]; d[p] = -(r[p] * r[p]); } break;
     case OP_NEG: CUSR_FOR_P { r[p] = -a[p]; d[p] = -one; } break;
     case OP_ABS:
@@ -219,24 +255,29 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
             d[p] = (a[p] > zero) ? inv : ((a[p] < zero) ? -inv : zero);
         }
         break;
-    case OP_CEXP:
+    case OP_CEXP: {
+        R xin[P], e[P];
+        CUSR_FOR_P xin[p] = (a[p] > R(20)) ? zero : a[p];
+        F::template exp_v<P>(xin, e);
         CUSR_FOR_P {
             const bool flat = a[p] > R(20);
-            const R e = F::exp_(flat ? zero : a[p]);
-            r[p] = flat ? F::cexp_cap : e;
-            d[p] = flat ? zero : e;
+            r[p] = flat ? F::cexp_cap : e[p];
+            d[p] = flat ? zero : e[p];
             z[p] = flat;
         }
         break;
+    }
     case OP_SQUARE: CUSR_FOR_P { r[p] = a[p] * a[p]; d[p] = a[p] + a[p]; } break;
-    case OP_PLOG:
+    case OP_PLOG: {
+        R t[P];
+        CUSR_FOR_P t[p] = F::abs_(a[p]) + F::eps9;
+        F::template log_v<P>(t, r);
         CUSR_FOR_P {
-            const R t = F::abs_(a[p]) + F::eps9;
-            r[p] = F::log_(t);
-            const R inv = one / t;
+            const R inv = one / t[p];
             d[p] = (a[p] > zero) ? inv : ((a[p] < zero) ? -inv : zero);
         }
         break;
+    }
     case OP_IDENT: CUSR_FOR_P { r[p] = a[p]; d[p] = one; } break;
     default: CUSR_FOR_P { r[p] = zero; d[p] = zero; } break;
     }

@@ -1,5 +1,5 @@
 """Constant-optimisation backend for a GP inner loop, with the reference
-demonstrator's contract (cusr/demonstrator/co_backend.py:25-47, 250-285;
+demonstrator's contract (cusr/demonstrator/co_backend.py:25-47, 240-285;
 cusr/demonstrator/kernel_bridge.py:140-238):
 
     fit_batch(skeletons, inits, X, y, *, max_iter, native) -> [COResult]
@@ -8,21 +8,38 @@ Every candidate shares one problem's (X, y). `native[j]` is candidate j's
 expression in prefix form, (nt, nv, ci) arrays of pop.bin node types, values
 and constant ranks (the reference extracts the same arrays from its EvoGP
 trees; that extraction belongs to the GP system, not to this library).
-`skeletons[j]` is only consulted for `n_constants` when it has one. (X, y)
-goes to the device once and stays there while later calls pass the same
-values; the reference re-sends X with y tiled per candidate on every call
-(kernel_bridge.py:200-206).
 
-Candidates the device cannot take (more than 16 constants, a value stack
-deeper than 16, more than 255 nodes, more than 8 variables) go to the
-`fallback` backend when one is given; without one they raise, since this
-library has no CPU path of its own. Results stay aligned with the input
-order; final_loss is mean(r^2) = 2 * loss / N in fp64; converged is
-status == CONVERGED (kernel_bridge.py:216).
+Three faces:
+  KernelLM      this library's fast path: (X, y) goes to the device once and
+                stays there while later calls pass the same values, the fit
+                runs in fp64 from the fp64 starting constants, and an optional
+                warm-start cache reuses fitted constants per structure.
+  CudaKernelLM  the reference's drop-in (co_backend.py:240-285): the same
+                constructor, the float32 pop.bin carrier with y tiled per
+                candidate, either through the CLI in a subprocess
+                (inproc=False, the reference's default) or through the
+                library's co_optimize in this process (inproc=True) -- the
+                two give the same bytes; the loss is recomputed in fp64 by
+                skeleton.residual when the skeleton has one; candidates the
+                device cannot take go to `fallback`, ScipyLM by default.
+  ScipyLM       the reference's CPU backend (co_backend.py:52-93) for those
+                candidates only: scipy least_squares over the skeleton's own
+                residual (and Jacobian when it has one).
+
+Candidates the device cannot take: more than CO_MAX_K (32) constants, a value
+stack deeper than CO_MAX_STACK (64), more than CO_MAX_VARS (255) variables,
+or node types beyond the pop.bin set (the reference's TFUNC). They never
+reach the device; eligible candidates never reach the CPU backend, and a
+missing library raises (no CPU path stands in for it). Results stay aligned
+with the input order; final_loss is mean(r^2); converged is status ==
+CONVERGED (kernel_bridge.py:216).
 """
 from __future__ import annotations
 
 import hashlib
+import pathlib
+import subprocess
+import tempfile
 from collections import OrderedDict
 from dataclasses import dataclass
 
@@ -213,6 +230,178 @@ class KernelLM:
             for sk, r in zip(keys, results):
                 self.cache.put(dkey, sk, r.constants, r.final_loss)
         stats["n_warm"] = n_warm
+        self.last_stats = stats
+        for k, v in stats.items():
+            self.cum_stats[k] = self.cum_stats.get(k, 0) + v
+        return results
+
+
+# ---------------------------------------------------------------------------
+# The reference's drop-in faces: ScipyLM (CPU, for what the device cannot
+# take) and CudaKernelLM (the kernel through pop.bin, subprocess or in-process)
+# ---------------------------------------------------------------------------
+
+class ScipyLM:
+    """scipy least_squares (method 'lm', max_nfev = max_iter) per candidate
+    over the skeleton's residual(c, X, y) and, when it has one, its
+    jacobian(c, X) (cusr/demonstrator/co_backend.py:52-93). A candidate whose
+    fit raises keeps its initial constants (converged False) instead of
+    failing the batch."""
+
+    name = "scipy_lm"
+
+    def fit_batch(self, skeletons, inits, X, y, *, max_iter=100, native=None) -> list[COResult]:
+        from scipy.optimize import least_squares
+
+        if skeletons is None:
+            raise ValueError("ScipyLM fits through skeleton.residual; no skeletons were given")
+        X = np.asarray(X, dtype=np.float64)
+        y = np.asarray(y, dtype=np.float64).ravel()
+        out = []
+        for skel, c0 in zip(skeletons, inits):
+            c0 = np.asarray(c0, dtype=np.float64).ravel()
+
+            def loss_at(c):
+                try:
+                    return float(np.mean(np.asarray(skel.residual(c, X, y)) ** 2))
+                except Exception:  # noqa: BLE001 -- scoring must not fail the batch
+                    return float("inf")
+
+            if c0.size == 0:
+                out.append(COResult(c0.copy(), 0, True, loss_at(c0)))
+                continue
+            kw = {"jac": (lambda c: skel.jacobian(c, X))} if hasattr(skel, "jacobian") else {}
+            try:
+                r = least_squares(lambda c: skel.residual(c, X, y), c0, method="lm",
+                                  max_nfev=int(max_iter), **kw)
+                out.append(COResult(np.asarray(r.x, np.float64), int(r.nfev), bool(r.success),
+                                    float(np.mean(r.fun ** 2))))
+            except Exception:  # noqa: BLE001 -- one candidate must not fail the batch
+                out.append(COResult(c0.copy(), 0, False, loss_at(c0)))
+        return out
+
+
+_KDIR = pathlib.Path(__file__).resolve().parents[1] / "kernel"
+DEFAULT_BINARY = _KDIR / "batch_lm"          # the reference's default (kernel_bridge.py:44)
+
+
+class KernelRunError(RuntimeError):
+    pass
+
+
+def variant_for_binary(binary) -> str:
+    """The library variant whose bytes the CLI `binary` reproduces: '_ad'
+    names the AD ordering, anything else the FD one (kernel_bridge.py:
+    120-129)."""
+    return "ad" if pathlib.Path(binary).name.endswith("_ad") else "fd"
+
+
+def run_cli(pop: dict, binary, max_iter: int):
+    """pop.bin through the CLI in a subprocess (kernel_bridge.py:94-113):
+    (c_final float64 from the float32 blob, raw status, loss_final float32)."""
+    binary = pathlib.Path(binary)
+    if not binary.exists():
+        raise KernelRunError(f"batch_lm binary not found: {binary}")
+    with tempfile.TemporaryDirectory(prefix="co_kernel_") as td:
+        td = pathlib.Path(td)
+        popio.save_pop_bin(pop, td / "pop.bin")
+        cmd = [str(binary), str(td / "pop.bin"), str(td), "--quiet"]
+        if max_iter is not None:
+            cmd += ["--max-iter", str(int(max_iter))]
+        r = subprocess.run(cmd, capture_output=True, encoding="utf-8")
+        if r.returncode != 0:
+            raise KernelRunError(f"exit={r.returncode}: {(r.stderr or r.stdout)[-500:]}")
+        status = np.fromfile(td / "status.bin", dtype=np.int32)
+        c_final = np.fromfile(td / "c_final.bin", dtype=np.float32).astype(np.float64)
+        loss_final = np.fromfile(td / "loss_final.bin", dtype=np.float32)
+    return c_final, status, loss_final
+
+
+def run_inproc(pop: dict, binary, max_iter: int, device_id: int):
+    """The same contract through co_optimize in this process (the float32
+    entry point the CLI's bytes come from): no subprocess, no disk, the
+    device context paid once per process (kernel_bridge.py:132-147)."""
+    from cusr_amd.kernel import co_inproc
+
+    co = co_inproc.get_inproc_co(device_id=device_id, variant=variant_for_binary(binary))
+    with co.lock:
+        out = co.optimize(pop, max_iter=max_iter)
+    return (np.asarray(out["c_final"], np.float32).astype(np.float64),
+            np.asarray(out["status"], np.int32), np.asarray(out["loss_final"], np.float32))
+
+
+class CudaKernelLM:
+    """The reference's kernel backend (cusr/demonstrator/co_backend.py:240-285)
+    with its constructor: binary (the CLI; None: DEFAULT_BINARY), max_iter (LM
+    iterations), fallback (None: ScipyLM), inproc (False: the CLI in a
+    subprocess per call; True: co_optimize in this process) and device_id.
+    last_stats / cum_stats count candidates by route."""
+
+    name = "cuda_kernel_lm"
+
+    def __init__(self, binary=None, max_iter: int = 50, fallback=None, inproc: bool = False,
+                 device_id: int = 0):
+        self.binary = binary
+        self.max_iter = max_iter
+        self.fallback = fallback
+        self.inproc = bool(inproc)
+        self.device_id = int(device_id)
+        self.last_stats: dict = {}
+        self.cum_stats: dict = {}
+
+    def fit_batch(self, skeletons, inits, X, y, *, max_iter=100, native=None) -> list[COResult]:
+        if native is None:
+            raise ValueError("CudaKernelLM needs every candidate's prefix arrays via native=")
+        X = np.asarray(X, dtype=np.float64)
+        y = np.asarray(y, dtype=np.float64).ravel()
+        n_vars = X.shape[1]
+        binary = self.binary or DEFAULT_BINARY
+        M = len(native)
+        results = [None] * M
+        take, fb, n_overflow, n_kmismatch = [], [], 0, 0
+        for j, nat in enumerate(native):
+            nt = np.asarray(nat[0])
+            K = int(np.sum(nt == popio.NODE_CONST))
+            skel = skeletons[j] if skeletons is not None else None
+            if not _eligible(nt, n_vars):
+                n_overflow += 1
+                fb.append(j)
+            elif skel is not None and hasattr(skel, "n_constants") and skel.n_constants != K:
+                n_kmismatch += 1
+                fb.append(j)
+            else:
+                take.append(j)
+        if take:
+            trees = [tuple(np.asarray(a) for a in native[j][:3]) +
+                     (np.asarray(inits[j], np.float32),) for j in take]
+            pop = popio.build_pop(trees, X, np.tile(y, (len(take), 1)))
+            if self.inproc:
+                c_final, status, loss32 = run_inproc(pop, binary, self.max_iter, self.device_id)
+            else:
+                c_final, status, loss32 = run_cli(pop, binary, self.max_iter)
+            for slot, j in enumerate(take):
+                _, _, c_off, K = (int(v) for v in pop["metas"][slot])
+                c = np.asarray(c_final[c_off:c_off + K], np.float64)
+                skel = skeletons[j] if skeletons is not None else None
+                if skel is not None and hasattr(skel, "residual"):
+                    try:
+                        loss = float(np.mean(np.asarray(skel.residual(c, X, y)) ** 2))
+                    except Exception:  # noqa: BLE001 -- scoring must not fail the batch
+                        loss = float("inf")
+                else:
+                    # the device's loss 0.5 * sum r^2 as mean r^2
+                    lf = float(loss32[slot])
+                    loss = 2.0 * lf / len(y) if np.isfinite(lf) else float("inf")
+                results[j] = COResult(c, -1, bool(int(status[slot]) == 0), loss)
+        if fb:
+            be = self.fallback if self.fallback is not None else ScipyLM()
+            fb_res = be.fit_batch([skeletons[j] for j in fb] if skeletons is not None else None,
+                                  [inits[j] for j in fb], X, y, max_iter=max_iter,
+                                  native=[native[j] for j in fb])
+            for j, r in zip(fb, fb_res):
+                results[j] = r
+        stats = dict(n_total=M, n_kernel=len(take), n_fallback=len(fb), n_overflow=n_overflow,
+                     n_kmismatch=n_kmismatch)
         self.last_stats = stats
         for k, v in stats.items():
             self.cum_stats[k] = self.cum_stats.get(k, 0) + v

@@ -453,6 +453,219 @@ CM_FN float cm_sinf(float x) { float s, c; cm_sincosf(x, &s, &c); return s; }
 CM_FN float cm_cosf(float x) { float s, c; cm_sincosf(x, &s, &c); return c; }
 CM_FN float cm_tanf(float x) { float s, c; cm_sincosf(x, &s, &c); return s / c; }
 
+/* ----------------------------------------------- P-wide forms (HIP only) */
+
+/* The interpreter evaluates an operator for P points per lane at once. These
+ * forms run exactly the operations of cm_exp, cm_log, cm_sincos, cm_expf,
+ * cm_logf and cm_sincosf, in the same order, on each of the P elements (so
+ * every element gets the bits of the scalar function), but interleaved
+ * statement by statement: the P polynomial chains are independent, and the
+ * coefficient table is loaded once for the P elements instead of once per
+ * element. */
+#if defined(__cplusplus) && (defined(__HIPCC__) || defined(__HIP__))
+#define CM_FORP _Pragma("unroll") for (int p = 0; p < P; ++p)
+
+template <int P>
+CM_FN void cm_exp_v(const double *x, double *res) {
+    cm_dtab t = CM_TAB(cm_dtab, cm_exp_tab);
+    int nan[P], hi[P], lo[P];
+    double kf[P], r[P], q[P];
+    CM_FORP {
+        nan[p] = cm_isnan(x[p]);
+        hi[p] = x[p] > 709.782712893384;
+        lo[p] = x[p] < -745.1332191019412;
+        const double xr = (nan[p] || hi[p] || lo[p]) ? 0.0 : x[p];
+        kf[p] = cm_rint_small(xr * t[0]);
+        r[p] = CM_FMA(-kf[p], t[1], xr);
+        r[p] = CM_FMA(-kf[p], t[2], r[p]);
+        q[p] = t[3];
+    }
+    _Pragma("unroll") for (int i = 4; i < 17; i++) CM_FORP q[p] = CM_HORNER(q[p], r[p], t[i]);
+    CM_FORP {
+        const int k = (int)kf[p];
+        const int big = k > 1022, small = k < -1020;
+        const int ka = big ? k - 2 : (small ? k + 1000 : k);
+        double v = q[p] * cm_pow2i(ka);
+        v = big ? v * 4.0 : (small ? v * cm_pow2i(-1000) : v);
+        res[p] = nan[p] ? x[p] : (hi[p] ? CM_INF : (lo[p] ? 0.0 : v));
+    }
+}
+
+template <int P>
+CM_FN void cm_log_v(const double *x, double *res) {
+    double f[P], s[P], z[P], R[P], dk[P];
+    CM_FORP {
+        const int sub = x[p] > 0.0 && x[p] < 2.2250738585072014e-308;
+        const double xs = sub ? x[p] * 18014398509481984.0 : x[p]; /* 2^54 */
+        const uint64_t u = cm_bits(xs);
+        int e = (int)((u >> 52) & 0x7ff) - (sub ? 54 : 0) - 1023;
+        double m = cm_dbl((u & 0x000fffffffffffffULL) | 0x3ff0000000000000ULL);
+        const int up = m > 1.4142135623730951;
+        m = up ? m * 0.5 : m;
+        e = up ? e + 1 : e;
+        f[p] = m - 1.0;
+        s[p] = f[p] / (2.0 + f[p]);
+        z[p] = s[p] * s[p];
+        dk[p] = (double)e;
+    }
+    cm_dtab t = CM_TAB(cm_dtab, cm_log_tab);
+    CM_FORP R[p] = t[0];
+    _Pragma("unroll") for (int i = 1; i < 11; i++) CM_FORP R[p] = CM_HORNER(R[p], z[p], t[i]);
+    CM_FORP {
+        const double Rz = R[p] * z[p];
+        const double hfsq = 0.5 * (f[p] * f[p]);
+        const double v =
+            dk[p] * t[11] - ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[12])) - f[p]);
+        res[p] = cm_isnan(x[p]) ? x[p]
+                 : (x[p] < 0.0 ? CM_NAN : (x[p] == 0.0 ? -CM_INF : (x[p] == CM_INF ? x[p] : v)));
+    }
+}
+
+template <int P>
+CM_FN void cm_sincos_v(const double *x, double *so, double *co) {
+    cm_dtab t = CM_TAB(cm_dtab, cm_trig_tab);
+    int bad[P], q[P];
+    double r[P], z[P], ps[P], pc[P];
+    CM_FORP {
+        const double ax = cm_fabs(x[p]);
+        bad[p] = !(ax < CM_INF);
+        const int huge = !bad[p] && ax >= 1125899906842624.0; /* 2^50 */
+        const double xr = (bad[p] || huge) ? 0.0 : x[p];
+        r[p] = cm_rem_pio2_cw(xr, &q[p], t);
+        if (huge) {
+            int qh;
+            const double rh = cm_rem_pio2_huge(ax, &qh, t);
+            r[p] = x[p] < 0.0 ? -rh : rh;
+            q[p] = (x[p] < 0.0 ? -qh : qh) & 3;
+        }
+        z[p] = r[p] * r[p];
+        ps[p] = t[0];
+        pc[p] = t[8];
+    }
+    _Pragma("unroll") for (int i = 1; i < 8; i++) CM_FORP {
+        ps[p] = CM_HORNER(ps[p], z[p], t[i]);
+        pc[p] = CM_HORNER(pc[p], z[p], t[8 + i]);
+    }
+    CM_FORP {
+        const double sr = CM_FMA(r[p] * z[p], ps[p], r[p]);
+        const double hz = 0.5 * z[p];
+        const double w = 1.0 - hz;
+        const double cr = w + (((1.0 - w) - hz) + z[p] * (z[p] * pc[p]));
+        double sv = (q[p] & 1) ? cr : sr;
+        double cv = (q[p] & 1) ? sr : cr;
+        sv = (q[p] & 2) ? -sv : sv;
+        cv = ((q[p] + 1) & 2) ? -cv : cv;
+        so[p] = bad[p] ? CM_NAN : sv;
+        co[p] = bad[p] ? CM_NAN : cv;
+    }
+}
+
+template <int P>
+CM_FN void cm_expf_v(const float *x, float *res) {
+    cm_ftab t = CM_TAB(cm_ftab, cm_expf_tab);
+    int nan[P], hi[P], lo[P];
+    float kf[P], r[P], q[P];
+    CM_FORP {
+        nan[p] = x[p] != x[p];
+        hi[p] = x[p] > 88.72283f;
+        lo[p] = x[p] < -103.97208f;
+        const float xr = (nan[p] || hi[p] || lo[p]) ? 0.0f : x[p];
+        kf[p] = cm_rint_smallf(xr * t[0]);
+        r[p] = CM_FMAF(-kf[p], t[1], xr);
+        r[p] = CM_FMAF(-kf[p], t[2], r[p]);
+        q[p] = t[3];
+    }
+    _Pragma("unroll") for (int i = 4; i < 11; i++) CM_FORP q[p] = CM_HORNERF(q[p], r[p], t[i]);
+    CM_FORP {
+        const int k = (int)kf[p];
+        const int big = k > 126, small = k < -124;
+        const int ka = big ? k - 2 : (small ? k + 100 : k);
+        float v = q[p] * cm_pow2if(ka);
+        v = big ? v * 4.0f : (small ? v * cm_pow2if(-100) : v);
+        res[p] = nan[p] ? x[p] : (hi[p] ? CM_INFF : (lo[p] ? 0.0f : v));
+    }
+}
+
+template <int P>
+CM_FN void cm_logf_v(const float *x, float *res) {
+    float f[P], s[P], z[P], R[P], dk[P];
+    CM_FORP {
+        const int sub = x[p] > 0.0f && x[p] < 1.17549435e-38f;
+        const float xs = sub ? x[p] * 33554432.0f : x[p]; /* 2^25 */
+        const uint32_t u = cm_bitsf(xs);
+        int e = (int)((u >> 23) & 0xff) - (sub ? 25 : 0) - 127;
+        float m = cm_flt((u & 0x007fffffu) | 0x3f800000u);
+        const int up = m > 1.4142135381698608f;
+        m = up ? m * 0.5f : m;
+        e = up ? e + 1 : e;
+        f[p] = m - 1.0f;
+        s[p] = f[p] / (2.0f + f[p]);
+        z[p] = s[p] * s[p];
+        dk[p] = (float)e;
+    }
+    cm_ftab t = CM_TAB(cm_ftab, cm_logf_tab);
+    CM_FORP R[p] = t[0];
+    _Pragma("unroll") for (int i = 1; i < 6; i++) CM_FORP R[p] = CM_HORNERF(R[p], z[p], t[i]);
+    CM_FORP {
+        const float Rz = R[p] * z[p];
+        const float hfsq = 0.5f * (f[p] * f[p]);
+        const float v = dk[p] * t[6] - ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[7])) - f[p]);
+        res[p] = (x[p] != x[p]) ? x[p]
+                 : (x[p] < 0.0f ? CM_NANF
+                                : (x[p] == 0.0f ? -CM_INFF : (x[p] == CM_INFF ? x[p] : v)));
+    }
+}
+
+template <int P>
+CM_FN void cm_sincosf_v(const float *x, float *so, float *co) {
+    cm_ftab t = CM_TAB(cm_ftab, cm_trigf_tab);
+    int bad[P], q[P];
+    float r[P], z[P], ps[P], pc[P];
+    CM_FORP {
+        const float ax = cm_fabsf(x[p]);
+        bad[p] = !(ax < CM_INFF);
+        const int huge = !bad[p] && ax >= 2097152.0f; /* 2^21 */
+        const float xr = (bad[p] || huge) ? 0.0f : x[p];
+        const float kf = cm_rint_smallf(xr * t[10]);
+        float rr = CM_FMAF(-kf, t[11], xr);
+        rr = CM_FMAF(-kf, t[12], rr);
+        rr = CM_FMAF(-kf, t[13], rr);
+        const float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
+        q[p] = (int)q4;
+        if (huge) {
+            cm_dtab td = CM_TAB(cm_dtab, cm_trig_tab);
+            const double axd = (double)ax;
+            int qh;
+            const double rd = axd >= 1125899906842624.0 ? cm_rem_pio2_huge(axd, &qh, td)
+                                                        : cm_rem_pio2_cw(axd, &qh, td);
+            rr = (float)(x[p] < 0.0f ? -rd : rd);
+            q[p] = (x[p] < 0.0f ? -qh : qh) & 3;
+        }
+        r[p] = rr;
+        z[p] = rr * rr;
+        ps[p] = t[0];
+        pc[p] = t[5];
+    }
+    _Pragma("unroll") for (int i = 1; i < 5; i++) CM_FORP {
+        ps[p] = CM_HORNERF(ps[p], z[p], t[i]);
+        pc[p] = CM_HORNERF(pc[p], z[p], t[5 + i]);
+    }
+    CM_FORP {
+        const float sr = CM_FMAF(r[p] * z[p], ps[p], r[p]);
+        const float hz = 0.5f * z[p];
+        const float w = 1.0f - hz;
+        const float cr = w + (((1.0f - w) - hz) + z[p] * (z[p] * pc[p]));
+        float sv = (q[p] & 1) ? cr : sr;
+        float cv = (q[p] & 1) ? sr : cr;
+        sv = (q[p] & 2) ? -sv : sv;
+        cv = ((q[p] + 1) & 2) ? -cv : cv;
+        so[p] = bad[p] ? CM_NANF : sv;
+        co[p] = bad[p] ? CM_NANF : cv;
+    }
+}
+#undef CM_FORP
+#endif
+
 /* ------------------------------------------------------ hyperbolic, pow */
 
 /* 1/19!, 1/17!, ..., 1/3! */

@@ -161,3 +161,52 @@ def test_kernel_lm_warm_start_reuses_fitted_constants():
     # the cold path ignores the cache
     cold = co_backend.KernelLM(max_iter=50).fit_batch(None, fresh, X, y, native=nat)
     assert np.mean([r.n_iter for r in cold]) > it2
+
+
+class _Skel:
+    """A skeleton with the reference's protocol (n_constants, residual,
+    jacobian) over prefix arrays, scored by the numpy interpreter."""
+
+    def __init__(self, nt, nv, ci):
+        self.nt, self.nv, self.ci = nt, nv, ci
+        self.n_constants = int(np.sum(np.asarray(nt) == 1))
+
+    def residual(self, c, X, y):
+        return interp.eval_tree_arrays(self.nt, self.nv, self.ci, X, np.asarray(c)) - y
+
+
+def test_scipy_lm_fits_through_the_skeleton():
+    nat, inits = _candidates(3, seed=2)
+    rng = np.random.default_rng(5)
+    X = rng.uniform(-2, 2, size=(200, 2))
+    y = 1.5 * X[:, 0] - 0.25
+    skels = [_Skel(*n) for n in nat]
+    res = co_backend.ScipyLM().fit_batch(skels, inits, X, y, max_iter=200)
+    assert np.allclose(res[0].constants, [1.5, -0.25], atol=1e-8) and res[0].converged
+    for r, s in zip(res, skels):
+        assert r.final_loss == pytest.approx(np.mean(s.residual(r.constants, X, y) ** 2))
+    with pytest.raises(ValueError):
+        co_backend.ScipyLM().fit_batch(None, inits, X, y)
+
+
+def test_cuda_kernel_lm_constructor_and_cpu_routing():
+    """The reference constructor (co_backend.py:250-263) and its defaults; a
+    batch of candidates beyond the device bounds goes to the default ScipyLM
+    without touching the device."""
+    lm = co_backend.CudaKernelLM()
+    assert (lm.binary, lm.max_iter, lm.fallback, lm.inproc, lm.device_id) == \
+        (None, 50, None, False, 0)
+    assert co_backend.variant_for_binary(co_backend.DEFAULT_BINARY) == "fd"
+    assert co_backend.variant_for_binary("/x/batch_lm_ad") == "ad"
+    nt = np.asarray([3] * 32 + [1] * 33, np.int32)            # 33 constants
+    big = (nt, np.asarray([1.0] * 32 + [0.0] * 33, np.float32),
+           np.asarray([-1] * 32 + list(range(33)), np.int32))
+    X = np.random.default_rng(1).uniform(-1, 1, size=(50, 2))
+    y = np.full(50, 3.0)
+    res = lm.fit_batch([_Skel(*big)], [np.zeros(33)], X, y, native=[big], max_iter=50)
+    assert lm.last_stats == dict(n_total=1, n_kernel=0, n_fallback=1, n_overflow=1,
+                                 n_kmismatch=0)
+    # y = 3 = c0 * c1 * ... : the fit reaches the target
+    assert res[0].final_loss < 1e-12
+    with pytest.raises(ValueError):
+        lm.fit_batch(None, [], X, y)
