@@ -7,6 +7,7 @@
            [--out JSON --workload-key KEY] [--last]
     python -m cusr_amd.benchmark.prof_summary traffic <fetch.db> <write.db> --kernel NAME
            --calib-fetch-bytes F --calib-write-bytes W [--out JSON --workload-key KEY]
+           [--last]
 
 trace: per kernel, calls and average / min / max / total duration plus the
 register and grid figures of the dispatch. pmc: per kernel, the average of
@@ -122,10 +123,11 @@ def _calib(db, counter):
     return rows[0][2]
 
 
-def traffic(fetch_db, write_db, kernel, calib_fetch, calib_write):
-    """Per kernel whose name contains `kernel`: HBM bytes per dispatch."""
-    f = pmc_per_dispatch(fetch_db, kernel)
-    w = pmc_per_dispatch(write_db, kernel)
+def traffic(fetch_db, write_db, kernel, calib_fetch, calib_write, last=False):
+    """Per kernel whose name contains `kernel`: HBM bytes per dispatch (last:
+    the kernel's last dispatch only, leaving out the calibration call's)."""
+    f = pmc_per_dispatch(fetch_db, kernel, last)
+    w = pmc_per_dispatch(write_db, kernel, last)
     if not f or sorted(f) != sorted(w):
         raise SystemExit(f"kernel {kernel!r} matches {sorted(f)} / {sorted(w)}")
     # FETCH_SIZE and WRITE_SIZE are in KiB per dispatch
@@ -161,8 +163,8 @@ def main():
     ap.add_argument("--take", type=int, default=None,
                     help="trace: then keep TAKE dispatches per kernel")
     ap.add_argument("--last", action="store_true",
-                    help="valu: each kernel's last dispatch only (runs whose earlier "
-                         "dispatches are warm-ups of another shape)")
+                    help="valu, traffic: each kernel's last dispatch only (runs whose "
+                         "earlier dispatches are warm-ups or calibration calls)")
     a = ap.parse_args()
     if a.mode == "trace":
         print(trace(a.dbs[0], a.match, a.skip, a.take))
@@ -175,7 +177,8 @@ def main():
             with open(a.out, "w") as fh:
                 json.dump(t, fh, indent=1)
     else:
-        t = traffic(a.dbs[0], a.dbs[1], a.kernel, a.calib_fetch_bytes, a.calib_write_bytes)
+        t = traffic(a.dbs[0], a.dbs[1], a.kernel, a.calib_fetch_bytes, a.calib_write_bytes,
+                    a.last)
         if a.workload_key:
             t["workload_key"] = a.workload_key
         print(json.dumps(t, indent=1))

@@ -504,7 +504,7 @@ __device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, co
     scale_entries<K, 0, R, P>(T, d, zm, mask, sel ? 1u : 0u);
 }
 
-// T[p*K + k] += v[p] for a wave-uniform k (same branch scheme as scale_range).
+// T[p*K + k] += v[p] for a wave-uniform k, the add in the branch of entry k.
 // The add sits in the asm of its branch: as plain C++ the compiler merges the
 // K branches into one add at a selected address, which puts T in scratch
 // memory. The arithmetic is the IEEE v_add_f64 / v_add_f32 of a plain add.
@@ -519,12 +519,20 @@ template <> struct AddAsm<float> {
         __asm__ volatile("v_add_f32 %0, %0, %1" : "+v"(t) : "v"(v));
     }
 };
+// k is found by halving [0, K): log2(K) uniform tests instead of one per entry.
+template <int K, int LO, int HI, typename R, int P>
+__device__ __forceinline__ void add_tangent_in(R *T, int k, const R *v) {
+    if constexpr (HI - LO == 1) {
+        CUSR_FOR_P AddAsm<R>::run(T[p * K + LO], v[p]);
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        if (k < MID) add_tangent_in<K, LO, MID, R, P>(T, k, v);
+        else add_tangent_in<K, MID, HI, R, P>(T, k, v);
+    }
+}
 template <int K, typename R, int P>
 __device__ __forceinline__ void add_tangent(R *T, int k, const R *v) {
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-        if (j == k) CUSR_FOR_P AddAsm<R>::run(T[p * K + j], v[p]);
-    }
+    if constexpr (K > 0) add_tangent_in<K, 0, K, R, P>(T, k, v);
 }
 
 // Fetch an operand of kind/idx for P points.
