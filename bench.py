@@ -219,6 +219,15 @@ def valu_issue(workload_key, kname_of, bins, device_ms, kdom):
     if not ctr:
         return None
     cyc = 4.0 / (MI355X_SIMDS * MI355X_CLOCK_HZ)
+    if kname_of(kdom).startswith("lm_pass_kernel"):
+        # the split path: a bin is many pass launches and the summary holds one
+        # launch per kernel, so only the per-launch figure is defined
+        dom = next(e for n, e in ctr.items() if kname_of(kdom).rstrip(">") in n)
+        return {"whole_fit_frac": None,
+                "dominant_alone_frac": dom["SQ_ACTIVE_INST_VALU"] * cyc / (dom["alone_ms"] / 1e3),
+                "dominant_alone_ms": dom["alone_ms"], "per": "one pass launch of the bin",
+                "clock_ghz": MI355X_CLOCK_HZ / 1e9, "simds": MI355X_SIMDS,
+                "source": str(_profile(workload_key, "valu").relative_to(REPO))}
     tot, missing = 0.0, []
     for k, v in enumerate(bins):
         if v < 0:

@@ -83,6 +83,18 @@ constexpr int audit_points() {
                : 1;
 }
 
+// Points per elementary-function call in the interpreter (the rest of an
+// operator always runs P-wide): fp64 forward-AD kernels from
+// CUSR_MATH_CHUNK_MIN_K constants on interleave two chains at a time, where
+// four would push the kernel past 256 VGPRs.
+#ifndef CUSR_MATH_CHUNK_MIN_K
+#define CUSR_MATH_CHUNK_MIN_K 7
+#endif
+template <int K, typename R, int P, int JAC>
+constexpr int math_chunk() {
+    return (sizeof(R) == 8 && JAC == 1 && K >= CUSR_MATH_CHUNK_MIN_K && P > 2) ? 2 : P;
+}
+
 // scalar-cache view of the program (constant address space)
 typedef const __attribute__((address_space(4))) uint64_t *ProgPtr;
 
@@ -200,24 +212,28 @@ template <> struct Fn<float> {
 // Value r and derivative d of a unary operator for P points. z[p]: the
 // tangent is zeroed instead of multiplied (a flat branch: derivative exactly
 // 0 by definition, so 0 * inf must not leak a NaN).
-template <typename R, int P>
+// sin, cos, tan, log and exp take the P-wide forms of include/cusr_math.h
+// (the scalar functions' bits, points interleaved), MC points at a time: the
+// kernels whose registers are tight interleave fewer chains.
+#define CUSR_MATH_V(fn, ...) \
+    _Pragma("unroll") for (int c0 = 0; c0 < P; c0 += MC) F::template fn<MC>(__VA_ARGS__)
+template <typename R, int P, int MC = P>
 __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) {
     typedef Fn<R> F;
+    static_assert(P % MC == 0, "math chunks must divide the points per lane");
     const R one = R(1), zero = R(0), two = R(2);
     CUSR_FOR_P z[p] = false;
-    // sin, cos, tan, log and exp take the P-wide forms of include/cusr_math.h
-    // (the scalar functions' bits, the P points interleaved)
     switch (f) {
-    case OP_SIN: F::template sincos_v<P>(a, r, d); break;
+    case OP_SIN: CUSR_MATH_V(sincos_v, a + c0, r + c0, d + c0); break;
     case OP_COS: {
         R s[P];
-        F::template sincos_v<P>(a, s, r);
+        CUSR_MATH_V(sincos_v, a + c0, s + c0, r + c0);
         CUSR_FOR_P d[p] = -s[p];
         break;
     }
     case OP_TAN: {
         R s[P], c[P];
-        F::template sincos_v<P>(a, s, c);
+        CUSR_MATH_V(sincos_v, a + c0, s + c0, c + c0);
         CUSR_FOR_P { r[p] = s[p] / c[p]; d[p] = one + r[p] * r[p]; }
         break;
     }
@@ -225,18 +241,18 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
     case OP_COSH: CUSR_FOR_P { r[p] = F::cosh_(a[p]); d[p] = F::sinh_(a[p]); } break;
     case OP_TANH: CUSR_FOR_P { r[p] = F::tanh_(a[p]); d[p] = one - r[p] * r[p]; } break;
     case OP_LOG:
-        F::template log_v<P>(a, r);
+        CUSR_MATH_V(log_v, a + c0, r + c0);
         CUSR_FOR_P d[p] = one / a[p];
         break;
     case OP_LOOSE_LOG: {
         R aa[P];
         CUSR_FOR_P aa[p] = F::abs_(a[p]);
-        F::template log_v<P>(aa, r);
+        CUSR_MATH_V(log_v, aa + c0, r + c0);
         CUSR_FOR_P d[p] = one / a[p];
         break;
     }
     case OP_EXP:
-        F::template exp_v<P>(a, r);
+        CUSR_MATH_V(exp_v, a + c0, r + c0);
         CUSR_FOR_P d[p] = r[p];
         break;
     case OP_INV: case OP_LOOSE_INV: CUSR_FOR_P { r[p] = one / a[p]; d[p] = -(r[p] * r[p]); } break;
@@ -258,7 +274,7 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
     case OP_CEXP: {
         R xin[P], e[P];
         CUSR_FOR_P xin[p] = (a[p] > R(20)) ? zero : a[p];
-        F::template exp_v<P>(xin, e);
+        CUSR_MATH_V(exp_v, xin + c0, e + c0);
         CUSR_FOR_P {
             const bool flat = a[p] > R(20);
             r[p] = flat ? F::cexp_cap : e[p];
@@ -271,7 +287,7 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
     case OP_PLOG: {
         R t[P];
         CUSR_FOR_P t[p] = F::abs_(a[p]) + F::eps9;
-        F::template log_v<P>(t, r);
+        CUSR_MATH_V(log_v, t + c0, r + c0);
         CUSR_FOR_P {
             const R inv = one / t[p];
             d[p] = (a[p] > zero) ? inv : ((a[p] < zero) ? -inv : zero);
@@ -282,6 +298,8 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
     default: CUSR_FOR_P { r[p] = zero; d[p] = zero; } break;
     }
 }
+
+#undef CUSR_MATH_V
 
 // Value o = l op rv and partials d1 = do/dl, d2 = do/drv for P points.
 // want_d2 false skips log(l) of POW when no constant is on the right.
@@ -499,8 +517,11 @@ __device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, co
     } else {   // hi up to 32: the shift is formed in 64 bits
         mask = (uint32_t)(((uint64_t)1 << hi) - 1u) & ~(uint32_t)(((uint64_t)1 << lo) - 1u);
     }
+    // the flat-branch lane masks are only read by the select rule: no
+    // vector-to-scalar transfer on the other operators' steps
     uint64_t zm[P];
-    CUSR_FOR_P zm[p] = __builtin_amdgcn_ballot_w64(z[p]);
+    CUSR_FOR_P zm[p] = 0;
+    if (sel) CUSR_FOR_P zm[p] = __builtin_amdgcn_ballot_w64(z[p]);
     scale_entries<K, 0, R, P>(T, d, zm, mask, sel ? 1u : 0u);
 }
 
@@ -576,7 +597,7 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
                 if (F::tape_b(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, t + ta, p, lane) = d2[p];
             }
         } else {
-            unary_p<R, P>(fid, a, o, d1, z1);
+            unary_p<R, P, math_chunk<K, R, P, JAC>()>(fid, a, o, d1, z1);
             CUSR_FOR_P { d2[p] = d1[p]; z2[p] = z1[p]; }   // unused: scale_b is never set
             if constexpr (JAC == 2) {
                 if (F::tape_a(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, F::tape(ins), p, lane) = d1[p];

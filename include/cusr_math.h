@@ -524,20 +524,25 @@ CM_FN void cm_log_v(const double *x, double *res) {
 template <int P>
 CM_FN void cm_sincos_v(const double *x, double *so, double *co) {
     cm_dtab t = CM_TAB(cm_dtab, cm_trig_tab);
-    int bad[P], q[P];
+    int bad[P], q[P], huge[P], any_huge = 0;
     double r[P], z[P], ps[P], pc[P];
     CM_FORP {
         const double ax = cm_fabs(x[p]);
         bad[p] = !(ax < CM_INF);
-        const int huge = !bad[p] && ax >= 1125899906842624.0; /* 2^50 */
-        const double xr = (bad[p] || huge) ? 0.0 : x[p];
+        huge[p] = !bad[p] && ax >= 1125899906842624.0; /* 2^50 */
+        any_huge |= huge[p];
+        const double xr = (bad[p] || huge[p]) ? 0.0 : x[p];
         r[p] = cm_rem_pio2_cw(xr, &q[p], t);
-        if (huge) {
+    }
+    if (any_huge) { /* one branch for the P points; the reduction rarely runs */
+        CM_FORP if (huge[p]) {
             int qh;
-            const double rh = cm_rem_pio2_huge(ax, &qh, t);
+            const double rh = cm_rem_pio2_huge(cm_fabs(x[p]), &qh, t);
             r[p] = x[p] < 0.0 ? -rh : rh;
             q[p] = (x[p] < 0.0 ? -qh : qh) & 3;
         }
+    }
+    CM_FORP {
         z[p] = r[p] * r[p];
         ps[p] = t[0];
         pc[p] = t[8];
@@ -619,30 +624,35 @@ CM_FN void cm_logf_v(const float *x, float *res) {
 template <int P>
 CM_FN void cm_sincosf_v(const float *x, float *so, float *co) {
     cm_ftab t = CM_TAB(cm_ftab, cm_trigf_tab);
-    int bad[P], q[P];
+    int bad[P], q[P], huge[P], any_huge = 0;
     float r[P], z[P], ps[P], pc[P];
     CM_FORP {
         const float ax = cm_fabsf(x[p]);
         bad[p] = !(ax < CM_INFF);
-        const int huge = !bad[p] && ax >= 2097152.0f; /* 2^21 */
-        const float xr = (bad[p] || huge) ? 0.0f : x[p];
+        huge[p] = !bad[p] && ax >= 2097152.0f; /* 2^21 */
+        any_huge |= huge[p];
+        const float xr = (bad[p] || huge[p]) ? 0.0f : x[p];
         const float kf = cm_rint_smallf(xr * t[10]);
         float rr = CM_FMAF(-kf, t[11], xr);
         rr = CM_FMAF(-kf, t[12], rr);
         rr = CM_FMAF(-kf, t[13], rr);
         const float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
         q[p] = (int)q4;
-        if (huge) {
-            cm_dtab td = CM_TAB(cm_dtab, cm_trig_tab);
-            const double axd = (double)ax;
+        r[p] = rr;
+    }
+    if (any_huge) { /* one branch for the P points; the reduction rarely runs */
+        cm_dtab td = CM_TAB(cm_dtab, cm_trig_tab);
+        CM_FORP if (huge[p]) {
+            const double axd = (double)cm_fabsf(x[p]);
             int qh;
             const double rd = axd >= 1125899906842624.0 ? cm_rem_pio2_huge(axd, &qh, td)
                                                         : cm_rem_pio2_cw(axd, &qh, td);
-            rr = (float)(x[p] < 0.0f ? -rd : rd);
+            r[p] = (float)(x[p] < 0.0f ? -rd : rd);
             q[p] = (x[p] < 0.0f ? -qh : qh) & 3;
         }
-        r[p] = rr;
-        z[p] = rr * rr;
+    }
+    CM_FORP {
+        z[p] = r[p] * r[p];
         ps[p] = t[0];
         pc[p] = t[5];
     }
