@@ -64,3 +64,52 @@ def test_quality_run_end_to_end(tmp_path):
     print(runner.report_markdown(res), flush=True)
     assert g["tier_b_rate"] >= 0.9 and g["selection_fidelity"]["spearman"] > 0.9
     assert res["noise_floor"]["n"] > 0
+
+
+def _harness_run(pop, label, c_true=None, nproc=16, repeats=3):
+    """run_quality with the GPU (fp64 in process, the CLI) and the scipy port,
+    against the serial scipy oracle cached by population hash."""
+    import os
+    from pathlib import Path
+    from oracle.scipy_pop import ScipyPop
+
+    serial = ScipyPop(nproc=1, timeout=300)
+    try:
+        cache = Path(os.environ.get("GRAFT_REPO_ROOT", ".")) / "gpurun_out" / "oracle_cache"
+        orc = runner.cached_oracle(pop, lambda p: serial.fit_pop(p)["c_final"],
+                                   lambda c: interp.loss_pop(pop, c), cache)
+    finally:
+        serial.close()
+    par = _Scipy(min(nproc, len(os.sched_getaffinity(0))))
+    try:
+        res = runner.run_quality(
+            pop, {"mi355x:fp64": backends.KernelPop(max_iter=50),
+                  "mi355x:cli-fp32": backends.CudaKernelPop(max_iter=50), "scipy": par},
+            orc["loss_star"], lambda c: interp.loss_pop(pop, c), repeats=repeats,
+            c_true=c_true, label=label)
+    finally:
+        par.sp.close()
+    print(f"\n[harness] oracle wall {orc['wall']:.1f} s (cached: {orc['cached']})\n"
+          + runner.report_markdown(res), flush=True)
+    return res
+
+
+@pytest.mark.gpu
+def test_quality_pop1000_reference_forest():
+    """The harness on the reference's real 1,000-tree forest (N = 1,000)."""
+    from tests.helpers import ref_pop
+    res = _harness_run(ref_pop("pop1000.bin"), "pop1000")
+    g = res["backends"]["mi355x:fp64"]
+    assert g["selection_fidelity"]["spearman"] > 0.9
+    assert g["tier_b_rate"] >= 0.8
+
+
+@pytest.mark.gpu
+def test_quality_c2_sample_with_noise_floor():
+    """The harness on 2,048 expressions of the C2 configuration, with the noise
+    floor of the true constants."""
+    pop, c_true = synth("C2", 2048)
+    res = _harness_run(pop, "C2-2048", c_true=c_true)
+    g = res["backends"]["mi355x:fp64"]
+    assert g["selection_fidelity"]["spearman"] > 0.8
+    assert res["noise_floor"]["n"] > 0
