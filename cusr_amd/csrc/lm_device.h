@@ -56,11 +56,12 @@ constexpr float kCexpCap32 = 485165184.0f;         // exp(20) rounded to float
 #define CUSR_PREV_TABLE 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
 // fp64 forward AD from kLargeN points on (C4's N = 100,000): each pass streams
-// y from memory, and two points per lane with three waves per SIMD at K = 5, 6
-// hide the loads better (C4 -6 %; at N = 1,024 four points measured faster).
-// Points per pass do not change any summation order.
+// y from memory, and two points per lane with three waves per SIMD hide the
+// loads better (C4 on the split path: 187 -> 179.5 ms with every K = 1..8 so,
+// against K = 5, 6 only; at N = 1,024 four points measured faster). Points per
+// pass do not change any summation order.
 #ifndef CUSR_P64_LARGE_N_TABLE
-#define CUSR_P64_LARGE_N_TABLE 4, 4, 4, 4, 4, 2, 2, 4, 4, 1, 1, 1, 1, 1, 1, 1, 1
+#define CUSR_P64_LARGE_N_TABLE 2, 2, 2, 2, 2, 2, 2, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
 constexpr int kLargeN = 16384;
 constexpr int kP64[CO_FAST_MAX_K + 1] = {CUSR_P64_TABLE};
@@ -1487,7 +1488,7 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
 #define CUSR_WREV64_TABLE 1, 1, 1, 1, 1, 1, 1, 1, 1, 2, 1, 1, 1, 1, 1, 1, 1
 #endif
 #ifndef CUSR_W64_LARGE_N_TABLE
-#define CUSR_W64_LARGE_N_TABLE 1, 1, 1, 2, 2, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1
+#define CUSR_W64_LARGE_N_TABLE 1, 3, 3, 3, 3, 3, 3, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
 #ifndef CUSR_WAVES_OTHER
 #define CUSR_WAVES_OTHER 1
