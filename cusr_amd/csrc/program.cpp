@@ -274,9 +274,10 @@ static void chunked(int M, int nthreads, const Fn &fn, const Redo &redo) {
     bool done = false;
     if (nthreads > 1) {
         std::vector<std::thread> pool;
+        const int chunk = (M + nthreads - 1) / nthreads;
         try {
-            const int chunk = (M + nthreads - 1) / nthreads;
-            for (int i = 0; i < nthreads; i++) {
+            // chunks 1.. on new threads, chunk 0 on this one
+            for (int i = 1; i < nthreads; i++) {
                 const int m0 = i * chunk, m1 = std::min(M, m0 + chunk);
                 if (m0 < m1) pool.emplace_back(std::cref(fn), m0, m1);
             }
@@ -284,6 +285,7 @@ static void chunked(int M, int nthreads, const Fn &fn, const Redo &redo) {
         } catch (...) {
             // no more threads
         }
+        if (done) fn(0, std::min(M, chunk));
         for (std::thread &th : pool) th.join();
     }
     if (!done) redo(0, M);
@@ -324,19 +326,24 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
     std::vector<int64_t> cost(descs ? M : 0);
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
     const int nthreads = (int)std::min<int64_t>(std::min(16u, hw), nsum / 65536 + 1);
-    // phase 1: check every expression, its stack depth and so its kernel
-    auto check_range = [&](int m0, int m1) {
-        TreeScratch s;
+    // phase 1: every expression's stack depth and so its kernel, by a count
+    // over the node types (the depth check_tree finds for a valid tree); the
+    // full check runs in phase 2, which still ends before anything is used
+    auto depth_range = [&](int m0, int m1) {
         for (int m = m0; m < m1; m++) {
             const TreeMeta &t = metas[m];
-            rcs[m] = check_tree(nt + t.node_offset, nv + t.node_offset, ci + t.node_offset,
-                                t.n_nodes, t.K, D, &depth[m], s);
+            const int32_t *tnt = nt + t.node_offset;
+            int sp = 0, dmax = 0;
+            for (int i = t.n_nodes - 1; i >= 0; i--) {
+                if (tnt[i] == NODE_BFUNC) sp -= 1;          // two operands in, one out
+                else if (tnt[i] != NODE_UFUNC) sp += 1;     // a leaf
+                if (sp > dmax) dmax = sp;
+            }
+            depth[m] = dmax;
             gen[m] = co_fast_path(t.K, depth[m], t.n_nodes, D) ? 0 : 1;
         }
     };
-    chunked(M, nthreads, check_range, check_range);
-    for (int m = 0; m < M; m++)
-        if (rcs[m] != CO_OK) return rcs[m];
+    chunked(M, nthreads, depth_range, depth_range);
     // programs are laid out expression after expression: n_nodes words in the
     // fast format, 2 * n_nodes in the wide one (node_offset order would let
     // overlapping metas alias each other's instructions)
@@ -361,6 +368,7 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
             if (words > 0) memset(out, 0, sizeof(uint64_t) * words);
             int dd = 0;
             rcs[m] = check_tree(tnt, tnv, tci, t.n_nodes, t.K, D, &dd, s);
+            if (rcs[m] == CO_OK && dd != depth[m]) rcs[m] = CO_ERR_PROGRAM;   // never, for a valid tree
             if (rcs[m] == CO_OK)
                 rcs[m] = emit_tree(tnt, tnv, tci, t.n_nodes, D, gen[m] ? kMaxSlotsWide : kMaxSlots,
                                    &tapes[m], &slots[m], s);
