@@ -113,3 +113,47 @@ def test_quality_c2_sample_with_noise_floor():
     g = res["backends"]["mi355x:fp64"]
     assert g["selection_fidelity"]["spearman"] > 0.8
     assert res["noise_floor"]["n"] > 0
+
+
+def test_cached_oracle_hits_by_population_hash(tmp_path):
+    """The serial oracle is cached by (population sha1, limit): a second call
+    on the same population reads the cache, any changed input misses it
+    (cusr/benchmark/runner.py:111-128)."""
+    pop, _ = synth("C1", 8, 32)
+    calls = []
+
+    def fit(p):
+        calls.append(p["M"])
+        return np.asarray(p["c_init"], np.float64) * 2.0
+
+    def score(c):
+        return np.asarray(c, np.float64) + 1.0
+
+    a = runner.cached_oracle(pop, fit, score, tmp_path)
+    b = runner.cached_oracle(pop, fit, score, tmp_path)
+    assert calls == [8] and not a["cached"] and b["cached"]
+    assert np.array_equal(a["c_star"], b["c_star"]) and np.array_equal(a["loss_star"], b["loss_star"])
+    other = dict(pop)
+    other["c_init"] = np.asarray(pop["c_init"]) + np.float32(1)
+    assert runner.pop_sha(other) != runner.pop_sha(pop)
+    runner.cached_oracle(other, fit, score, tmp_path)
+    assert calls == [8, 8]
+    c = runner.cached_oracle(pop, fit, score, tmp_path, limit=4)
+    assert not c["cached"] and calls == [8, 8, 4] and len(c["c_star"]) == int(
+        np.sum(pop["metas"][:4, 3]))
+
+
+def test_bench_host_description_and_launch_bins():
+    """bench.py's CPU-baseline host record and the launch bin of every
+    expression (the fast kernel of its K, or the general kernel)."""
+    import bench
+    from cusr_amd.kernel import co_inproc as ci
+    from tests.general_pops import general_pop
+    cores, host = bench.cpu_cores()
+    assert 1 <= cores <= host["affinity_cores"] and host["numpy"] and host["scipy"]
+    pop, _ = general_pop("mixed", 24, 64)
+    b = bench.launch_bins(pop)
+    K = pop["metas"][:, 3]
+    gen = b == ci.CO_GENERAL_BIN
+    assert gen.any() and (~gen).any()
+    assert np.array_equal(b[~gen], K[~gen]) and np.all(K[gen] > ci.CO_FAST_MAX_K)
