@@ -115,10 +115,16 @@ struct Operand {
     int producer;  // instruction that produced an ACC value, else -1
 };
 
+struct Visit {
+    int node;   // subtree root (prefix index)
+    int stage;  // 0: nothing evaluated, 1: first operand done, 2: both done
+};
+
 struct TreeScratch {
-    std::vector<int> size, left, cc;
+    std::vector<int> size, left, cc, need;
     std::vector<int> depth_stack;
-    std::vector<Operand> opd;
+    std::vector<Operand> res;
+    std::vector<Visit> work;
     std::vector<Ins> ins;
 };
 
@@ -179,30 +185,73 @@ static int check_tree(const int32_t *nt, const float *nv, const int32_t *ci, int
 // Emit the instructions of a checked expression into s.ins in execution
 // order. max_slots: slots the target format can address. Returns CO_OK,
 // CO_ERR_BOUNDS or CO_ERR_PROGRAM; sets the tape and spill-slot counts.
+//
+// Operands are evaluated in Sethi-Ullman order: when both operands of a binary
+// operator need instructions, the one whose subtree needs more spill slots runs
+// first (the right one on a tie, as the reference's last-node-first order
+// does) and its value waits in a slot while the other runs. A subtree's value
+// and its constants' tangents and adjoints do not depend on which sibling runs
+// first, and the order keeps the slot count at the minimum (at most
+// log2(nodes + 1)), which is what sizes each wavefront's LDS.
 static int emit_tree(const int32_t *nt, const float *nv, const int32_t *ci, int n, int D,
                      int max_slots_fmt, int *tape_slots, int *slots_used, TreeScratch &s) {
-    s.opd.clear();
     s.ins.clear();
-    int tape = 0, live_slots = 0, max_slots = 0;
+    auto leaf = [&](int i) { return nt[i] == NODE_VAR || nt[i] == NODE_CONST; };
+    // need[i]: spill slots the subtree at node i needs in this order (children
+    // follow their parent in prefix order, so a descending pass sees them first)
+    s.need.assign(n, 0);
     for (int i = n - 1; i >= 0; i--) {
+        if (nt[i] == NODE_UFUNC) {
+            s.need[i] = s.need[i + 1];
+        } else if (nt[i] == NODE_BFUNC) {
+            const int l = i + 1, r = i + 1 + s.left[i];
+            const int nl = s.need[l], nr = s.need[r];
+            const int hi = nl > nr ? nl : nr;
+            s.need[i] = (!leaf(l) && !leaf(r) && nl == nr) ? nl + 1 : hi;
+        }
+    }
+    s.res.assign(n, Operand{OPD_ACC, 0, -1});
+    s.work.clear();
+    s.work.push_back({0, 0});
+    int tape = 0, live_slots = 0, max_slots = 0;
+    while (!s.work.empty()) {
+        const int i = s.work.back().node, stage = s.work.back().stage;
         const int t = nt[i];
-        if (t == NODE_VAR) {
-            s.opd.push_back({OPD_VAR, node_int(nv[i], D), -1});
+        if (t == NODE_VAR || t == NODE_CONST) {
+            s.res[i] = t == NODE_VAR ? Operand{OPD_VAR, node_int(nv[i], D), -1}
+                                     : Operand{OPD_CONST, ci[i], -1};
+            s.work.pop_back();
             continue;
         }
-        if (t == NODE_CONST) {
-            s.opd.push_back({OPD_CONST, ci[i], -1});
-            continue;
-        }
-        const int f = (int)nv[i];
         const bool bin = (t == NODE_BFUNC);
-        const Operand a = s.opd.back();
-        s.opd.pop_back();
-        Operand b = {OPD_ACC, 0, -1};
-        if (bin) {
-            b = s.opd.back();
-            s.opd.pop_back();
+        const int l = i + 1, r = bin ? i + 1 + s.left[i] : -1;
+        const bool both = bin && !leaf(l) && !leaf(r);
+        const int first = (!bin || (both && s.need[l] > s.need[r])) ? l : r;
+        const int second = !bin ? -1 : (first == l ? r : l);
+        if (stage == 0) {
+            s.work.back().stage = 1;
+            s.work.push_back({first, 0});
+            continue;
         }
+        if (stage == 1 && bin) {
+            s.work.back().stage = 2;
+            if (both) {
+                // the first operand's value waits in the next free slot
+                if (live_slots >= max_slots_fmt) return CO_ERR_BOUNDS;
+                const int slot = live_slots++;
+                if (live_slots > max_slots) max_slots = live_slots;
+                Operand &o = s.res[first];
+                if (o.kind != OPD_ACC || o.producer < 0) return CO_ERR_PROGRAM;
+                s.ins[o.producer].toslot = 1;
+                s.ins[o.producer].di = slot;
+                o = {OPD_SLOT, slot, -1};
+            }
+            s.work.push_back({second, 0});
+            continue;
+        }
+        s.work.pop_back();
+        const Operand a = s.res[l];
+        const Operand b = bin ? s.res[r] : Operand{OPD_ACC, 0, -1};
         // spill slots are used last in, first out
         if (a.kind == OPD_SLOT) {
             if (a.idx != live_slots - 1) return CO_ERR_PROGRAM;
@@ -212,21 +261,8 @@ static int emit_tree(const int32_t *nt, const float *nv, const int32_t *ci, int 
             if (b.idx != live_slots - 1) return CO_ERR_PROGRAM;
             live_slots--;
         }
-        // this instruction overwrites ACC: an ACC value still waiting on the
-        // operand stack (at most one) moves to the next free slot instead
-        for (Operand &o : s.opd) {
-            if (o.kind != OPD_ACC) continue;
-            if (live_slots >= max_slots_fmt) return CO_ERR_BOUNDS;
-            const int slot = live_slots++;
-            if (live_slots > max_slots) max_slots = live_slots;
-            s.ins[o.producer].toslot = 1;
-            s.ins[o.producer].di = slot;
-            o.kind = OPD_SLOT;
-            o.idx = slot;
-            o.producer = -1;
-        }
         Ins w = {};
-        w.fid = f;
+        w.fid = (int)nv[i];
         w.bin = bin ? 1 : 0;
         w.ak = a.kind;
         w.ai = a.idx;
@@ -240,16 +276,16 @@ static int emit_tree(const int32_t *nt, const float *nv, const int32_t *ci, int 
         w.tape = tape;
         set_flags(w);
         // reverse-AD tape slots only for partials that are read and not exactly +-1
-        const bool unit = bin && (f == OP_ADD || f == OP_SUB);
+        const bool unit = bin && (w.fid == OP_ADD || w.fid == OP_SUB);
         w.ta = a.kind != OPD_VAR && !unit;
         w.tb = bin && b.kind != OPD_VAR && !unit;
         tape += (w.ta ? 1 : 0) + (w.tb ? 1 : 0);
-        s.opd.push_back({OPD_ACC, 0, (int)s.ins.size()});
+        s.res[i] = {OPD_ACC, 0, (int)s.ins.size()};
         s.ins.push_back(w);
     }
     if (s.ins.empty()) {
         // the expression is one leaf: its value is the identity of that leaf
-        const Operand a = s.opd.back();
+        const Operand a = s.res[0];
         Ins w = {};
         w.fid = OP_IDENT;
         w.ak = a.kind;

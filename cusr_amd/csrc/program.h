@@ -2,13 +2,17 @@
 // the device interpreter.
 //
 // An expression (pop.bin nt/nv/ci, cusr/kernel/pop_format.h:6-16, prefix
-// order) is evaluated last node first (cusr/kernel/lm_core.cuh:67). In that
-// order the left operand of every operator is produced immediately before the
-// operator itself, so the decoded program is a list of operator instructions
-// over three kinds of operand:
+// order) is a tree the reference evaluates last node first
+// (cusr/kernel/lm_core.cuh:67), right operand before left. Here each operator
+// runs after its operands, and when both operands need instructions the one
+// whose subtree needs more spill slots runs first (Sethi-Ullman order; the
+// right one on a tie): values, tangents and adjoints do not depend on which
+// sibling runs first, and the spill slots (the LDS a wavefront reserves) stay
+// at the tree's minimum. The decoded program is a list of operator
+// instructions over three kinds of operand:
 //   ACC   the running value, i.e. the result of the previous instruction;
-//   SLOT  a spill slot holding a right operand computed before a left subtree
-//         that itself needed instructions (slots are used last-in first-out);
+//   SLOT  a spill slot holding the operand computed first while the other
+//         operand's instructions run (slots are used last-in first-out);
 //   VAR / CONST  a leaf, folded into the instruction that consumes it.
 // Leaves therefore cost no instruction; an expression that is a single leaf
 // becomes one OP_IDENT instruction.

@@ -140,6 +140,80 @@ def test_stack_depth_and_k_bins(idx):
     assert orc_rc == 0 and np.array_equal(orc_stack, stack)
 
 
+def sethi_ullman(nt):
+    """Fewest spill slots an accumulator machine needs for the prefix tree nt
+    when each binary operator may run either operand first: a leaf needs no
+    instruction; two operands that both need instructions hold one value in a
+    slot while the other runs, so equal needs cost one more slot."""
+    def walk(i):
+        t = nt[i]
+        if t <= 1:
+            return 0, 1, True
+        if t == 2:
+            need, size, _ = walk(i + 1)
+            return need, size + 1, False
+        nl, sl, ll = walk(i + 1)
+        nr, sr, lr = walk(i + 1 + sl)
+        if not ll and not lr:
+            need = nl + 1 if nl == nr else max(nl, nr)
+        else:
+            need = max(nl, nr)
+        return need, sl + sr + 1, False
+    return walk(0)[0]
+
+
+def live_slots(ins):
+    """Most spill slots a program holds at once (operands freed before the
+    result is stored)."""
+    live = peak = 0
+    for f in ins:
+        live -= (f["ak"] == 3) + (f["bin"] and f["bk"] == 3)
+        assert live >= 0
+        if f["ts"]:
+            live += 1
+            peak = max(peak, live)
+    assert live == 0
+    return peak
+
+
+@pytest.mark.parametrize("idx", range(9))
+def test_spill_slots_are_minimal(idx):
+    """Operands run in Sethi-Ullman order: every program holds no more spill
+    slots at once than the tree's minimum (the LDS each wavefront reserves)."""
+    pop = _pops()[idx]
+    rc, prog, order, bins, stack = ci.decode(pop)
+    assert rc == 0
+    off = 0
+    for m in range(pop["M"]):
+        o, n, _, _ = (int(v) for v in pop["metas"][m])
+        ins = instructions(prog, off, n, False)
+        assert live_slots(ins) == sethi_ullman(pop["nt"][o:o + n].tolist())
+        off += n
+
+
+def test_sethi_ullman_order_cases():
+    """Hand-made trees: two leaf pairs need one slot in either order; a full
+    tree of depth 3 needs 2; when the left operand needs more slots it runs
+    first, so the tree needs 1 where the right-first order needs 2."""
+    pair = [3, 0, 0]                       # x0 + x0
+    two_pairs = [3] + pair + pair          # (x0 + x0) + (x0 + x0): 1 slot in either order
+    full = [3] + two_pairs + two_pairs     # full depth-3 tree: 2 slots
+    lean = [3] + two_pairs + pair          # right operand first would hold 2
+    trees = [(t, [1.0 if x == 3 else 0.0 for x in t], [-1] * len(t), np.zeros(0))
+             for t in (two_pairs, full, lean)]
+    pop = popio.build_pop(trees, np.zeros((4, 1)), np.zeros((3, 4)))
+    rc, prog, order, bins, stack = ci.decode(pop)
+    assert rc == 0
+    got = []
+    off = 0
+    for m in range(pop["M"]):
+        o, n, _, _ = (int(v) for v in pop["metas"][m])
+        got.append(live_slots(instructions(prog, off, n, False)))
+        off += n
+    assert got == [1, 2, 1]
+    assert [sethi_ullman(t[0]) for t in trees] == [1, 2, 1]
+
+
 # flat-branch operators (the select rule): MAX, MIN, LT, GT, LE, GE, PDIV, CEXP
 SELECT_OPS = {8, 9, 10, 11, 12, 13, 32, 33}
 
