@@ -93,6 +93,7 @@ struct HostBuf {
 // (C2: 20.5 ms, the sum of the two streams' bins). So four streams in all.
 constexpr int kExtraStreams = 3;
 constexpr int kStreams = kExtraStreams + 1;
+constexpr int kMaxRanges = 2;   // launch ranges of one fit (the upload pipeline's two)
 
 // launchers per (precision, AD mode) come from fit_kernels.hip, each variant
 // in its own translation unit so the four compile in parallel
@@ -120,10 +121,14 @@ struct Ctx {
     hipEvent_t ev_start = nullptr;
     hipEvent_t ev_done[kExtraStreams] = {};
     hipEvent_t ev_t0 = nullptr, ev_t1 = nullptr;  // timing pair around the fit launches
-    hipEvent_t ev_b0[CO_BINS] = {}, ev_b1[CO_BINS] = {};  // per bin launch
-    bool bin_launched[CO_BINS] = {};
+    // per bin and launch range (a pipelined co_optimize launches each bin once
+    // per range): a bin's time is the sum of its launches' durations
+    hipEvent_t ev_b0[kMaxRanges][CO_BINS] = {}, ev_b1[kMaxRanges][CO_BINS] = {};
+    bool bin_launched[kMaxRanges][CO_BINS] = {};
     Plan plan = {};
     bool resident = false;
+    std::vector<int> ranges;   // launch-order ranges of the resident descriptors: [r[i], r[i+1])
+    hipStream_t copy_stream = nullptr;   // uploads of a pipelined co_optimize
     bool shared_y = false;   // the resident y is one row for every expression
     bool on_data = false;    // the resident population fits the uploaded data set
     int data_N = -1, data_D = 0;  // shape of the uploaded data set (-1: none)
@@ -240,36 +245,13 @@ size_t fit_lds_bytes(bool mixed, bool rev, int K, int N, int D, int slots, int t
                : lds_for_k<double, CO_AD_FORWARD>(K, N, D, slots, tape);
 }
 
-// Check, decode and upload one population into the context (fp32 or fp64
-// host inputs); the population stays resident until the next upload.
-// With on_data, xs and ym are unused: the population fits the data set of
-// co_data_upload, whose shape must match the header's.
-int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const float *nv,
-                      const int32_t *ci, const TreeMeta *metas, const void *c, const void *xs,
-                      const void *ym, bool in32, bool on_data = false) {
-    CO_HIP(hipSetDevice(ctx->device));
-    ctx->resident = false;
-    const int M = h->M_prob;
-    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1);
-    CO_GROW_HOST(ctx->h_desc, M > 0 ? (size_t)M : 1);
-    int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
-                               ctx->h_desc.data(), nullptr, nullptr, nullptr, nullptr,
-                               &ctx->plan);
-    if (rc != CO_OK) return rc;
-    if (on_data && (ctx->data_N < 0 || h->N != ctx->data_N || h->n_vars != ctx->data_D))
-        return CO_ERR_DATA;
-    ctx->on_data = on_data;
-    if (M == 0) {
-        ctx->resident = true;
-        return CO_OK;
-    }
-    const int N = h->N, D = h->n_vars, C = h->total_c;
-    const bool shared_y = on_data || (pop_flags(h) & POP_FLAG_SHARED_Y) != 0;
-    // the data set's X and y stay in their own buffers
+// Device buffers of a population of M expressions with `words` program words.
+int grow_buffers(Ctx *ctx, const PopHeader *h, size_t words, bool in32, bool on_data,
+                 bool shared_y) {
+    const int M = h->M_prob, N = h->N, D = h->n_vars, C = h->total_c;
     const size_t nX = on_data ? 0 : (size_t)N * D;
     const size_t nY = on_data ? 0 : shared_y ? (size_t)N : (size_t)M * N;
     const size_t esz = in32 ? 4 : 8;
-    const size_t words = (size_t)ctx->plan.words;
     CO_GROW(ctx->prog, sizeof(uint64_t) * words);
     CO_GROW(ctx->desc, sizeof(ExprDesc) * M);
     CO_GROW(ctx->X, sizeof(double) * nX);
@@ -284,13 +266,17 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
     if (in32 && esz * nY > stage) stage = esz * nY;
     if (in32 && esz * C > stage) stage = esz * C;
     CO_GROW(ctx->stage, stage);
-    hipStream_t s = ctx->stream;
+    return CO_OK;
+}
 
-    if (words)
-        CO_HIP(hipMemcpyAsync(ctx->prog.p, ctx->h_prog.data(), sizeof(uint64_t) * words,
-                              hipMemcpyHostToDevice, s));
-    CO_HIP(hipMemcpyAsync(ctx->desc.p, ctx->h_desc.data(), sizeof(ExprDesc) * M,
-                          hipMemcpyHostToDevice, s));
+// Queue the copies of the data (X, y) and c_init on stream s (fp32 host
+// inputs are widened on the device). With on_data only c_init goes over.
+int upload_data(Ctx *ctx, const PopHeader *h, const void *c, const void *xs, const void *ym,
+                bool in32, bool on_data, bool shared_y, hipStream_t s) {
+    const int M = h->M_prob, N = h->N, D = h->n_vars, C = h->total_c;
+    const size_t nX = on_data ? 0 : (size_t)N * D;
+    const size_t nY = on_data ? 0 : shared_y ? (size_t)N : (size_t)M * N;
+    const size_t esz = in32 ? 4 : 8;
     // xs: row-major host array -> column-major fp64 on the device
     if (nX) {
         CO_HIP(hipMemcpyAsync(ctx->stage.p, xs, esz * nX, hipMemcpyHostToDevice, s));
@@ -319,6 +305,45 @@ int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const flo
         if (nY) CO_HIP(hipMemcpyAsync(ctx->Y.p, ym, 8 * nY, hipMemcpyHostToDevice, s));
         if (C) CO_HIP(hipMemcpyAsync(ctx->C0.p, c, 8 * (size_t)C, hipMemcpyHostToDevice, s));
     }
+    return CO_OK;
+}
+
+// Check, decode and upload one population into the context (fp32 or fp64
+// host inputs); the population stays resident until the next upload.
+// With on_data, xs and ym are unused: the population fits the data set of
+// co_data_upload, whose shape must match the header's.
+int upload_population(Ctx *ctx, const PopHeader *h, const int32_t *nt, const float *nv,
+                      const int32_t *ci, const TreeMeta *metas, const void *c, const void *xs,
+                      const void *ym, bool in32, bool on_data = false) {
+    CO_HIP(hipSetDevice(ctx->device));
+    ctx->resident = false;
+    const int M = h->M_prob;
+    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1);
+    CO_GROW_HOST(ctx->h_desc, M > 0 ? (size_t)M : 1);
+    int rc = decode_population(h, nt, nv, ci, metas, ctx->h_prog.data(), nullptr, nullptr,
+                               ctx->h_desc.data(), nullptr, nullptr, nullptr, nullptr,
+                               &ctx->plan);
+    if (rc != CO_OK) return rc;
+    if (on_data && (ctx->data_N < 0 || h->N != ctx->data_N || h->n_vars != ctx->data_D))
+        return CO_ERR_DATA;
+    ctx->on_data = on_data;
+    ctx->ranges.assign({0, M});
+    if (M == 0) {
+        ctx->resident = true;
+        return CO_OK;
+    }
+    const bool shared_y = on_data || (pop_flags(h) & POP_FLAG_SHARED_Y) != 0;
+    const size_t words = (size_t)ctx->plan.words;
+    rc = grow_buffers(ctx, h, words, in32, on_data, shared_y);
+    if (rc != CO_OK) return rc;
+    hipStream_t s = ctx->stream;
+    if (words)
+        CO_HIP(hipMemcpyAsync(ctx->prog.p, ctx->h_prog.data(), sizeof(uint64_t) * words,
+                              hipMemcpyHostToDevice, s));
+    CO_HIP(hipMemcpyAsync(ctx->desc.p, ctx->h_desc.data(), sizeof(ExprDesc) * M,
+                          hipMemcpyHostToDevice, s));
+    rc = upload_data(ctx, h, c, xs, ym, in32, on_data, shared_y, s);
+    if (rc != CO_OK) return rc;
     CO_HIP(hipStreamSynchronize(s));
     ctx->shared_y = shared_y;
     ctx->resident = true;
@@ -334,238 +359,474 @@ struct LaunchPlan {
     size_t lds[2];
 };
 
+typedef hipError_t (*Launcher)(int, unsigned, size_t, hipStream_t, const FitArgs &);
+
+// The launches of one fit, planned and issued range by range. The
+// descriptors of a range are in launch order (decode_population /
+// decode_range): a population decoded in several ranges has its bins planned
+// range by range.
+struct FitRun {
+    struct Segment {
+        int parts, it_end, resume;
+    };
+    Ctx *ctx = nullptr;
+    CoOptions opt = {};
+    FitArgs fa = {};
+    bool rev = false, mixed = false, split = false, started = false;
+    int parts = 0, nseg = 1, pwidth = 0;
+    Segment seg[2] = {};
+    bool lane_used[kExtraStreams] = {};
+    int range = 0;   // ranges issued so far
+    Launcher launch = nullptr, launch_pass = nullptr;
+
+    // Option checks and the fit's arguments (ctx->plan holds N, D, M, C).
+    int begin(Ctx *c, const CoOptions &o) {
+        ctx = c;
+        opt = o;
+        if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
+        if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED)
+            return CO_ERR_NULLARG;
+        if (opt.max_iter < 0) return CO_ERR_NULLARG;
+        if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
+            return CO_ERR_NULLARG;
+        if (opt.tail_iter < -1 || (opt.tail_partitions != 0 && opt.tail_partitions != 1 &&
+                                   opt.tail_partitions != 2 && opt.tail_partitions != 4))
+            return CO_ERR_NULLARG;
+        CO_HIP(hipSetDevice(ctx->device));
+        const Plan &plan = ctx->plan;
+        ctx->last_kernel_ms = 0.0;
+        for (int k = 0; k < CO_BINS; ++k) {
+            for (int r = 0; r < kMaxRanges; ++r) ctx->bin_launched[r][k] = false;
+            ctx->last_bin_ms[k] = -1.0;
+        }
+        parts = co_partitions_resolve(&opt, plan.N);
+        if (parts == 0) return CO_ERR_NULLARG;
+        split = parts > CO_MAX_PARTITIONS;
+        fa.prog = ptr<uint64_t>(ctx->prog);
+        fa.desc = ptr<ExprDesc>(ctx->desc);
+        fa.X = ptr<double>(ctx->on_data ? ctx->data_X : ctx->X);
+        fa.Y = ptr<double>(ctx->on_data ? ctx->data_Y : ctx->Y);
+        fa.C0 = ptr<double>(ctx->C0);
+        fa.C = ptr<double>(ctx->C);
+        fa.status = ptr<int32_t>(ctx->status);
+        fa.loss_init = ptr<double>(ctx->li);
+        fa.loss_final = ptr<double>(ctx->lf);
+        fa.iters = ptr<int32_t>(ctx->iters);
+        fa.N = plan.N;
+        fa.D = plan.D;
+        fa.max_iter = opt.max_iter;
+        fa.guard = opt.fp64_guard ? 1 : 0;
+        fa.shared_y = ctx->shared_y ? 1 : 0;
+        fa.f32_range = opt.f32_range ? 1 : 0;
+        fa.lm_order = opt.lm_order;
+        fa.lambda0 = opt.lambda0;
+        fa.xtol = opt.xtol;
+        fa.psum = nullptr;
+        fa.psum_width = 0;
+        fa.state = nullptr;
+        fa.state_stride = 0;
+        rev = opt.ad_mode == CO_AD_REVERSE;
+        mixed = opt.precision == CO_PREC_MIXED;
+        // segments of the iteration loop: all expressions up to tail_it, then the
+        // ones still running with tail_parts partitions (one launch each per bin)
+        int tail_parts = parts;
+        const int tail_it = co_tail_resolve(&opt, plan.N, &tail_parts);
+        seg[0] = {parts, opt.max_iter, 0};
+        nseg = 1;
+        if (tail_it > 0) {
+            seg[0].it_end = tail_it;
+            seg[1] = {tail_parts, opt.max_iter, 1};
+            nseg = 2;
+        }
+        launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
+                       : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
+        launch_pass = mixed ? (rev ? launch_pass_f32_rev : launch_pass_f32_fwd)
+                            : (rev ? launch_pass_f64_rev : launch_pass_f64_fwd);
+        return CO_OK;
+    }
+
+    // The bins of descriptors [p0, p1) in launch order: the general kernel's
+    // bin, then the fast K bins, largest K first. The streams are dealt
+    // round-robin in that order (stream kExtraStreams is the handle's own).
+    // The kernel launched first on a stream takes the machine first and so
+    // ends first, so each stream's next bin is the next largest; this beats
+    // balancing estimated costs over the streams (C2 12.15 -> 11.66 ms, C4
+    // 173 -> 170 ms, C3 139.7 -> 137.8 ms on an MI355X).
+    int plan_range(int p0, int p1, LaunchPlan *lp, int *nl_out, int *kmax_out) const {
+        const Plan &plan = ctx->plan;
+        int nl = 0, kmax = 0, pos = p0;
+        for (int i = 0; i < CO_BINS; ++i) {
+            const int bin = i == 0 ? CO_GENERAL_BIN : CO_FAST_MAX_K - (i - 1);
+            const bool gen = bin == CO_GENERAL_BIN;
+            LaunchPlan b = {};
+            b.bin = bin;
+            b.pos = pos;
+            while (pos < p1 && (gen ? ctx->h_desc[pos].gen != 0
+                                    : (!ctx->h_desc[pos].gen && ctx->h_desc[pos].K == bin))) {
+                const ExprDesc &d = ctx->h_desc[pos];
+                if (d.slots > b.slots) b.slots = d.slots;
+                if (d.tape > b.tape) b.tape = d.tape;
+                if (d.K > b.kmax) b.kmax = d.K;
+                ++b.cnt;
+                ++pos;
+            }
+            if (b.cnt == 0) continue;
+            if (!rev) b.tape = 0;
+            if (b.kmax > kmax) kmax = b.kmax;
+            b.stream = nl % kStreams;
+            // per-wavefront areas, then the partition sums; fewer wavefronts per
+            // workgroup (each summing several partitions) when LDS is short. The
+            // split path's pass workgroups are one wavefront with no partition
+            // sums in LDS.
+            b.wave_bytes =
+                (fit_lds_bytes(mixed, rev, bin, plan.N, plan.D, b.slots, b.tape) + 15) &
+                ~(size_t)15;
+            const size_t cap = max_dyn_lds(ctx, gen);
+            const int ks = gen ? b.kmax : bin;
+            for (int g = 0; g < (b.kmax == 0 || split ? 1 : nseg); ++g) {
+                const int sp = split ? 1 : seg[g].parts;
+                const size_t part_bytes = sp > 1 ? (size_t)sp * sums_width(ks) * 8 : 0;
+                int pw = sp;
+                while (pw > 1 && pw * b.wave_bytes + part_bytes > cap) pw /= 2;
+                b.pwaves[g] = pw;
+                b.lds[g] = pw * b.wave_bytes + part_bytes;
+                if (b.lds[g] > cap) return CO_ERR_BOUNDS;   // before any launch
+            }
+            lp[nl++] = b;
+        }
+        if (pos != p1) return CO_ERR_PROGRAM;   // descriptors out of launch order: never
+        *nl_out = nl;
+        *kmax_out = kmax;
+        return CO_OK;
+    }
+
+    // Scratch of the whole fit: loop-state rows by expression, then the split
+    // path's partition sums by launch position (null sc: the handle's buffer,
+    // grown as needed; a fixed region that is too small refuses the fit).
+    int set_scratch(int kmax, const Scratch *sc) {
+        const int M = ctx->plan.M;
+        int tail_parts = parts;
+        const int tail_it = co_tail_resolve(&opt, ctx->plan.N, &tail_parts);
+        const int stride = split ? kSplitStride : state_stride_for(kmax);
+        pwidth = sums_width(kmax);
+        const size_t state_bytes =
+            (split || tail_it > 0) ? (((sizeof(double) * stride * (size_t)M) + 255) & ~(size_t)255)
+                                   : 0;
+        const size_t psum_bytes = split ? sizeof(double) * (size_t)parts * pwidth * M : 0;
+        Scratch own;
+        if (!sc) {
+            if (state_bytes + psum_bytes) CO_GROW(ctx->state, state_bytes + psum_bytes);
+            own.p = ctx->state.p;
+            own.cap = ctx->state.cap;
+            sc = &own;
+        } else if (state_bytes + psum_bytes > sc->cap) {
+            return CO_ERR_BOUNDS;   // a fixed region is never grown
+        }
+        fa.state = state_bytes ? (double *)sc->p : nullptr;
+        fa.state_stride = stride;
+        if (split) {
+            fa.psum = (double *)((char *)sc->p + state_bytes);
+            fa.psum_width = pwidth;
+        }
+        return CO_OK;
+    }
+
+    // After the first launch an error must not return with work still running
+    // on the streams: they are joined first.
+    int join_all() {
+        for (int i = 0; i < kExtraStreams; ++i)
+            if (lane_used[i]) (void)hipStreamSynchronize(ctx->lanes[i]);
+        (void)hipStreamSynchronize(ctx->stream);
+        return CO_OK;
+    }
+    int fail(hipError_t e, int line) {
+        fprintf(stderr, "[cusr_co] HIP error %s at %s:%d\n", hipGetErrorString(e), __FILE__,
+                line);
+        join_all();
+        return CO_ERR_CUDA;
+    }
+
+#define CO_LAUNCH_HIP(call)                              \
+    do {                                                 \
+        hipError_t e_ = (call);                          \
+        if (e_ != hipSuccess) return fail(e_, __LINE__); \
+    } while (0)
+
+    // Issue the planned launches of one range (its inputs already on the device).
+    int issue(const LaunchPlan *lp, int nl) {
+        const hipStream_t s = ctx->stream;
+        const int M = ctx->plan.M;
+        if (range >= kMaxRanges) return CO_ERR_BOUNDS;   // never: at most kMaxRanges ranges
+        if (!started) {
+            CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t0, s));
+            if (split) {
+                // every expression starts with a pass at c_init pending
+                FitArgs fi = fa;
+                lm_split_init_kernel<<<M, kLanes, 0, s>>>(fi);
+                CO_LAUNCH_HIP(hipGetLastError());
+            }
+            CO_LAUNCH_HIP(hipEventRecord(ctx->ev_start, s));
+            started = true;
+        }
+        // the split path's (pass, step) rounds: the pass at c_init, one per
+        // iteration, two fp64 audit passes for mixed precision
+        const int rounds = 1 + opt.max_iter + (mixed ? 2 : 0);
+        for (int i = 0; i < nl; ++i) {
+            const LaunchPlan &b = lp[i];
+            hipStream_t ks = b.stream < kExtraStreams ? ctx->lanes[b.stream] : s;
+            if (b.stream < kExtraStreams && !lane_used[b.stream]) {
+                lane_used[b.stream] = true;
+                CO_LAUNCH_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
+            }
+            CO_LAUNCH_HIP(hipEventRecord(ctx->ev_b0[range][b.bin], ks));
+            if (split) {
+                FitArgs fk = fa;
+                fk.desc = fa.desc + b.pos;
+                fk.psum = fa.psum + (size_t)b.pos * parts * pwidth;
+                fk.slots = b.slots;
+                fk.tape = b.tape;
+                fk.parts = parts;
+                fk.pwaves = 1;
+                fk.wave_bytes = (int)b.wave_bytes;
+                fk.it_end = opt.max_iter;
+                fk.resume = 0;
+                for (int r = 0; r < rounds; ++r) {
+                    CO_LAUNCH_HIP(launch_pass(b.bin, (unsigned)b.cnt * parts, b.lds[0], ks, fk));
+                    lm_step_kernel<<<b.cnt, kLanes, 0, ks>>>(fk, mixed ? 1 : 0);
+                    CO_LAUNCH_HIP(hipGetLastError());
+                }
+            } else {
+                // K = 0 expressions have no iterations, so no tail either
+                for (int g = 0; g < (b.kmax == 0 ? 1 : nseg); ++g) {
+                    FitArgs fk = fa;
+                    fk.desc = fa.desc + b.pos;
+                    fk.slots = b.slots;
+                    fk.tape = b.tape;
+                    fk.parts = seg[g].parts;
+                    fk.pwaves = b.pwaves[g];
+                    fk.wave_bytes = (int)b.wave_bytes;
+                    fk.it_end = seg[g].it_end;
+                    fk.resume = seg[g].resume;
+                    CO_LAUNCH_HIP(launch(b.bin, (unsigned)b.cnt, b.lds[g], ks, fk));
+                }
+            }
+            CO_LAUNCH_HIP(hipEventRecord(ctx->ev_b1[range][b.bin], ks));
+            ctx->bin_launched[range][b.bin] = true;
+        }
+        ++range;
+        return CO_OK;
+    }
+
+    // Join the streams, copy results to the host pointers that are non-null
+    // (results otherwise stay on the device) and record the timings. Returns
+    // after the device work and copies are complete.
+    int finish(double *c_out, int32_t *status_out, double *li_out, double *lf_out,
+               int32_t *iters_out) {
+        const hipStream_t s = ctx->stream;
+        const int M = ctx->plan.M, C = ctx->plan.total_c;
+        for (int i = 0; i < kExtraStreams; ++i) {
+            if (!lane_used[i]) continue;
+            CO_LAUNCH_HIP(hipEventRecord(ctx->ev_done[i], ctx->lanes[i]));
+            CO_LAUNCH_HIP(hipStreamWaitEvent(s, ctx->ev_done[i], 0));
+        }
+        CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t1, s));
+        if (c_out && C)
+            CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, hipMemcpyDeviceToHost, s));
+        if (status_out)
+            CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M,
+                                  hipMemcpyDeviceToHost, s));
+        if (li_out)
+            CO_HIP(hipMemcpyAsync(li_out, ctx->li.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
+        if (lf_out)
+            CO_HIP(hipMemcpyAsync(lf_out, ctx->lf.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
+        if (iters_out)
+            CO_HIP(hipMemcpyAsync(iters_out, ctx->iters.p, 4 * (size_t)M,
+                                  hipMemcpyDeviceToHost, s));
+        CO_HIP(hipStreamSynchronize(s));
+        float ms = 0.0f;
+        CO_HIP(hipEventElapsedTime(&ms, ctx->ev_t0, ctx->ev_t1));
+        ctx->last_kernel_ms = ms;
+        for (int k = 0; k < CO_BINS; ++k) {
+            double sum = -1.0;
+            for (int r = 0; r < kMaxRanges; ++r) {
+                if (!ctx->bin_launched[r][k]) continue;
+                CO_HIP(hipEventElapsedTime(&ms, ctx->ev_b0[r][k], ctx->ev_b1[r][k]));
+                sum = (sum < 0.0 ? 0.0 : sum) + ms;
+            }
+            ctx->last_bin_ms[k] = sum;
+        }
+        return CO_OK;
+    }
+#undef CO_LAUNCH_HIP
+};
+
 // Fit the resident population; copy results to the host pointers that are
 // non-null (c_out and status_out too may be null: results then stay on the
 // device). sc: where the fit's scratch goes (null: the handle's buffer, grown
 // as needed; a fixed region is never grown, and a fit that needs more is
-// refused with CO_ERR_BOUNDS before anything is launched). Returns after the
-// device work and copies are complete.
+// refused with CO_ERR_BOUNDS before anything is launched). Every range's
+// launches are planned before the first is issued. Returns after the device
+// work and copies are complete.
 int run_fit(Ctx *ctx, const CoOptions &opt, double *c_out, int32_t *status_out, double *li_out,
             double *lf_out, int32_t *iters_out, const Scratch *sc = nullptr) {
     if (!ctx->resident) return CO_ERR_NULLARG;
-    if (opt.ad_mode != CO_AD_FORWARD && opt.ad_mode != CO_AD_REVERSE) return CO_ERR_NULLARG;
-    if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
-    if (opt.max_iter < 0) return CO_ERR_NULLARG;
-    if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
-        return CO_ERR_NULLARG;
-    if (opt.tail_iter < -1 || (opt.tail_partitions != 0 && opt.tail_partitions != 1 &&
-                               opt.tail_partitions != 2 && opt.tail_partitions != 4))
-        return CO_ERR_NULLARG;
-    CO_HIP(hipSetDevice(ctx->device));
-    const Plan &plan = ctx->plan;
-    const int M = plan.M, C = plan.total_c;
-    ctx->last_kernel_ms = 0.0;
-    for (int k = 0; k < CO_BINS; ++k) {
-        ctx->bin_launched[k] = false;
-        ctx->last_bin_ms[k] = -1.0;
+    FitRun fr;
+    int rc = fr.begin(ctx, opt);
+    if (rc != CO_OK) return rc;
+    if (ctx->plan.M == 0) return CO_OK;
+    const int nr = (int)ctx->ranges.size() - 1;
+    std::vector<LaunchPlan> lp((size_t)nr * CO_BINS);
+    std::vector<int> nl(nr, 0);
+    int kmax = 0;
+    for (int r = 0; r < nr; ++r) {
+        int km = 0;
+        rc = fr.plan_range(ctx->ranges[r], ctx->ranges[r + 1], lp.data() + (size_t)r * CO_BINS,
+                           &nl[r], &km);
+        if (rc != CO_OK) return rc;
+        if (km > kmax) kmax = km;
     }
-    const int parts = co_partitions_resolve(&opt, plan.N);
-    if (parts == 0) return CO_ERR_NULLARG;
-    if (M == 0) return CO_OK;
-    const bool split = parts > CO_MAX_PARTITIONS;
-    hipStream_t s = ctx->stream;
-    FitArgs fa;
-    fa.prog = ptr<uint64_t>(ctx->prog);
-    fa.desc = ptr<ExprDesc>(ctx->desc);
-    fa.X = ptr<double>(ctx->on_data ? ctx->data_X : ctx->X);
-    fa.Y = ptr<double>(ctx->on_data ? ctx->data_Y : ctx->Y);
-    fa.C0 = ptr<double>(ctx->C0);
-    fa.C = ptr<double>(ctx->C);
-    fa.status = ptr<int32_t>(ctx->status);
-    fa.loss_init = ptr<double>(ctx->li);
-    fa.loss_final = ptr<double>(ctx->lf);
-    fa.iters = ptr<int32_t>(ctx->iters);
-    fa.N = plan.N;
-    fa.D = plan.D;
-    fa.max_iter = opt.max_iter;
-    fa.guard = opt.fp64_guard ? 1 : 0;
-    fa.shared_y = ctx->shared_y ? 1 : 0;
-    fa.f32_range = opt.f32_range ? 1 : 0;
-    fa.lm_order = opt.lm_order;
-    fa.lambda0 = opt.lambda0;
-    fa.xtol = opt.xtol;
-    fa.psum = nullptr;
-    fa.psum_width = 0;
-    const bool rev = opt.ad_mode == CO_AD_REVERSE;
-    const bool mixed = opt.precision == CO_PREC_MIXED;
-    // segments of the iteration loop: all expressions up to tail_it, then the
-    // ones still running with tail_parts partitions (one launch each per bin)
+    rc = fr.set_scratch(kmax, sc);
+    if (rc != CO_OK) return rc;
+    for (int r = 0; r < nr; ++r) {
+        rc = fr.issue(lp.data() + (size_t)r * CO_BINS, nl[r]);
+        if (rc != CO_OK) return rc;
+    }
+    return fr.finish(c_out, status_out, li_out, lf_out, iters_out);
+}
+
+// A population uploaded from host buffers of at least 2 kPipeMinRange
+// expressions is decoded, uploaded and launched in two ranges: the first, an
+// eighth of the population (at least kPipeMinRange expressions), is decoded
+// alone, and while the device fits it the host decodes the rest. (The host
+// decode of C5's 65,536 expressions, 1.7 M nodes, takes about 5 ms of a 41 ms
+// round. Measured on an MI355X, C5 rounds: one piece 41.1 ms, two ranges
+// 38.1 ms, three growing ranges 38.2 ms, four equal ranges 38.6 ms, eight
+// 40.5 ms: each range's bins are launches of their own, and more of them
+// lengthen the fit's tail.)
+constexpr int kPipeMinRange = 8192;
+
+// Ranges a co_optimize of this population is decoded in (1: one piece).
+int pipe_ranges(const CoOptions &opt, const PopHeader *h) {
+    if (!h || h->M_prob < 2 * kPipeMinRange) return 1;
+    const int parts = co_partitions_resolve(&opt, h->N);
     int tail_parts = parts;
-    const int tail_it = co_tail_resolve(&opt, plan.N, &tail_parts);
-    struct Segment { int parts, it_end, resume; } seg[2] = {{parts, opt.max_iter, 0}, {}};
-    int nseg = 1;
-    if (tail_it > 0) {
-        seg[0].it_end = tail_it;
-        seg[1] = {tail_parts, opt.max_iter, 1};
-        nseg = 2;
+    // the split path and the tail segments size their scratch over the whole
+    // population: those fits take the one-piece path
+    if (parts == 0 || parts > CO_MAX_PARTITIONS || co_tail_resolve(&opt, h->N, &tail_parts) > 0)
+        return 1;
+    return 2;
+}
+
+// End of range j of the nr ranges of M expressions.
+int range_end(int M, int j, int nr) {
+    if (j + 1 >= nr) return M;
+    return M / 8 > kPipeMinRange ? M / 8 : kPipeMinRange;
+}
+
+// co_optimize in ranges: X, y and c_init go over first, then each range is
+// decoded, copied (on the handle's copy stream, waited for by the host) and
+// launched while the host decodes the next. Same checks, results and
+// error codes as upload_population + run_fit; a range that fails to decode
+// after earlier ones were launched returns its code once they are done, with
+// no output written. setup_ms: host time to the first launch.
+int fit_pipelined(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t *nt,
+                  const float *nv, const int32_t *ci, const TreeMeta *metas, const void *c,
+                  const void *xs, const void *ym, bool in32, double *c_out, int32_t *status_out,
+                  double *li_out, double *lf_out, int32_t *iters_out, bool on_data, int nr,
+                  double t0, double *setup_ms) {
+    CO_HIP(hipSetDevice(ctx->device));
+    ctx->resident = false;
+    int rc = check_header(h, nt, nv, ci, metas);
+    if (rc != CO_OK) return rc;
+    if (on_data && (ctx->data_N < 0 || h->N != ctx->data_N || h->n_vars != ctx->data_D))
+        return CO_ERR_DATA;
+    const int M = h->M_prob;
+    const bool shared_y = on_data || (pop_flags(h) & POP_FLAG_SHARED_Y) != 0;
+    CO_GROW_HOST(ctx->h_prog, h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1);
+    CO_GROW_HOST(ctx->h_desc, (size_t)M);
+    rc = grow_buffers(ctx, h, h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1, in32, on_data,
+                      shared_y);
+    if (rc != CO_OK) return rc;
+    ctx->on_data = on_data;
+    ctx->shared_y = shared_y;
+    Plan &pl = ctx->plan;
+    pl = Plan{};
+    pl.M = M;
+    pl.N = h->N;
+    pl.D = h->n_vars;
+    pl.total_nodes = h->total_nodes;
+    pl.total_c = h->total_c;
+    FitRun fr;
+    rc = fr.begin(ctx, opt);
+    if (rc != CO_OK) return rc;
+    const hipStream_t cs = ctx->copy_stream;
+    rc = upload_data(ctx, h, c, xs, ym, in32, on_data, shared_y, cs);
+    if (rc != CO_OK) {
+        (void)hipStreamSynchronize(cs);
+        return rc;
     }
-    // bins in launch order (descriptors are in launch order): the general
-    // kernel's bin, then the fast K bins, largest K first; the streams are
-    // dealt round-robin in that order (stream kExtraStreams is the handle's
-    // own). The kernel launched first on a stream takes the machine first and
-    // so ends first, so each stream's next bin is the next largest; this beats
-    // balancing estimated costs over the streams (C2 12.15 -> 11.66 ms, C4
-    // 173 -> 170 ms, C3 139.7 -> 137.8 ms on an MI355X).
-    LaunchPlan lp[CO_BINS];
-    int nl = 0, kmax = 0;
-    for (int i = 0, pos = 0; i < CO_BINS; ++i) {
-        const int bin = i == 0 ? CO_GENERAL_BIN : CO_FAST_MAX_K - (i - 1);
-        const bool gen = bin == CO_GENERAL_BIN;
-        LaunchPlan b = {};
-        b.bin = bin;
-        b.pos = pos;
-        while (pos < M && (gen ? ctx->h_desc[pos].gen != 0
-                               : (!ctx->h_desc[pos].gen && ctx->h_desc[pos].K == bin))) {
-            const ExprDesc &d = ctx->h_desc[pos];
-            if (d.slots > b.slots) b.slots = d.slots;
-            if (d.tape > b.tape) b.tape = d.tape;
-            if (d.K > b.kmax) b.kmax = d.K;
-            ++b.cnt;
-            ++pos;
+    ctx->ranges.assign(1, 0);
+    int64_t wb = 0;
+    for (int j = 0; j < nr; ++j) {
+        const int m0 = j == 0 ? 0 : range_end(M, j - 1, nr), m1 = range_end(M, j, nr);
+        Plan rp = {};
+#ifdef CUSR_EXP_TIMING
+        const double q0 = now_ms();
+#endif
+        rc = decode_range(h, nt, nv, ci, metas, m0, m1, wb, ctx->h_prog.data(),
+                          ctx->h_desc.data(), &rp);
+#ifdef CUSR_EXP_TIMING
+        const double q1 = now_ms();
+#endif
+        LaunchPlan lp[CO_BINS];
+        int nl = 0, km = 0;
+        if (rc == CO_OK) rc = fr.plan_range(m0, m1, lp, &nl, &km);
+        hipError_t e = hipSuccess;
+        if (rc == CO_OK && rp.words)
+            e = hipMemcpyAsync((char *)ctx->prog.p + sizeof(uint64_t) * wb, ctx->h_prog.data() + wb,
+                               sizeof(uint64_t) * rp.words, hipMemcpyHostToDevice, cs);
+        if (rc == CO_OK && e == hipSuccess)
+            e = hipMemcpyAsync((char *)ctx->desc.p + sizeof(ExprDesc) * m0, ctx->h_desc.data() + m0,
+                               sizeof(ExprDesc) * (m1 - m0), hipMemcpyHostToDevice, cs);
+        // the host waits for the range's copies (tens of microseconds): an event
+        // the streams waited on would be signalled through a hardware queue
+        // that a fitting stream shares, after that stream's earlier kernels
+        if (rc == CO_OK && e == hipSuccess) e = hipStreamSynchronize(cs);
+        if (e != hipSuccess) {
+            fprintf(stderr, "[cusr_co] HIP error %s at %s:%d\n", hipGetErrorString(e), __FILE__,
+                    __LINE__);
+            rc = CO_ERR_CUDA;
         }
-        if (b.cnt == 0) continue;
-        if (!rev) b.tape = 0;
-        if (b.kmax > kmax) kmax = b.kmax;
-        b.stream = nl % kStreams;
-        // per-wavefront areas, then the partition sums; fewer wavefronts per
-        // workgroup (each summing several partitions) when LDS is short. The
-        // split path's pass workgroups are one wavefront with no partition
-        // sums in LDS.
-        b.wave_bytes =
-            (fit_lds_bytes(mixed, rev, bin, plan.N, plan.D, b.slots, b.tape) + 15) & ~(size_t)15;
-        const size_t cap = max_dyn_lds(ctx, gen);
-        const int ks = gen ? b.kmax : bin;
-        for (int g = 0; g < (b.kmax == 0 || split ? 1 : nseg); ++g) {
-            const int sp = split ? 1 : seg[g].parts;
-            const size_t part_bytes = sp > 1 ? (size_t)sp * sums_width(ks) * 8 : 0;
-            int pw = sp;
-            while (pw > 1 && pw * b.wave_bytes + part_bytes > cap) pw /= 2;
-            b.pwaves[g] = pw;
-            b.lds[g] = pw * b.wave_bytes + part_bytes;
-            if (b.lds[g] > cap) return CO_ERR_BOUNDS;   // before any launch
+        if (rc != CO_OK) {
+            fr.join_all();
+            (void)hipStreamSynchronize(cs);
+            return rc;
         }
-        lp[nl++] = b;
-    }
-    // scratch: loop-state rows by expression, then the split path's partition
-    // sums by launch position
-    const int stride = split ? kSplitStride : state_stride_for(kmax);
-    const int pwidth = sums_width(kmax);
-    const size_t state_bytes =
-        (split || tail_it > 0) ? (((sizeof(double) * stride * (size_t)M) + 255) & ~(size_t)255) : 0;
-    const size_t psum_bytes = split ? sizeof(double) * (size_t)parts * pwidth * M : 0;
-    Scratch own;
-    if (!sc) {
-        if (state_bytes + psum_bytes) CO_GROW(ctx->state, state_bytes + psum_bytes);
-        own.p = ctx->state.p;
-        own.cap = ctx->state.cap;
-        sc = &own;
-    } else if (state_bytes + psum_bytes > sc->cap) {
-        return CO_ERR_BOUNDS;   // a fixed region is never grown
-    }
-    fa.state = state_bytes ? (double *)sc->p : nullptr;
-    fa.state_stride = stride;
-    if (split) {
-        fa.psum = (double *)((char *)sc->p + state_bytes);
-        fa.psum_width = pwidth;
-    }
-    typedef hipError_t (*Launcher)(int, unsigned, size_t, hipStream_t, const FitArgs &);
-    const Launcher launch = mixed ? (rev ? launch_fit_f32_rev : launch_fit_f32_fwd)
-                                  : (rev ? launch_fit_f64_rev : launch_fit_f64_fwd);
-    const Launcher launch_pass = mixed ? (rev ? launch_pass_f32_rev : launch_pass_f32_fwd)
-                                       : (rev ? launch_pass_f64_rev : launch_pass_f64_fwd);
-    bool lane_used[kExtraStreams] = {};
-    // after the first launch an error must not return with work still running
-    // on the lanes: they are joined first
-    auto fail = [&](hipError_t e, int line) {
-        fprintf(stderr, "[cusr_co] HIP error %s at %s:%d\n", hipGetErrorString(e), __FILE__,
-                line);
-        for (int i = 0; i < kExtraStreams; ++i)
-            if (lane_used[i]) (void)hipStreamSynchronize(ctx->lanes[i]);
-        (void)hipStreamSynchronize(s);
-        return CO_ERR_CUDA;
-    };
-#define CO_LAUNCH_HIP(call)                          \
-    do {                                             \
-        hipError_t e_ = (call);                      \
-        if (e_ != hipSuccess) return fail(e_, __LINE__); \
-    } while (0)
-    CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t0, s));
-    if (split) {
-        // every expression starts with a pass at c_init pending
-        FitArgs fi = fa;
-        lm_split_init_kernel<<<M, kLanes, 0, s>>>(fi);
-        CO_LAUNCH_HIP(hipGetLastError());
-    }
-    CO_LAUNCH_HIP(hipEventRecord(ctx->ev_start, s));
-    // the split path's (pass, step) rounds: the pass at c_init, one per
-    // iteration, two fp64 audit passes for mixed precision
-    const int rounds = 1 + opt.max_iter + (mixed ? 2 : 0);
-    for (int i = 0; i < nl; ++i) {
-        const LaunchPlan &b = lp[i];
-        hipStream_t ks = b.stream < kExtraStreams ? ctx->lanes[b.stream] : s;
-        if (b.stream < kExtraStreams && !lane_used[b.stream]) {
-            lane_used[b.stream] = true;
-            CO_LAUNCH_HIP(hipStreamWaitEvent(ks, ctx->ev_start, 0));
+#ifdef CUSR_EXP_TIMING
+        const double q2 = now_ms();
+#endif
+        rc = fr.issue(lp, nl);
+#ifdef CUSR_EXP_TIMING
+        fprintf(stderr, "[pipe] range %d at %.2f: decode %.2f copies %.2f issue %.2f ms\n", j,
+                q0 - t0, q1 - q0, q2 - q1, now_ms() - q2);
+#endif
+        if (rc != CO_OK) {
+            (void)hipStreamSynchronize(cs);
+            return rc;
         }
-        CO_LAUNCH_HIP(hipEventRecord(ctx->ev_b0[b.bin], ks));
-        if (split) {
-            FitArgs fk = fa;
-            fk.desc = fa.desc + b.pos;
-            fk.psum = fa.psum + (size_t)b.pos * parts * pwidth;
-            fk.slots = b.slots;
-            fk.tape = b.tape;
-            fk.parts = parts;
-            fk.pwaves = 1;
-            fk.wave_bytes = (int)b.wave_bytes;
-            fk.it_end = opt.max_iter;
-            fk.resume = 0;
-            for (int r = 0; r < rounds; ++r) {
-                CO_LAUNCH_HIP(launch_pass(b.bin, (unsigned)b.cnt * parts, b.lds[0], ks, fk));
-                lm_step_kernel<<<b.cnt, kLanes, 0, ks>>>(fk, mixed ? 1 : 0);
-                CO_LAUNCH_HIP(hipGetLastError());
-            }
-        } else {
-            // K = 0 expressions have no iterations, so no tail either
-            for (int g = 0; g < (b.kmax == 0 ? 1 : nseg); ++g) {
-                FitArgs fk = fa;
-                fk.desc = fa.desc + b.pos;
-                fk.slots = b.slots;
-                fk.tape = b.tape;
-                fk.parts = seg[g].parts;
-                fk.pwaves = b.pwaves[g];
-                fk.wave_bytes = (int)b.wave_bytes;
-                fk.it_end = seg[g].it_end;
-                fk.resume = seg[g].resume;
-                CO_LAUNCH_HIP(launch(b.bin, (unsigned)b.cnt, b.lds[g], ks, fk));
-            }
-        }
-        CO_LAUNCH_HIP(hipEventRecord(ctx->ev_b1[b.bin], ks));
-        ctx->bin_launched[b.bin] = true;
+        if (j == 0) *setup_ms = now_ms() - t0;
+        wb += rp.words;
+        pl.n_gen += rp.n_gen;
+        if (rp.max_tape > pl.max_tape) pl.max_tape = rp.max_tape;
+        if (rp.max_n > pl.max_n) pl.max_n = rp.max_n;
+        if (rp.max_slots > pl.max_slots) pl.max_slots = rp.max_slots;
+        ctx->ranges.push_back(m1);
     }
-    for (int i = 0; i < kExtraStreams; ++i) {
-        if (!lane_used[i]) continue;
-        CO_LAUNCH_HIP(hipEventRecord(ctx->ev_done[i], ctx->lanes[i]));
-        CO_LAUNCH_HIP(hipStreamWaitEvent(s, ctx->ev_done[i], 0));
-    }
-    CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t1, s));
-#undef CO_LAUNCH_HIP
-    if (c_out && C) CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, hipMemcpyDeviceToHost, s));
-    if (status_out)
-        CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M, hipMemcpyDeviceToHost, s));
-    if (li_out) CO_HIP(hipMemcpyAsync(li_out, ctx->li.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
-    if (lf_out) CO_HIP(hipMemcpyAsync(lf_out, ctx->lf.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
-    if (iters_out)
-        CO_HIP(hipMemcpyAsync(iters_out, ctx->iters.p, 4 * (size_t)M, hipMemcpyDeviceToHost, s));
-    CO_HIP(hipStreamSynchronize(s));
-    float ms = 0.0f;
-    CO_HIP(hipEventElapsedTime(&ms, ctx->ev_t0, ctx->ev_t1));
-    ctx->last_kernel_ms = ms;
-    for (int k = 0; k < CO_BINS; ++k) {
-        if (!ctx->bin_launched[k]) continue;
-        CO_HIP(hipEventElapsedTime(&ms, ctx->ev_b0[k], ctx->ev_b1[k]));
-        ctx->last_bin_ms[k] = ms;
-    }
-    return CO_OK;
+    pl.words = wb;
+    rc = fr.finish(c_out, status_out, li_out, lf_out, iters_out);
+    CO_HIP(hipStreamSynchronize(cs));
+    if (rc == CO_OK) ctx->resident = true;
+    return rc;
 }
 
 // Shared body of co_optimize / co_optimize_ex: upload, fit, read back.
@@ -579,6 +840,16 @@ int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t
     if (opt.max_iter < 0) return CO_ERR_NULLARG;
     if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
         return CO_ERR_NULLARG;
+    const int nr = pipe_ranges(opt, h);
+    if (nr > 1) {
+        double setup = 0.0;
+        const int rc = fit_pipelined(ctx, opt, h, nt, nv, ci, metas, c, xs, ym, in32, c_out,
+                                     status_out, li_out, lf_out, iters_out, on_data, nr, t0,
+                                     &setup);
+        g_setup_ms = setup;
+        g_loop_ms = now_ms() - t0 - setup;
+        return rc;
+    }
     int rc = upload_population(ctx, h, nt, nv, ci, metas, c, xs, ym, in32, on_data);
     if (rc != CO_OK) return rc;
     const double t1 = now_ms();
@@ -639,12 +910,15 @@ extern "C" int co_init(int device_id, void **handle_out) {
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     for (int i = 0; i < kExtraStreams && e == hipSuccess; ++i)
         e = hipStreamCreateWithFlags(&ctx->lanes[i], hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t0);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_t1);
     for (int k = 0; k < CO_BINS && e == hipSuccess; ++k) {
-        e = hipEventCreate(&ctx->ev_b0[k]);
-        if (e == hipSuccess) e = hipEventCreate(&ctx->ev_b1[k]);
+        for (int r = 0; r < kMaxRanges && e == hipSuccess; ++r) {
+            e = hipEventCreate(&ctx->ev_b0[r][k]);
+            if (e == hipSuccess) e = hipEventCreate(&ctx->ev_b1[r][k]);
+        }
     }
     for (int i = 0; i < kExtraStreams && e == hipSuccess; ++i)
         e = hipEventCreateWithFlags(&ctx->ev_done[i], hipEventDisableTiming);
@@ -986,6 +1260,7 @@ extern "C" void co_teardown(void *handle) {
     if (ctx->h_prog.p) (void)hipHostFree(ctx->h_prog.p);
     if (ctx->h_desc.p) (void)hipHostFree(ctx->h_desc.p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    if (ctx->copy_stream) (void)hipStreamDestroy(ctx->copy_stream);
     for (int i = 0; i < kExtraStreams; ++i) {
         if (ctx->lanes[i]) (void)hipStreamDestroy(ctx->lanes[i]);
         if (ctx->ev_done[i]) (void)hipEventDestroy(ctx->ev_done[i]);
@@ -994,8 +1269,10 @@ extern "C" void co_teardown(void *handle) {
     if (ctx->ev_t0) (void)hipEventDestroy(ctx->ev_t0);
     if (ctx->ev_t1) (void)hipEventDestroy(ctx->ev_t1);
     for (int k = 0; k < CO_BINS; ++k) {
-        if (ctx->ev_b0[k]) (void)hipEventDestroy(ctx->ev_b0[k]);
-        if (ctx->ev_b1[k]) (void)hipEventDestroy(ctx->ev_b1[k]);
+        for (int r = 0; r < kMaxRanges; ++r) {
+            if (ctx->ev_b0[r][k]) (void)hipEventDestroy(ctx->ev_b0[r][k]);
+            if (ctx->ev_b1[r][k]) (void)hipEventDestroy(ctx->ev_b1[r][k]);
+        }
     }
     delete ctx;
 }

@@ -8,8 +8,13 @@
 // move is validated, so the device interpreter never indexes out of bounds.
 #include <string.h>
 
+#include <unistd.h>
+
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
 #include <functional>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -120,71 +125,103 @@ struct Visit {
     int stage;  // 0: nothing evaluated, 1: first operand done, 2: both done
 };
 
+// Per-thread working arrays, grown to the largest expression seen and not
+// cleared between expressions (every entry read is written first).
 struct TreeScratch {
-    std::vector<int> size, left, cc, need;
-    std::vector<int> depth_stack;
+    std::vector<int> size, left, cc, need, depth_stack;
     std::vector<Operand> res;
     std::vector<Visit> work;
-    std::vector<Ins> ins;
+    void reserve(int n) {
+        if ((int)size.size() >= n + 1) return;
+        size.resize(n + 1);
+        left.resize(n + 1);
+        cc.resize(n + 1);
+        need.resize(n + 1);
+        depth_stack.resize(n + 1);
+        res.resize(n + 1);
+        work.resize(n + 1);
+    }
 };
+
+static inline bool is_leaf(int t) { return t == NODE_VAR || t == NODE_CONST; }
 
 // Validate one expression (n nodes, K constants, D variables): node types,
 // operator ids, variable indices, prefix-order constant ranks and stack moves.
 // Returns CO_OK, CO_ERR_BOUNDS (value stack beyond CO_MAX_STACK) or
-// CO_ERR_PROGRAM, and its value-stack depth. Fills s.size / s.left / s.cc for
-// the emission.
+// CO_ERR_PROGRAM, and its value-stack depth. Fills s.size / s.left / s.cc and
+// s.need (the spill slots of each subtree in the emission's order) for the
+// emission.
 static int check_tree(const int32_t *nt, const float *nv, const int32_t *ci, int n, int K,
                       int D, int *stack_depth, TreeScratch &s) {
     if (n <= 0) return CO_ERR_PROGRAM;
-    s.size.assign(n, 0);
-    s.left.assign(n, 0);
-    s.cc.assign(n + 1, 0);
+    s.reserve(n);
+    int *size = s.size.data(), *left = s.left.data(), *cc = s.cc.data(), *need = s.need.data();
+    int *st = s.depth_stack.data();
     // prefix pass: constant ranks must be 0..K-1 in prefix order
+    cc[0] = 0;
     for (int i = 0; i < n; i++) {
-        s.cc[i + 1] = s.cc[i] + (nt[i] == NODE_CONST ? 1 : 0);
-        if (nt[i] == NODE_CONST && ci[i] != s.cc[i]) return CO_ERR_PROGRAM;
+        const int c = nt[i] == NODE_CONST;
+        if (c && ci[i] != cc[i]) return CO_ERR_PROGRAM;
+        cc[i + 1] = cc[i] + c;
     }
-    if (s.cc[n] != K) return CO_ERR_PROGRAM;
-    // execution pass (last node first): validation, stack depth, subtree sizes
-    s.depth_stack.clear();
-    int depth = 0;
+    if (cc[n] != K) return CO_ERR_PROGRAM;
+    // execution pass (last node first): validation, stack depth, subtree sizes;
+    // the stack holds subtree roots (a subtree's size is known when it is pushed)
+    int sp = 0, depth = 0;
     for (int i = n - 1; i >= 0; i--) {
         const int t = nt[i];
-        if (t == NODE_VAR) {
-            if (node_int(nv[i], D) < 0) return CO_ERR_PROGRAM;
-            s.depth_stack.push_back(1);
-            s.size[i] = 1;
-        } else if (t == NODE_CONST) {
-            s.depth_stack.push_back(1);
-            s.size[i] = 1;
+        if (t == NODE_VAR || t == NODE_CONST) {
+            if (t == NODE_VAR && node_int(nv[i], D) < 0) return CO_ERR_PROGRAM;
+            size[i] = 1;
+            need[i] = 0;
+            st[sp++] = i;
         } else if (t == NODE_UFUNC) {
             if (!unary_op(node_int(nv[i], 64))) return CO_ERR_PROGRAM;
-            if (s.depth_stack.empty()) return CO_ERR_PROGRAM;
-            s.size[i] = s.depth_stack.back() + 1;
-            s.depth_stack.back() = s.size[i];
+            if (sp < 1) return CO_ERR_PROGRAM;
+            const int c = st[sp - 1];
+            size[i] = size[c] + 1;
+            need[i] = need[c];
+            st[sp - 1] = i;
         } else if (t == NODE_BFUNC) {
             if (!binary_op(node_int(nv[i], 64))) return CO_ERR_PROGRAM;
-            if (s.depth_stack.size() < 2) return CO_ERR_PROGRAM;
-            const int sl = s.depth_stack.back();  // left operand = top of stack
-            s.depth_stack.pop_back();
-            const int sr = s.depth_stack.back();
-            s.left[i] = sl;
-            s.size[i] = sl + sr + 1;
-            s.depth_stack.back() = s.size[i];
+            if (sp < 2) return CO_ERR_PROGRAM;
+            const int l = st[sp - 1], r = st[sp - 2];   // left operand = top of stack
+            --sp;
+            left[i] = size[l];
+            size[i] = size[l] + size[r] + 1;
+            // the operand that needs more slots runs first; two that both need
+            // instructions hold one value in a slot while the other runs
+            const int nl = need[l], nr = need[r];
+            const int hi = nl > nr ? nl : nr;
+            need[i] = (!is_leaf(nt[l]) && !is_leaf(nt[r]) && nl == nr) ? nl + 1 : hi;
+            st[sp - 1] = i;
         } else {
             return CO_ERR_PROGRAM;
         }
-        if ((int)s.depth_stack.size() > depth) depth = (int)s.depth_stack.size();
+        if (sp > depth) depth = sp;
     }
-    if (s.depth_stack.size() != 1) return CO_ERR_PROGRAM;
+    if (sp != 1) return CO_ERR_PROGRAM;
     *stack_depth = depth;
     if (depth > CO_MAX_STACK) return CO_ERR_BOUNDS;
     return CO_OK;
 }
 
-// Emit the instructions of a checked expression into s.ins in execution
-// order. max_slots: slots the target format can address. Returns CO_OK,
-// CO_ERR_BOUNDS or CO_ERR_PROGRAM; sets the tape and spill-slot counts.
+// An instruction's word(s) in out (fast: one word, wide: two), and the later
+// mark that sends its result to slot di.
+static inline void put_ins(uint64_t *out, bool wide, int k, Ins &w) {
+    set_flags(w);
+    if (wide) encode_wide(w, out + 2 * k);
+    else out[k] = encode_fast(w);
+}
+static inline void put_spill(uint64_t *out, bool wide, int k, int di) {
+    if (wide) out[2 * k] |= (uint64_t)1 << 27 | (uint64_t)(di & 255) << 28;
+    else out[k] |= (uint64_t)1 << 19 | (uint64_t)(di & 15) << 20;
+}
+
+// Emit the instructions of a checked expression, encoded, into out in
+// execution order (out holds zeros on entry). max_slots: slots the target
+// format can address. Returns CO_OK, CO_ERR_BOUNDS or CO_ERR_PROGRAM; sets the
+// instruction count, the tape and spill-slot counts and the cost estimate.
 //
 // Operands are evaluated in Sethi-Ullman order: when both operands of a binary
 // operator need instructions, the one whose subtree needs more spill slots runs
@@ -194,161 +231,230 @@ static int check_tree(const int32_t *nt, const float *nv, const int32_t *ci, int
 // first, and the order keeps the slot count at the minimum (at most
 // log2(nodes + 1)), which is what sizes each wavefront's LDS.
 static int emit_tree(const int32_t *nt, const float *nv, const int32_t *ci, int n, int D,
-                     int max_slots_fmt, int *tape_slots, int *slots_used, TreeScratch &s) {
-    s.ins.clear();
-    auto leaf = [&](int i) { return nt[i] == NODE_VAR || nt[i] == NODE_CONST; };
-    // need[i]: spill slots the subtree at node i needs in this order (children
-    // follow their parent in prefix order, so a descending pass sees them first)
-    s.need.assign(n, 0);
-    for (int i = n - 1; i >= 0; i--) {
-        if (nt[i] == NODE_UFUNC) {
-            s.need[i] = s.need[i + 1];
-        } else if (nt[i] == NODE_BFUNC) {
-            const int l = i + 1, r = i + 1 + s.left[i];
-            const int nl = s.need[l], nr = s.need[r];
-            const int hi = nl > nr ? nl : nr;
-            s.need[i] = (!leaf(l) && !leaf(r) && nl == nr) ? nl + 1 : hi;
-        }
-    }
-    s.res.assign(n, Operand{OPD_ACC, 0, -1});
-    s.work.clear();
-    s.work.push_back({0, 0});
-    int tape = 0, live_slots = 0, max_slots = 0;
-    while (!s.work.empty()) {
-        const int i = s.work.back().node, stage = s.work.back().stage;
-        const int t = nt[i];
-        if (t == NODE_VAR || t == NODE_CONST) {
-            s.res[i] = t == NODE_VAR ? Operand{OPD_VAR, node_int(nv[i], D), -1}
-                                     : Operand{OPD_CONST, ci[i], -1};
-            s.work.pop_back();
-            continue;
-        }
-        const bool bin = (t == NODE_BFUNC);
-        const int l = i + 1, r = bin ? i + 1 + s.left[i] : -1;
-        const bool both = bin && !leaf(l) && !leaf(r);
-        const int first = (!bin || (both && s.need[l] > s.need[r])) ? l : r;
-        const int second = !bin ? -1 : (first == l ? r : l);
-        if (stage == 0) {
-            s.work.back().stage = 1;
-            s.work.push_back({first, 0});
-            continue;
-        }
-        if (stage == 1 && bin) {
-            s.work.back().stage = 2;
-            if (both) {
-                // the first operand's value waits in the next free slot
-                if (live_slots >= max_slots_fmt) return CO_ERR_BOUNDS;
-                const int slot = live_slots++;
-                if (live_slots > max_slots) max_slots = live_slots;
-                Operand &o = s.res[first];
-                if (o.kind != OPD_ACC || o.producer < 0) return CO_ERR_PROGRAM;
-                s.ins[o.producer].toslot = 1;
-                s.ins[o.producer].di = slot;
-                o = {OPD_SLOT, slot, -1};
-            }
-            s.work.push_back({second, 0});
-            continue;
-        }
-        s.work.pop_back();
-        const Operand a = s.res[l];
-        const Operand b = bin ? s.res[r] : Operand{OPD_ACC, 0, -1};
-        // spill slots are used last in, first out
-        if (a.kind == OPD_SLOT) {
-            if (a.idx != live_slots - 1) return CO_ERR_PROGRAM;
-            live_slots--;
-        }
-        if (bin && b.kind == OPD_SLOT) {
-            if (b.idx != live_slots - 1) return CO_ERR_PROGRAM;
-            live_slots--;
-        }
-        Ins w = {};
-        w.fid = (int)nv[i];
-        w.bin = bin ? 1 : 0;
-        w.ak = a.kind;
-        w.ai = a.idx;
-        if (bin) {
-            w.bk = b.kind;
-            w.bi = b.idx;
-        }
-        w.lo = s.cc[i + 1];
-        w.hi = s.cc[i + s.size[i]];
-        w.mid = bin ? s.cc[i + 1 + s.left[i]] : w.hi;
-        w.tape = tape;
-        set_flags(w);
-        // reverse-AD tape slots only for partials that are read and not exactly +-1
-        const bool unit = bin && (w.fid == OP_ADD || w.fid == OP_SUB);
-        w.ta = a.kind != OPD_VAR && !unit;
-        w.tb = bin && b.kind != OPD_VAR && !unit;
-        tape += (w.ta ? 1 : 0) + (w.tb ? 1 : 0);
-        s.res[i] = {OPD_ACC, 0, (int)s.ins.size()};
-        s.ins.push_back(w);
-    }
-    if (s.ins.empty()) {
+                     bool wide, int max_slots_fmt, uint64_t *out, int *n_ins, int *tape_slots,
+                     int *slots_used, int64_t *cost, TreeScratch &s) {
+    const int *left = s.left.data(), *cc = s.cc.data(), *need = s.need.data(),
+              *size = s.size.data();
+    Operand *res = s.res.data();
+    Visit *work = s.work.data();
+    auto leaf_opd = [&](int i) -> Operand {
+        return nt[i] == NODE_VAR ? Operand{OPD_VAR, node_int(nv[i], D), -1}
+                                 : Operand{OPD_CONST, ci[i], -1};
+    };
+    int k = 0, tape = 0, live_slots = 0, max_slots = 0;
+    int64_t c = 229;   // fixed per-pass cost, then op_cost of each instruction
+    if (is_leaf(nt[0])) {
         // the expression is one leaf: its value is the identity of that leaf
-        const Operand a = s.res[0];
+        const Operand a = leaf_opd(0);
         Ins w = {};
         w.fid = OP_IDENT;
         w.ak = a.kind;
         w.ai = a.idx;
-        w.lo = s.cc[0];
-        w.mid = w.hi = s.cc[n];
+        w.lo = cc[0];
+        w.mid = w.hi = cc[n];
         w.tape = tape;     // the identity's partial is +1: no tape slot
-        set_flags(w);
-        s.ins.push_back(w);
+        put_ins(out, wide, k++, w);
+        c += op_cost(OP_IDENT);
+    } else {
+        int sp = 0;
+        work[sp++] = {0, 0};
+        while (sp > 0) {
+            Visit &fr = work[sp - 1];
+            const int i = fr.node;
+            const bool bin = nt[i] == NODE_BFUNC;
+            const int l = i + 1, r = bin ? i + 1 + left[i] : -1;
+            const bool both = bin && !is_leaf(nt[l]) && !is_leaf(nt[r]);
+            const int first = (!bin || (both && need[l] > need[r])) ? l : r;
+            const int second = !bin ? -1 : (first == l ? r : l);
+            if (fr.stage == 0) {
+                fr.stage = 1;
+                if (!is_leaf(nt[first])) {
+                    work[sp++] = {first, 0};
+                    continue;
+                }
+                res[first] = leaf_opd(first);
+            }
+            if (fr.stage == 1 && bin) {
+                fr.stage = 2;
+                if (both) {
+                    // the first operand's value waits in the next free slot
+                    if (live_slots >= max_slots_fmt) return CO_ERR_BOUNDS;
+                    const int slot = live_slots++;
+                    if (live_slots > max_slots) max_slots = live_slots;
+                    Operand &o = res[first];
+                    if (o.kind != OPD_ACC || o.producer < 0) return CO_ERR_PROGRAM;
+                    put_spill(out, wide, o.producer, slot);
+                    o = {OPD_SLOT, slot, -1};
+                }
+                if (!is_leaf(nt[second])) {
+                    work[sp++] = {second, 0};
+                    continue;
+                }
+                res[second] = leaf_opd(second);
+            }
+            --sp;
+            const Operand a = res[l];
+            const Operand b = bin ? res[r] : Operand{OPD_ACC, 0, -1};
+            // spill slots are used last in, first out
+            if (a.kind == OPD_SLOT) {
+                if (a.idx != live_slots - 1) return CO_ERR_PROGRAM;
+                live_slots--;
+            }
+            if (bin && b.kind == OPD_SLOT) {
+                if (b.idx != live_slots - 1) return CO_ERR_PROGRAM;
+                live_slots--;
+            }
+            Ins w = {};
+            w.fid = (int)nv[i];
+            w.bin = bin ? 1 : 0;
+            w.ak = a.kind;
+            w.ai = a.idx;
+            if (bin) {
+                w.bk = b.kind;
+                w.bi = b.idx;
+            }
+            w.lo = cc[i + 1];
+            w.hi = cc[i + size[i]];
+            w.mid = bin ? cc[i + 1 + left[i]] : w.hi;
+            w.tape = tape;
+            // reverse-AD tape slots only for partials that are read and not exactly +-1
+            const bool unit = bin && (w.fid == OP_ADD || w.fid == OP_SUB);
+            w.ta = a.kind != OPD_VAR && !unit;
+            w.tb = bin && b.kind != OPD_VAR && !unit;
+            tape += (w.ta ? 1 : 0) + (w.tb ? 1 : 0);
+            c += op_cost(w.fid);
+            res[i] = {OPD_ACC, 0, k};
+            put_ins(out, wide, k++, w);
+        }
     }
     if (live_slots != 0) return CO_ERR_PROGRAM;
+    *n_ins = k;
     *tape_slots = tape;
     *slots_used = max_slots;
+    *cost = c;
     return CO_OK;
 }
 
-// Runs fn(m0, m1) over contiguous chunks of [0, M) on up to nthreads host
-// threads (fewer threads than chunks when the system refuses more: the chunks
-// already started finish, then fn runs over everything on this thread).
+// Worker threads for the decode, started on first use and kept for the
+// process: a decode phase hands its chunks to them instead of starting threads
+// (starting 15 threads twice per decode cost about 1.5 ms of C5's 6 ms). One
+// job at a time; a caller that finds the pool busy, or runs in a process
+// forked after the pool started, does its chunks itself.
+class DecodePool {
+  public:
+    static DecodePool &get() {
+        static DecodePool pool;
+        return pool;
+    }
+    // fn(i) for every i in [0, n) on the workers and this thread; false (and
+    // nothing run) when the pool cannot take the job
+    bool run(int n, const std::function<void(int)> &fn) {
+        if (workers_.empty() || getpid() != pid_) return false;
+        std::unique_lock<std::mutex> job(job_mu_, std::try_to_lock);
+        if (!job.owns_lock()) return false;
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            fn_ = &fn;
+            n_ = n;
+            next_.store(0);
+            busy_ = (int)workers_.size();
+            ++gen_;
+        }
+        cv_.notify_all();
+        work();
+        std::unique_lock<std::mutex> g(mu_);
+        done_cv_.wait(g, [&] { return busy_ == 0; });
+        fn_ = nullptr;
+        return true;
+    }
+
+  private:
+    DecodePool() : pid_(getpid()) {
+        const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+        const int n = (int)std::min(15u, hw - 1);
+        try {
+            for (int i = 0; i < n; i++) workers_.emplace_back([this] { loop(); });
+        } catch (...) {
+            // fewer workers than asked: the ones started serve
+        }
+    }
+    ~DecodePool() {
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (std::thread &t : workers_) t.join();
+    }
+    void work() {
+        for (int i = next_.fetch_add(1); i < n_; i = next_.fetch_add(1)) (*fn_)(i);
+    }
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> g(mu_);
+                cv_.wait(g, [&] { return stop_ || gen_ != seen; });
+                if (stop_) return;
+                seen = gen_;
+            }
+            work();
+            std::lock_guard<std::mutex> g(mu_);
+            if (--busy_ == 0) done_cv_.notify_one();
+        }
+    }
+    std::vector<std::thread> workers_;
+    std::mutex job_mu_, mu_;
+    std::condition_variable cv_, done_cv_;
+    const std::function<void(int)> *fn_ = nullptr;
+    int n_ = 0, busy_ = 0;
+    std::atomic<int> next_{0};
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+    const pid_t pid_;
+};
+
+// Runs fn(m0, m1) over nthreads contiguous chunks of [0, M) on the decode
+// pool and this thread; without the pool, redo(0, M) runs on this thread.
 template <typename Fn, typename Redo>
 static void chunked(int M, int nthreads, const Fn &fn, const Redo &redo) {
-    bool done = false;
-    if (nthreads > 1) {
-        std::vector<std::thread> pool;
+    if (nthreads > 1 && M > 0) {
         const int chunk = (M + nthreads - 1) / nthreads;
-        try {
-            // chunks 1.. on new threads, chunk 0 on this one
-            for (int i = 1; i < nthreads; i++) {
-                const int m0 = i * chunk, m1 = std::min(M, m0 + chunk);
-                if (m0 < m1) pool.emplace_back(std::cref(fn), m0, m1);
-            }
-            done = true;
-        } catch (...) {
-            // no more threads
-        }
-        if (done) fn(0, std::min(M, chunk));
-        for (std::thread &th : pool) th.join();
+        const int n = (M + chunk - 1) / chunk;
+        const std::function<void(int)> job = [&](int i) {
+            fn(i * chunk, std::min(M, (i + 1) * chunk));
+        };
+        if (DecodePool::get().run(n, job)) return;
     }
-    if (!done) redo(0, M);
+    redo(0, M);
 }
 
-int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
-                      const int32_t *ci, const TreeMeta *metas, uint64_t *prog,
-                      int32_t *order, int32_t *bin_start, ExprDesc *descs,
-                      int32_t *stack, int32_t *n_ins, int32_t *prog_off, int32_t *route,
-                      Plan *plan) {
+int check_header(const PopHeader *h, const int32_t *nt, const float *nv, const int32_t *ci,
+                 const TreeMeta *metas) {
     if (!h || !metas) return CO_ERR_NULLARG;
     if (h->total_nodes > 0 && (!nt || !nv || !ci)) return CO_ERR_NULLARG;
     if (h->M_prob < 0 || h->N < 0 || h->n_vars < 0 || h->total_nodes < 0 || h->total_c < 0)
         return CO_ERR_NULLARG;
     if (h->K_max > CO_MAX_K || h->max_stack > CO_MAX_STACK || h->n_vars > CO_MAX_VARS)
         return CO_ERR_BOUNDS;
-    const int M = h->M_prob, D = h->n_vars;
     long ksum = 0, nsum = 0;
-    for (int m = 0; m < M; m++) { ksum += metas[m].K; nsum += metas[m].n_nodes; }
+    for (int m = 0; m < h->M_prob; m++) { ksum += metas[m].K; nsum += metas[m].n_nodes; }
     if (ksum != (long)h->total_c) return CO_ERR_SUM_C;
     if (nsum != (long)h->total_nodes) return CO_ERR_SUM_NODES;
+    return CO_OK;
+}
 
-    std::vector<uint64_t> tmp;
-    if (!prog) {
-        tmp.assign(h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1, 0);
-        prog = tmp.data();
-    }
+// Decode the M expressions at metas (rows row_base.. of the population whose
+// header h is checked): programs into prog (word 0 of this range at word
+// word_base of the device program buffer), descriptors in launch order.
+static int decode_core(const PopHeader *h, const int32_t *nt, const float *nv,
+                       const int32_t *ci, const TreeMeta *metas, int M, int row_base,
+                       int64_t word_base, uint64_t *prog, int32_t *order, int32_t *bin_start,
+                       ExprDesc *descs, int32_t *stack, int32_t *n_ins, int32_t *prog_off,
+                       int32_t *route, Plan *plan, int64_t nodes_per_thread) {
+    const int D = h->n_vars;
+    long nsum = 0;
+    for (int m = 0; m < M; m++) nsum += metas[m].n_nodes;
     for (int m = 0; m < M; m++) {
         const TreeMeta &t = metas[m];
         if (t.K < 0 || t.n_nodes < 0 || t.node_offset < 0 || t.c_offset < 0 ||
@@ -361,7 +467,7 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
     std::vector<int32_t> rcs(M, CO_OK), gen(M, 0);
     std::vector<int64_t> cost(descs ? M : 0);
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-    const int nthreads = (int)std::min<int64_t>(std::min(16u, hw), nsum / 65536 + 1);
+    const int nthreads = (int)std::min<int64_t>(std::min(16u, hw), nsum / nodes_per_thread + 1);
     // phase 1: every expression's stack depth and so its kernel, by a count
     // over the node types (the depth check_tree finds for a valid tree); the
     // full check runs in phase 2, which still ends before anything is used
@@ -405,20 +511,17 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
             int dd = 0;
             rcs[m] = check_tree(tnt, tnv, tci, t.n_nodes, t.K, D, &dd, s);
             if (rcs[m] == CO_OK && dd != depth[m]) rcs[m] = CO_ERR_PROGRAM;   // never, for a valid tree
+            int64_t c = 0;
+            int ni = 0;
             if (rcs[m] == CO_OK)
-                rcs[m] = emit_tree(tnt, tnv, tci, t.n_nodes, D, gen[m] ? kMaxSlotsWide : kMaxSlots,
-                                   &tapes[m], &slots[m], s);
+                rcs[m] = emit_tree(tnt, tnv, tci, t.n_nodes, D, gen[m] != 0,
+                                   gen[m] ? kMaxSlotsWide : kMaxSlots, out, &ni, &tapes[m],
+                                   &slots[m], &c, s);
             if (rcs[m] != CO_OK) return;
-            nins[m] = (int32_t)s.ins.size();
+            nins[m] = ni;
             if (!gen[m] && tapes[m] > 255) {   // 8-bit tape field (n <= 255 keeps it below)
                 rcs[m] = CO_ERR_BOUNDS;
                 return;
-            }
-            int64_t c = 229;
-            for (int i = 0; i < nins[m]; i++) {
-                if (gen[m]) encode_wide(s.ins[i], out + 2 * i);
-                else out[i] = encode_fast(s.ins[i]);
-                c += op_cost(s.ins[i].fid);
             }
             if (descs) cost[m] = c;
         }
@@ -478,11 +581,11 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
         for (int p = 0; p < M; p++) {
             const int m = launch[p];
             ExprDesc &d = descs[p];
-            d.prog_off = poff[m];
+            d.prog_off = (int32_t)(word_base + poff[m]);
             d.n = nins[m];
             d.c_off = metas[m].c_offset;
             d.K = metas[m].K;
-            d.y_row = m;
+            d.y_row = row_base + m;
             d.tape = tapes[m];
             d.slots = slots[m];
             d.gen = gen[m];
@@ -501,6 +604,32 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
         plan->n_gen = n_gen;
     }
     return CO_OK;
+}
+
+int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
+                      const int32_t *ci, const TreeMeta *metas, uint64_t *prog,
+                      int32_t *order, int32_t *bin_start, ExprDesc *descs,
+                      int32_t *stack, int32_t *n_ins, int32_t *prog_off, int32_t *route,
+                      Plan *plan) {
+    const int rc = check_header(h, nt, nv, ci, metas);
+    if (rc != CO_OK) return rc;
+    std::vector<uint64_t> tmp;
+    if (!prog) {
+        tmp.assign(h->total_nodes > 0 ? 2 * (size_t)h->total_nodes : 1, 0);
+        prog = tmp.data();
+    }
+    return decode_core(h, nt, nv, ci, metas, h->M_prob, 0, 0, prog, order, bin_start, descs,
+                       stack, n_ins, prog_off, route, plan, 65536);
+}
+
+int decode_range(const PopHeader *h, const int32_t *nt, const float *nv, const int32_t *ci,
+                 const TreeMeta *metas, int m0, int m1, int64_t word_base, uint64_t *prog,
+                 ExprDesc *descs, Plan *plan) {
+    // a range is decoded while the device fits the ones before it: more
+    // threads per node than a whole population gets
+    return decode_core(h, nt, nv, ci, metas + m0, m1 - m0, m0, word_base, prog + word_base,
+                       nullptr, nullptr, descs + m0, nullptr, nullptr, nullptr, nullptr, plan,
+                       16384);
 }
 
 }  // namespace cusr

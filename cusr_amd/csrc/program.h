@@ -142,4 +142,20 @@ int decode_population(const PopHeader *h, const int32_t *nt, const float *nv,
                       int32_t *stack, int32_t *n_ins, int32_t *prog_off, int32_t *route,
                       Plan *plan);
 
+// The header-level checks decode_population makes first: null inputs, device
+// bounds on K_max / max_stack / n_vars, and the sums of K and of n_nodes.
+int check_header(const PopHeader *h, const int32_t *nt, const float *nv, const int32_t *ci,
+                 const TreeMeta *metas);
+
+// Decode expressions [m0, m1) of a population whose header passed
+// check_header, for an upload that decodes a population in pieces: their
+// programs go to prog from word word_base on (the range's layout as
+// decode_population's, its descriptors' prog_off counting from word 0 of
+// prog), their descriptors to descs[m0..m1) in launch order within the range
+// (y_row the population row). plan describes the range (M, words, slots,
+// tape); the same per-expression checks and error codes as decode_population.
+int decode_range(const PopHeader *h, const int32_t *nt, const float *nv, const int32_t *ci,
+                 const TreeMeta *metas, int m0, int m1, int64_t word_base, uint64_t *prog,
+                 ExprDesc *descs, Plan *plan);
+
 }  // namespace cusr

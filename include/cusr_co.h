@@ -228,7 +228,10 @@ int co_optimize(void *handle, const PopHeader *header,
 
 /* Wall-clock split of the last co_optimize / co_optimize_ex call on this
  * process: setup (entry to loop start: checks, plan, uploads) and loop
- * (device fit until results are back on the host). Returns 0 and fills
+ * (device fit until results are back on the host). A population of 16,384
+ * or more expressions is decoded, uploaded and launched in ranges, the host
+ * decoding a range while the device fits the ones before: setup then ends at
+ * the first range's launch. Returns 0 and fills
  * both (the reference returns 1 and -1.0 unless built with -DPROFILE,
  * cusr/kernel/co_lib.cu:531-541; this build always records). */
 int co_last_split(double *setup_ms_out, double *loop_ms_out);
