@@ -222,7 +222,9 @@ def valu_issue(workload_key, kname_of, bins, device_ms, kdom):
     if kname_of(kdom).startswith("lm_pass_kernel"):
         # the split path: a bin is many pass launches and the summary holds one
         # launch per kernel, so only the per-launch figure is defined
-        dom = next(e for n, e in ctr.items() if kname_of(kdom).rstrip(">") in n)
+        dom = next((e for n, e in ctr.items() if kname_of(kdom).rstrip(">") in n), None)
+        if dom is None:
+            return None
         return {"whole_fit_frac": None,
                 "dominant_alone_frac": dom["SQ_ACTIVE_INST_VALU"] * cyc / (dom["alone_ms"] / 1e3),
                 "dominant_alone_ms": dom["alone_ms"], "per": "one pass launch of the bin",
@@ -237,9 +239,9 @@ def valu_issue(workload_key, kname_of, bins, device_ms, kdom):
             missing.append(k)
             continue
         tot += e["SQ_ACTIVE_INST_VALU"]
-    if missing:
+    dom = next((e for n, e in ctr.items() if kname_of(kdom).rstrip(">") in n), None)
+    if missing or dom is None:
         return None
-    dom = next(e for n, e in ctr.items() if kname_of(kdom).rstrip(">") in n)
     return {"whole_fit_frac": tot * cyc / (device_ms / 1e3),
             "dominant_alone_frac": dom["SQ_ACTIVE_INST_VALU"] * cyc / (dom["alone_ms"] / 1e3),
             "dominant_alone_ms": dom["alone_ms"], "clock_ghz": MI355X_CLOCK_HZ / 1e9,
@@ -265,15 +267,17 @@ def launch_bins(pop):
     return np.where(route != 0, co_inproc.CO_GENERAL_BIN, K)
 
 
-def kernel_name(cfg, pop, k):
+def kernel_name(cfg, pop, k, parts=0):
     """Kernel name (as rocprofv3 shows it, without the last template
-    arguments) of bin k's fit: lm_fit_kernel / lm_fit_gen_kernel, or the
-    split path's lm_pass_kernel, which the step kernel follows."""
+    arguments) of bin k's fit with `parts` point partitions (0: the default
+    for N and the AD mode): lm_fit_kernel / lm_fit_gen_kernel, or the split
+    path's lm_pass_kernel, which the step kernel follows."""
     from cusr_amd.kernel import co_inproc
 
     rname = "double" if cfg.precision == 0 else "float"
     gen = k == co_inproc.CO_GENERAL_BIN
-    if co_inproc.co_partitions_for_n(int(pop["N"])) > co_inproc.CO_MAX_PARTITIONS:
+    G = parts or co_inproc.co_partitions_for(int(pop["N"]), cfg.ad_mode)
+    if G > co_inproc.CO_MAX_PARTITIONS:
         return (f"lm_pass_kernel<{co_inproc.CO_MAX_K if gen else k}, {rname}, "
                 f"{cfg.ad_mode}")
     if gen:
@@ -291,7 +295,8 @@ def alone_leg(fit_alone, pop, bin_of, kdom, reps):
     return float(np.mean(ms)), ms
 
 
-def roofline(pop, cfg, iters, bins, kdom, alone_ms, alone_runs, bin_of, device_ms=None):
+def roofline(pop, cfg, iters, bins, kdom, alone_ms, alone_runs, bin_of, device_ms=None,
+             parts=0):
     """Dominant launch against the fp64 (fp32 for mixed) vector peak, with
     the HBM figure as a secondary block."""
     from cusr_amd.benchmark import accounting
@@ -301,7 +306,7 @@ def roofline(pop, cfg, iters, bins, kdom, alone_ms, alone_runs, bin_of, device_m
     vpeak = FP64_VECTOR_PEAK_TFLOPS if cfg.precision == 0 else FP32_VECTOR_PEAK_TFLOPS
     tflops = w["flops"] / dom_s / 1e12
     gbs = w["bytes"] / dom_s / 1e9
-    kname = kernel_name(cfg, pop, kdom)
+    kname = kernel_name(cfg, pop, kdom, parts)
     key = f"{cfg.name}:{pop['M']}x{pop['N']}:seed{cfg.seed}:it{cfg.max_iter}"
     out = {"bound": "valu", "achieved": tflops, "peak": vpeak, "unit": "TFLOP/s",
            "frac": tflops / vpeak, "traffic": load_traffic(key, kname),
@@ -313,7 +318,7 @@ def roofline(pop, cfg, iters, bins, kdom, alone_ms, alone_runs, bin_of, device_m
            "hbm": {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                    "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": w["bytes"]}}
     if device_ms:
-        out["measured_valu_busy"] = valu_issue(key, lambda k: kernel_name(cfg, pop, k), bins,
+        out["measured_valu_busy"] = valu_issue(key, lambda k: kernel_name(cfg, pop, k, parts), bins,
                                                device_ms, kdom)
     return out
 
@@ -358,7 +363,7 @@ def run_resident(args, cfg, co, pop):
 
     alone_ms, alone_runs = alone_leg(fit_alone, pop, bin_of, kdom, args.alone_reps)
     roof = roofline(pop, cfg, res["iters"], bins, kdom, alone_ms, alone_runs, bin_of,
-                    device_ms=kms)
+                    device_ms=kms, parts=args.partitions)
     whole = accounting.algorithmic_work(pop, res["iters"], cfg.ad_mode)
     status_counts = np.bincount(res["status"], minlength=5).tolist()
     _say(f"{args.steps} steps: {ms_per_step:.2f} ms/step, device {kms:.2f} ms/fit, "
@@ -440,7 +445,7 @@ def main():
     ap.add_argument("--alone-reps", type=int, default=3,
                     help="launches of the dominant bin alone (the roofline's duration)")
     ap.add_argument("--partitions", type=int, default=0,
-                    help="point partitions per expression (0: by N, co_partitions_for_n; "
+                    help="point partitions per expression (0: by N and AD mode, co_partitions_for; "
                          "above 4 the split path)")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -1,8 +1,9 @@
 // lm_split.h -- the split path: one expression's passes spread over many
 // workgroups.
 //
-// With more than CO_MAX_PARTITIONS point partitions (co_partitions_for_n from
-// CO_SPLIT_MIN_N points, or CoOptions.partitions), each partition of a pass
+// With more than CO_MAX_PARTITIONS point partitions (co_partitions_for: from
+// CO_SPLIT_MIN_N points, and for reverse AD from 2,048 to 16,383 points; or
+// CoOptions.partitions), each partition of a pass
 // is a workgroup of its own: lm_pass_kernel runs one wavefront over the
 // granules g = part, part + G, ... (the partition rule of data_pass) and
 // writes the partition's sums to HBM; lm_step_kernel, one wavefront per

@@ -60,6 +60,14 @@ def co_partitions_for_n(N: int) -> int:
         return g
     return 4 if N >= 16384 else (2 if N >= 1024 else 1)
 
+
+def co_partitions_for(N: int, ad_mode: int = 0) -> int:
+    """include/cusr_co.h co_partitions_for: reverse AD from 2,048 to 16,383
+    points takes the split path with 8 partitions."""
+    if ad_mode == 1 and 2048 <= N < 16384:
+        return 8
+    return co_partitions_for_n(N)
+
 CO_AD_FORWARD, CO_AD_REVERSE = 0, 1
 CO_PREC_FP64, CO_PREC_MIXED = 0, 1
 CO_ORDER_IMPROVE_FIRST, CO_ORDER_CONVERGE_FIRST = 0, 1

@@ -96,7 +96,7 @@ typedef struct CoOptions {
     int32_t fp64_guard; /* 1: deliver c_init where the fp64 loss at c_final is
                            non-finite or worse (cusr/kernel/lm_core.cuh:299-351) */
     int32_t partitions; /* point partitions per expression (a power of two up to
-                           CO_MAX_SPLIT; 0: by N, co_partitions_for_n). Part of
+                           CO_MAX_SPLIT; 0: co_partitions_for). Part of
                            the arithmetic order: the sums of each partition are
                            formed separately and added in partition order. Up
                            to CO_MAX_PARTITIONS the wavefronts of one
@@ -156,10 +156,23 @@ static inline int co_partitions_for_n(int N) {
     return N >= 16384 ? 4 : (N >= 1024 ? 2 : 1);
 }
 
+/* Point partitions when CoOptions.partitions is 0, by N and the AD mode.
+ * Reverse AD from 2,048 to 16,383 points takes the split path with 8
+ * partitions: its passes hold a tape and an adjoint sweep per point, so a
+ * wavefront's pass is long and the split path's eight workgroups per
+ * expression hide its loads where two wavefronts of one workgroup do not
+ * (C3, N = 2,048, K 4-16, measured on MI355X: 136.5 -> 126.4 ms per fit;
+ * 16 partitions 130.0, 32 140.2). Forward AD keeps co_partitions_for_n (C2
+ * with 8 split partitions: 11.6 -> 23.5 ms). */
+static inline int co_partitions_for(int N, int ad_mode) {
+    if (ad_mode == CO_AD_REVERSE && N >= 2048 && N < 16384) return 8;
+    return co_partitions_for_n(N);
+}
+
 /* The partitions options o give for N points (0 if o->partitions is not a
  * power of two up to CO_MAX_SPLIT). */
 static inline int co_partitions_resolve(const CoOptions *o, int N) {
-    const int g = o->partitions ? o->partitions : co_partitions_for_n(N);
+    const int g = o->partitions ? o->partitions : co_partitions_for(N, o->ad_mode);
     return (g >= 1 && g <= CO_MAX_SPLIT && (g & (g - 1)) == 0) ? g : 0;
 }
 

@@ -862,7 +862,7 @@ int orc_pass_api(const PopHeader *h, const int32_t *nt, const float *nv, const i
     free(depth);
     if (rc != CO_OK) return rc;
     PassOut *p = (PassOut *)malloc(sizeof(PassOut));
-    const int G = partitions ? partitions : co_partitions_for_n(h->N);
+    const int G = partitions ? partitions : co_partitions_for(h->N, ad_mode);
     orc_pass(&t, h->N, h->n_vars, xs, y, c, prec, mt->K > 0 ? (ad_mode ? 2 : 1) : 0, G, p);
     *loss = p->loss;
     for (int j = 0; j < mt->K; j++) {
