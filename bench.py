@@ -210,7 +210,7 @@ def load_valu(workload_key):
     return d["kernels"]
 
 
-def valu_issue(workload_key, kname_of, bins, device_ms, kdom):
+def valu_issue(workload_key, kname_of, bins, device_ms, kdom, rounds=0):
     """Measured VALU busy fraction: SQ_ACTIVE_INST_VALU x 4 cycles over the
     machine's VALU cycles (1024 SIMDs at the 2.4 GHz peak clock, so a lower
     bound) -- for the whole fit (all K bins over the fit's device time) and
@@ -220,14 +220,31 @@ def valu_issue(workload_key, kname_of, bins, device_ms, kdom):
         return None
     cyc = 4.0 / (MI355X_SIMDS * MI355X_CLOCK_HZ)
     if kname_of(kdom).startswith("lm_pass_kernel"):
-        # the split path: a bin is many pass launches and the summary holds one
-        # launch per kernel, so only the per-launch figure is defined
+        # the split path: a bin is `rounds` pass launches, each followed by a
+        # step launch; the summary holds per-launch means over each kernel's
+        # last `rounds` dispatches (one fit of the bin; the step kernel's are
+        # the last bin's), so the whole fit is those means times the launches
         dom = next((e for n, e in ctr.items() if kname_of(kdom).rstrip(">") in n), None)
         if dom is None:
             return None
-        return {"whole_fit_frac": None,
+        step = next((e for n, e in ctr.items() if n.startswith("cusr::lm_step_kernel")), None)
+        tot, nb, whole = 0.0, 0, None
+        for k, v in enumerate(bins):
+            if v < 0:
+                continue
+            e = next((e for n, e in ctr.items() if kname_of(k).rstrip(">") in n), None)
+            if e is None:
+                tot = None
+                break
+            tot += e["SQ_ACTIVE_INST_VALU"] * rounds
+            nb += 1
+        if tot is not None and step is not None and rounds:
+            tot += step["SQ_ACTIVE_INST_VALU"] * rounds * nb
+            whole = tot * cyc / (device_ms / 1e3)
+        return {"whole_fit_frac": whole,
                 "dominant_alone_frac": dom["SQ_ACTIVE_INST_VALU"] * cyc / (dom["alone_ms"] / 1e3),
-                "dominant_alone_ms": dom["alone_ms"], "per": "one pass launch of the bin",
+                "dominant_alone_ms": dom["alone_ms"],
+                "per": "a pass launch of the bin, the mean over one fit's launches",
                 "clock_ghz": MI355X_CLOCK_HZ / 1e9, "simds": MI355X_SIMDS,
                 "source": str(_profile(workload_key, "valu").relative_to(REPO))}
     tot, missing = 0.0, []
@@ -319,7 +336,8 @@ def roofline(pop, cfg, iters, bins, kdom, alone_ms, alone_runs, bin_of, device_m
                    "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": w["bytes"]}}
     if device_ms:
         out["measured_valu_busy"] = valu_issue(key, lambda k: kernel_name(cfg, pop, k, parts), bins,
-                                               device_ms, kdom)
+                                               device_ms, kdom,
+                                               1 + cfg.max_iter + (2 if cfg.precision else 0))
     return out
 
 

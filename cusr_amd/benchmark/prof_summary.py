@@ -62,17 +62,25 @@ def trace(db, match=None, skip=0, take=None):
     return "\n".join(out)
 
 
-def pmc_per_dispatch(db, match=None, last=False):
+def _tail_ids(pairs, tail):
+    """{kernel: the ids of its last `tail` dispatches} from (kernel, id) pairs."""
+    ids = collections.defaultdict(set)
+    for name, disp in pairs:
+        ids[name].add(disp)
+    return {k: set(sorted(v)[-tail:]) for k, v in ids.items()}
+
+
+def pmc_per_dispatch(db, match=None, last=False, tail=0):
     """Per kernel, each counter's mean over its dispatches (last: the value of
-    the kernel's last dispatch only)."""
+    the kernel's last dispatch only; tail: the mean over its last `tail`
+    dispatches, e.g. one whole split-path fit of a bin)."""
     rows = _rows(db, "select kernel_name, dispatch_id, counter_name, sum(value) "
                      "from counters_collection group by kernel_name, dispatch_id, counter_name")
     acc = collections.defaultdict(lambda: collections.defaultdict(list))
-    if last:
-        top = {}
-        for name, disp, _ctr, _val in rows:
-            top[name] = max(top.get(name, disp), disp)
-        rows = [r for r in rows if r[1] == top[r[0]]]
+    tail = 1 if last and not tail else tail
+    if tail:
+        keep = _tail_ids(((r[0], r[1]) for r in rows), tail)
+        rows = [r for r in rows if r[1] in keep[r[0]]]
     for name, _disp, ctr, val in rows:
         if match and match not in name:
             continue
@@ -90,18 +98,18 @@ def pmc(db, match=None):
     return "\n".join(out)
 
 
-def valu(db, match=None, workload_key=None, last=False):
+def valu(db, match=None, workload_key=None, last=False, tail=0):
     """Per kernel: the average per dispatch of every collected counter and
     the dispatch duration (counter runs serialise dispatches, so these are
-    the kernels running alone); last: the kernel's last dispatch only."""
-    d = pmc_per_dispatch(db, match, last)
+    the kernels running alone); last: the kernel's last dispatch only; tail:
+    the averages over its last `tail` dispatches."""
+    d = pmc_per_dispatch(db, match, last, tail)
     durs = collections.defaultdict(list)
     rows = _rows(db, "select name, dispatch_id, duration from kernels")
-    top = {}
-    for name, disp, _dur in rows:
-        top[name] = max(top.get(name, disp), disp)
+    tail = 1 if last and not tail else tail
+    keep = _tail_ids(((r[0], r[1]) for r in rows), tail) if tail else None
     for name, disp, dur in rows:
-        if name in d and (not last or disp == top[name]):
+        if name in d and (keep is None or disp in keep[name]):
             durs[name].append(dur / 1e6)
     out = {"kernels": {}}
     for name in sorted(d):
@@ -165,13 +173,16 @@ def main():
     ap.add_argument("--last", action="store_true",
                     help="valu, traffic: each kernel's last dispatch only (runs whose "
                          "earlier dispatches are warm-ups or calibration calls)")
+    ap.add_argument("--tail", type=int, default=0,
+                    help="valu: averages over each kernel's last TAIL dispatches (the "
+                         "split path: 1 + max_iter pass launches are one fit of a bin)")
     a = ap.parse_args()
     if a.mode == "trace":
         print(trace(a.dbs[0], a.match, a.skip, a.take))
     elif a.mode == "pmc":
         print(pmc(a.dbs[0], a.match))
     elif a.mode == "valu":
-        t = valu(a.dbs[0], a.match, a.workload_key, a.last)
+        t = valu(a.dbs[0], a.match, a.workload_key, a.last, a.tail)
         print(json.dumps(t, indent=1))
         if a.out:
             with open(a.out, "w") as fh:

@@ -1482,8 +1482,9 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
 #ifndef CUSR_W64_TABLE
 #define CUSR_W64_TABLE 1, 1, 1, 2, 2, 2, 2, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1
 #endif
-// fp64 reverse AD: no cap except K = 9 (256 VGPRs with 23 spilled beats 300
-// at one wave per SIMD; from K = 10 the spills grow to 76 and more)
+// fp64 reverse AD, the fit kernels (N below the split path's): no cap except
+// K = 9 (256 VGPRs with 23 spilled beats 300 at one wave per SIMD; from K = 10
+// the spills grow to 76 and more)
 #ifndef CUSR_WREV64_TABLE
 #define CUSR_WREV64_TABLE 1, 1, 1, 1, 1, 1, 1, 1, 1, 2, 1, 1, 1, 1, 1, 1, 1
 #endif
@@ -1500,6 +1501,20 @@ template <typename R, int K, int AD, int LN = 0>
 constexpr int waves_per_eu() {
     return sizeof(R) == 8 ? (AD == CO_AD_FORWARD ? (LN ? kW64LargeN[K] : kW64[K]) : kWRev64[K])
                           : CUSR_WAVES_OTHER;
+}
+// fp64 reverse AD on the split path (the pass kernels: one wavefront per
+// workgroup, one point per lane): two waves per SIMD from K = 9 to 14, where
+// one wavefront per SIMD issued its SALU and VALU back to back (C3 127.4 ->
+// 116.7 ms); K = 15, 16 keep their 358 and 390 VGPRs (at 256 they spill
+// heavily: C3 126.6 ms with two waves for K = 9..16).
+#ifndef CUSR_WREV64_SPLIT_TABLE
+#define CUSR_WREV64_SPLIT_TABLE 1, 1, 1, 1, 1, 1, 1, 1, 1, 2, 2, 2, 2, 2, 2, 1, 1
+#endif
+constexpr int kWRev64Split[CO_FAST_MAX_K + 1] = {CUSR_WREV64_SPLIT_TABLE};
+template <typename R, int K, int AD, int LN = 0>
+constexpr int pass_waves_per_eu() {
+    return (sizeof(R) == 8 && AD == CO_AD_REVERSE) ? kWRev64Split[K]
+                                                   : waves_per_eu<R, K, AD, LN>();
 }
 // True when the large-N tables give (R, K, AD) another kernel (only those
 // get an LN = 1 instance).

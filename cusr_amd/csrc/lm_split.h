@@ -55,7 +55,7 @@ __global__ void __launch_bounds__(kLanes) lm_split_init_kernel(FitArgs fa) {
 // c_try (value only for K = 0); the audits are fp64 value passes at c_cur and
 // c_init.
 template <int K, typename R, int AD, int LN, bool GEN>
-__global__ void __launch_bounds__(kLanes, (GEN ? CUSR_WAVES_GEN : waves_per_eu<R, (GEN ? 0 : K), AD, LN>()))
+__global__ void __launch_bounds__(kLanes, (GEN ? CUSR_WAVES_GEN : pass_waves_per_eu<R, (GEN ? 0 : K), AD, LN>()))
 lm_pass_kernel(FitArgs fa) {
     typedef typename std::conditional<GEN, WideFmt, FastFmt>::type F;
     constexpr int KC = FitStatic<GEN>::KC;
