@@ -698,7 +698,15 @@ typedef double cusr_double4 __attribute__((ext_vector_type(4)));
 constexpr int kJtStride = 17;                       // doubles per row (bank spread)
 constexpr size_t kJtBytes = (size_t)kLanes * kJtStride * sizeof(double);
 template <int K, int AD>
-constexpr bool matrix_sums() { return AD == CO_AD_FORWARD && K >= CO_SUMS_MATRIX_MIN_K; }
+constexpr bool matrix_sums() {
+    return AD == CO_AD_FORWARD ? K >= CO_SUMS_MATRIX_MIN_K : K >= CO_SUMS_MATRIX_MIN_K_REV;
+}
+// Reverse AD stages the rows (and the solve's K x K factor) in the tape's LDS:
+// a batch's rows are written after its reverse sweep has read the tape, and
+// the solve runs between passes. Every column the matrix instruction reads
+// (0..15) is rewritten for each batch, the ones past r with zeros.
+template <int K, int AD>
+constexpr bool sums_over_tape() { return AD == CO_AD_REVERSE && matrix_sums<K, AD>(); }
 
 constexpr int sums_width(int K) { return 1 + K + K * (K + 1) / 2; }
 
@@ -820,7 +828,7 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
                           double *out, int lane) {
     constexpr int W = (JAC == 0) ? 1 : sums_width(K);
     constexpr int KT = (K > 0) ? K : 1;
-    constexpr bool MX = (JAC == 1) && matrix_sums<K, CO_AD_FORWARD>();
+    constexpr bool MX = (JAC != 0) && matrix_sums<K, (JAC == 2 ? CO_AD_REVERSE : CO_AD_FORWARD)>();
     // per-lane accumulators: all sums, or (matrix sums, K = 16) r^2 and J^T r
     constexpr int WL = MX ? ((K < 16) ? 1 : 1 + K) : W;
     const int granules = (a.N + kLanes - 1) / kLanes;
@@ -866,6 +874,11 @@ __device__ __forceinline__ void data_pass(const PassArgs &a, const WaveLds<R, P>
                 double *row = a.jt + lane * kJtStride;
 #pragma unroll
                 for (int j = 0; j < K; ++j) row[j] = valid[p] ? (double)T[p * KT + j] : 0.0;
+                if constexpr (JAC == 2) {
+                    // rows over the tape: the columns past r are rewritten too
+#pragma unroll
+                    for (int j = K + 1; j < 16; ++j) row[j] = 0.0;
+                }
                 if constexpr (K < 16) {
                     row[K] = r;
                 } else if (valid[p]) {
@@ -1262,11 +1275,11 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     const bool lead = wave == 0;     // the wavefront that writes shared state
     double *jt = (double *)my_lds;   // matrix sums: the slice's augmented rows first
     // then the K x K Cholesky factor and rhs (the general kernel's solve
-    // reuses the rows' bytes: it runs between passes)
-    double *lds_l = GEN ? jt : jt + kLanes * kJtStride;
+    // reuses the rows' bytes: it runs between passes; reverse AD puts both
+    // in the tape's bytes)
     if constexpr (GEN) {
         my_lds += kGenJtBytes;
-    } else if constexpr (matrix_sums<K, AD>()) {
+    } else if constexpr (matrix_sums<K, AD>() && !sums_over_tape<K, AD>()) {
         // columns K+1.. of every row stay zero for the whole fit
 #pragma unroll
         for (int j = 0; j < kJtStride; ++j) jt[lane * kJtStride + j] = 0.0;
@@ -1276,6 +1289,8 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
     wl.x = (R *)my_lds;
     wl.slot = wl.x + (size_t)fa.D * P * kLanes;
     wl.tape = wl.slot + (size_t)fa.slots * P * kLanes;
+    if constexpr (!GEN && sums_over_tape<K, AD>()) jt = (double *)wl.tape;
+    double *lds_l = GEN ? jt : jt + kLanes * kJtStride;
     PassArgs pa;
     pa.prog = (ProgPtr)(fa.prog + e.prog_off);
     pa.n = e.n;
@@ -1562,11 +1577,12 @@ constexpr size_t fit_static_lds(bool gen) {
 // fp64 audit pass reuses the same bytes at audit_points per lane).
 template <typename R, int K, int AD, int LN = 0>
 constexpr size_t fit_lds_bytes_t(int D, int slots, int tape) {
-    const size_t a =
-        (size_t)(D + slots + tape) * points_per_pass<R, K, AD, LN>() * kLanes * sizeof(R);
+    const size_t row = (size_t)points_per_pass<R, K, AD, LN>() * kLanes * sizeof(R);
+    const size_t mx = matrix_sums<K, AD>() ? kJtBytes + (size_t)K * (K + 1) * sizeof(double) : 0;
+    const size_t t = sums_over_tape<K, AD>() && mx > (size_t)tape * row ? mx : (size_t)tape * row;
+    const size_t a = (size_t)(D + slots) * row + t;
     const size_t b = (size_t)(D + slots) * audit_points<R, K, AD, LN>() * kLanes * sizeof(double);
-    return (matrix_sums<K, AD>() ? kJtBytes + (size_t)K * (K + 1) * sizeof(double) : 0) +
-           (a > b ? a : b);
+    return (sums_over_tape<K, AD>() ? 0 : mx) + (a > b ? a : b);
 }
 
 // ... of a general-kernel launch (one point per lane; the fp64 audit at one)

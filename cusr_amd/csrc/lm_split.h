@@ -81,6 +81,9 @@ lm_pass_kernel(FitArgs fa) {
     double *jt = (double *)my_lds;
     if constexpr (GEN) {
         my_lds += kGenJtBytes;
+    } else if constexpr (sums_over_tape<K, AD>()) {
+        // the rows go to the Jacobian pass's tape bytes (x and slot rows first)
+        jt = (double *)(my_lds + (size_t)(fa.D + fa.slots) * P * kLanes * sizeof(R));
     } else if constexpr (matrix_sums<K, AD>()) {
 #pragma unroll
         for (int j = 0; j < kJtStride; ++j) jt[lane * kJtStride + j] = 0.0;

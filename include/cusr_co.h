@@ -207,17 +207,23 @@ static inline int co_tail_resolve(const CoOptions *o, int N, int *tail_parts) {
     return (t > 0 && t < o->max_iter) ? t : 0;
 }
 
-/* Forward-AD fits of expressions with K >= CO_SUMS_MATRIX_MIN_K form their
- * sums with the fp64 matrix instruction (v_mfma_f64_16x16x4): the augmented
- * Jacobian rows [J | r] of a partition's points are multiplied into one
- * 16 x 16 accumulator, which adds the products of each entry with one fused
+/* Forward-AD fits of expressions with K >= CO_SUMS_MATRIX_MIN_K, and
+ * reverse-AD fits with K >= CO_SUMS_MATRIX_MIN_K_REV, form their sums with
+ * the fp64 matrix instruction (v_mfma_f64_16x16x4): the augmented Jacobian
+ * rows [J | r] of a partition's points are multiplied into one 16 x 16
+ * accumulator, which adds the products of each entry with one fused
  * multiply-add per point in ascending point order (no per-lane split, no
  * butterfly). For K = 16 the r column does not fit: r^2 and J^T r then keep
  * the per-lane order. Part of the arithmetic order, so the CPU oracle
- * follows the same rule. (Below the threshold, and in reverse mode, whose
- * LDS tape already limits occupancy, the per-lane sums are faster.) */
+ * follows the same rule. (Below the thresholds the per-lane sums are
+ * faster. In reverse mode the staged rows share the LDS of the tape, which
+ * the reverse sweep has consumed by then, so they cost no LDS, and they free
+ * the registers of the per-lane sums.) */
 #ifndef CO_SUMS_MATRIX_MIN_K
 #define CO_SUMS_MATRIX_MIN_K 13
+#endif
+#ifndef CO_SUMS_MATRIX_MIN_K_REV
+#define CO_SUMS_MATRIX_MIN_K_REV 15
 #endif
 
 /* --- reference ABI (cusr/kernel/co_lib.h:45-71) ------------------------ */

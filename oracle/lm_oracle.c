@@ -468,11 +468,12 @@ typedef struct {
  * partitions' sums are added in order 0, 1, ..., G-1 at the end. Within a
  * partition:
  *   - value-only passes, and Jacobian passes of the fast kernels with smaller
- *     K or reverse AD: point i goes to lane i mod 64, which sums its points
+ *     K: point i goes to lane i mod 64, which sums its points
  *     in ascending order from 0.0 with fma; the lanes combine with strides
  *     32..1;
  *   - Jacobian passes of the fast kernels in forward AD with
- *     K >= CO_SUMS_MATRIX_MIN_K: every entry of [J | r]^T [J | r] is one fma
+ *     K >= CO_SUMS_MATRIX_MIN_K, or in reverse AD with
+ *     K >= CO_SUMS_MATRIX_MIN_K_REV: every entry of [J | r]^T [J | r] is one fma
  *     chain over the partition's points in ascending order (the matrix
  *     instruction's order); for K = 16, r^2 and J^T r keep the lane order;
  *   - Jacobian passes of the general kernel (either AD mode, any K): every
@@ -482,7 +483,8 @@ static void orc_pass(const Tree *t, int N, int D, const double *xs, const double
     int K = t->K;
     int nq = K * (K + 1) / 2;
     int width = 1 + K + nq;
-    const int mx = jac != 0 && (t->general || (jac == 1 && K >= CO_SUMS_MATRIX_MIN_K));
+    const int mx = jac != 0 && (t->general || (jac == 1 && K >= CO_SUMS_MATRIX_MIN_K) ||
+                                (jac == 2 && K >= CO_SUMS_MATRIX_MIN_K_REV));
     const int full = t->general || K < 16;  /* r is a column of the product */
     const int ncol = full ? K + 1 : 16;     /* columns of the matrix product */
     const int lane_w = mx ? (full ? 0 : 1 + K) : width;

@@ -289,6 +289,55 @@ def test_general_sums_are_one_chain_per_entry(kind, ad_mode, G):
     assert checked >= 4
 
 
+@pytest.mark.parametrize("K", [15, 16])
+def test_reverse_high_k_sums_are_one_chain_per_entry(K):
+    """Fast-kernel expressions in reverse AD with K >= CO_SUMS_MATRIX_MIN_K_REV
+    (15): every J^T J entry is one fused multiply-add chain over the points in
+    ascending order (the matrix instruction's order); with K = 15, r^2 and
+    J^T r too (r is a column of the product), with K = 16 they keep the lane
+    order (lane l folds points l, l+64, ... from 0.0; lanes combine with
+    strides 32..1). Restated with exact rational arithmetic, so the lane order
+    where the chain belongs (or the reverse) fails it bit for bit."""
+    pop, _ = synth("C3", 96, 150)
+    x = pop["xs"].astype(np.float64)
+    checked = 0
+    for m in range(pop["M"]):
+        if int(pop["metas"][m][3]) != K or checked >= 2:
+            continue
+        off = int(pop["metas"][m][2])
+        c = pop["c_init"][off:off + K].astype(np.float64)
+        y = pop["ym"][m].astype(np.float64)
+        sub = popio.select_pop(pop, [m])
+        J = lm_oracle.jacobian(sub, c=c, xs=x, ad_mode=1)[0]
+        r = lm_oracle.eval_pop(sub, c=c, xs=x)[0] - y
+        aug = np.concatenate([J, r[:, None]], axis=1)
+        n = len(r)
+        chain = np.zeros((K + 1, K + 1))
+        for a_ in range(K + 1):
+            for b_ in range(a_, K + 1):
+                acc = 0.0
+                for i in range(n):
+                    acc = _fma(aug[i, a_], aug[i, b_], acc)
+                chain[a_, b_] = acc
+        loss, jtj, jtr = lm_oracle.pass_sums(pop, m, c, xs=x, y=y, ad_mode=1, partitions=1)
+        assert np.array_equal(np.triu(jtj), np.triu(chain[:K, :K]))
+        if K < 16:
+            assert loss == 0.5 * chain[K, K]
+            assert np.array_equal(jtr, chain[:K, K])
+        else:
+            def lane_order(col_a, col_b):
+                v = [0.0] * 64
+                for i in range(n):
+                    v[i % 64] = _fma(aug[i, col_a], aug[i, col_b], v[i % 64])
+                for st in (32, 16, 8, 4, 2, 1):
+                    v = [v[l] + v[l ^ st] for l in range(64)]
+                return v[0]
+            assert loss == 0.5 * lane_order(K, K)
+            assert np.array_equal(jtr, [lane_order(j, K) for j in range(K)])
+        checked += 1
+    assert checked >= 1
+
+
 def test_general_sums_match_textbook():
     """The same sums against numpy's J^T J and J^T r, K up to 32."""
     from tests.general_pops import general_pop
