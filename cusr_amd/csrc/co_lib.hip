@@ -131,6 +131,7 @@ struct Ctx {
     hipStream_t copy_stream = nullptr;   // uploads of a pipelined co_optimize
     bool shared_y = false;   // the resident y is one row for every expression
     bool on_data = false;    // the resident population fits the uploaded data set
+    bool dev_io = false;     // co_optimize_data_device: constants in, results out in device memory
     int data_N = -1, data_D = 0;  // shape of the uploaded data set (-1: none)
     double last_kernel_ms = -1.0;
     double last_bin_ms[CO_BINS] = {};
@@ -303,7 +304,10 @@ int upload_data(Ctx *ctx, const PopHeader *h, const void *c, const void *xs, con
         }
     } else {
         if (nY) CO_HIP(hipMemcpyAsync(ctx->Y.p, ym, 8 * nY, hipMemcpyHostToDevice, s));
-        if (C) CO_HIP(hipMemcpyAsync(ctx->C0.p, c, 8 * (size_t)C, hipMemcpyHostToDevice, s));
+        if (C)
+            CO_HIP(hipMemcpyAsync(ctx->C0.p, c, 8 * (size_t)C,
+                                  ctx->dev_io ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                  s));
     }
     return CO_OK;
 }
@@ -630,18 +634,13 @@ struct FitRun {
             CO_LAUNCH_HIP(hipStreamWaitEvent(s, ctx->ev_done[i], 0));
         }
         CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t1, s));
-        if (c_out && C)
-            CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, hipMemcpyDeviceToHost, s));
-        if (status_out)
-            CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M,
-                                  hipMemcpyDeviceToHost, s));
-        if (li_out)
-            CO_HIP(hipMemcpyAsync(li_out, ctx->li.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
-        if (lf_out)
-            CO_HIP(hipMemcpyAsync(lf_out, ctx->lf.p, 8 * (size_t)M, hipMemcpyDeviceToHost, s));
-        if (iters_out)
-            CO_HIP(hipMemcpyAsync(iters_out, ctx->iters.p, 4 * (size_t)M,
-                                  hipMemcpyDeviceToHost, s));
+        // co_optimize_data_device: the outputs are device memory of the caller
+        const hipMemcpyKind k = ctx->dev_io ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
+        if (c_out && C) CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, k, s));
+        if (status_out) CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M, k, s));
+        if (li_out) CO_HIP(hipMemcpyAsync(li_out, ctx->li.p, 8 * (size_t)M, k, s));
+        if (lf_out) CO_HIP(hipMemcpyAsync(lf_out, ctx->lf.p, 8 * (size_t)M, k, s));
+        if (iters_out) CO_HIP(hipMemcpyAsync(iters_out, ctx->iters.p, 4 * (size_t)M, k, s));
         CO_HIP(hipStreamSynchronize(s));
         float ms = 0.0f;
         CO_HIP(hipEventElapsedTime(&ms, ctx->ev_t0, ctx->ev_t1));
@@ -1105,6 +1104,37 @@ extern "C" int co_optimize_data(void *handle, const CoOptions *opt, const PopHea
     if (opt->struct_size != (int32_t)sizeof(CoOptions)) return CO_ERR_NULLARG;
     return fit_common((Ctx *)handle, *opt, h, nt, nv, ci, metas, c, nullptr, nullptr, false,
                       c_final_out, status_out, loss_init_out, loss_final_out, iters_out, true);
+}
+
+extern "C" int co_optimize_data_device(void *handle, const CoOptions *opt, const PopHeader *h,
+                                       const int32_t *nt, const float *nv, const int32_t *ci,
+                                       const TreeMeta *metas, const double *c_dev,
+                                       double *c_final_dev, int32_t *status_dev,
+                                       double *loss_init_dev, double *loss_final_dev,
+                                       int32_t *iters_dev) {
+    if (!handle || !opt || !h || !nt || !nv || !ci || !metas) return CO_ERR_NULLARG;
+    if (opt->struct_size != (int32_t)sizeof(CoOptions)) return CO_ERR_NULLARG;
+    Ctx *ctx = (Ctx *)handle;
+    const int M = h->M_prob, C = h->total_c;
+    if (M < 0 || C < 0) return CO_ERR_NULLARG;
+    if ((C > 0 && (!c_dev || !c_final_dev)) || (M > 0 && !status_dev)) return CO_ERR_NULLARG;
+    CO_HIP(hipSetDevice(ctx->device));
+    // every pointer that is given must be device memory of this handle's
+    // device covering its extent, checked before anything is copied
+    const size_t cb = sizeof(double) * (size_t)C, mb = sizeof(double) * (size_t)M,
+                 ib = sizeof(int32_t) * (size_t)M;
+    if ((C > 0 && (!on_device(c_dev, cb, ctx->device) || !on_device(c_final_dev, cb, ctx->device))) ||
+        (M > 0 && !on_device(status_dev, ib, ctx->device)) ||
+        (M > 0 && loss_init_dev && !on_device(loss_init_dev, mb, ctx->device)) ||
+        (M > 0 && loss_final_dev && !on_device(loss_final_dev, mb, ctx->device)) ||
+        (M > 0 && iters_dev && !on_device(iters_dev, ib, ctx->device)))
+        return CO_ERR_DATA;
+    ctx->dev_io = true;
+    const int rc = fit_common(ctx, *opt, h, nt, nv, ci, metas, c_dev, nullptr, nullptr, false,
+                              c_final_dev, status_dev, loss_init_dev, loss_final_dev, iters_dev,
+                              true);
+    ctx->dev_io = false;
+    return rc;
 }
 
 extern "C" int co_eval_ex(void *handle, const PopHeader *h, const int32_t *nt, const float *nv,

@@ -133,7 +133,8 @@ _HERE = Path(__file__).resolve().parent
 EXPORTED = ("co_init", "co_optimize", "co_last_split", "co_teardown", "co_options_default",
             "co_optimize_ex", "co_eval_ex", "co_upload_ex", "co_fit_resident",
             "co_last_kernel_ms", "co_last_bin_ms", "co_decode", "co_data_upload",
-            "co_optimize_data", "co_data_upload_device", "co_narrow_fp32",
+            "co_optimize_data", "co_data_upload_device", "co_optimize_data_device",
+            "co_narrow_fp32",
             "co_fit_resident_static")
 
 
@@ -210,6 +211,9 @@ def _bind(lib) -> None:
     lib.co_data_upload_device.restype = ctypes.c_int
     lib.co_optimize_data.argtypes = [_VP, ctypes.POINTER(CoOptions), ctypes.POINTER(PopHeader)] + [_VP] * 10
     lib.co_optimize_data.restype = ctypes.c_int
+    lib.co_optimize_data_device.argtypes = ([_VP, ctypes.POINTER(CoOptions),
+                                             ctypes.POINTER(PopHeader)] + [_VP] * 10)
+    lib.co_optimize_data_device.restype = ctypes.c_int
     lib.co_last_kernel_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
     lib.co_last_kernel_ms.restype = ctypes.c_int
     lib.co_last_bin_ms.argtypes = [_VP, ctypes.POINTER(dbl)]
@@ -543,6 +547,52 @@ class InProcessCO:
         out["c_final"] = out["c_final"][:C]
         for k in ("status", "loss_init", "loss_final", "iters"):
             out[k] = out[k][:M]
+        return out
+
+    def optimize_data_device(self, pop: dict, c_init, max_iter: int = 50, *,
+                             ad_mode: int = CO_AD_FORWARD, precision: int = CO_PREC_FP64,
+                             lambda0: float = 1e-3, xtol: float = 1e-6, fp64_guard: bool = True,
+                             partitions: int = 0, lm_order: int | None = None,
+                             f32_range: bool = False) -> dict:
+        """optimize_data with the constants and results on the device
+        (co_optimize_data_device): c_init is a float64 CUDA tensor of
+        total_c values; returns CUDA tensors c_final (float64), status
+        (int32), loss_init, loss_final (float64) and iters (int32) on its
+        device. The programs go from pop (host) as in optimize_data."""
+        import torch
+
+        self._check()
+        M, C = int(pop["M"]), int(pop["total_c"])
+        if (not isinstance(c_init, torch.Tensor) or not c_init.is_cuda
+                or c_init.dtype != torch.float64 or c_init.numel() != C):
+            raise ValueError(f"c_init must be a float64 CUDA tensor of {C} values")
+        dev = c_init.device
+        c0 = c_init.contiguous()
+        h = _header(pop)
+        o = default_options(ad_mode=int(ad_mode), precision=int(precision),
+                            max_iter=int(max_iter), lambda0=float(lambda0), xtol=float(xtol),
+                            fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
+                            f32_range=1 if f32_range else 0)
+        o.lm_order = self.default_order if lm_order is None else int(lm_order)
+        nt, pnt = _arr(pop["nt"], np.int32)
+        nv, pnv = _arr(pop["nv"], np.float32)
+        ci, pci = _arr(pop["ci"], np.int32)
+        me, pme = _metas(pop)
+        out = {"c_final": torch.empty(C, dtype=torch.float64, device=dev),
+               "status": torch.empty(M, dtype=torch.int32, device=dev),
+               "loss_init": torch.empty(M, dtype=torch.float64, device=dev),
+               "loss_final": torch.empty(M, dtype=torch.float64, device=dev),
+               "iters": torch.empty(M, dtype=torch.int32, device=dev)}
+        # the library copies on its own stream: torch's work on these tensors
+        # (the allocations, c_init's producer) is complete first
+        torch.cuda.synchronize(dev)
+        ptr = lambda t: ctypes.c_void_p(t.data_ptr() if t.numel() else 0)  # noqa: E731
+        rc = self._lib.co_optimize_data_device(
+            self._handle, ctypes.byref(o), ctypes.byref(h), pnt, pnv, pci, pme, ptr(c0),
+            *(ptr(out[k]) for k in ("c_final", "status", "loss_init", "loss_final", "iters")))
+        if rc != CO_OK:
+            raise COError(rc, "co_optimize_data_device")
+        self._resident = (M, C)
         return out
 
     def fit_resident(self, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,

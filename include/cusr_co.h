@@ -355,6 +355,25 @@ int co_optimize_data(void *handle, const CoOptions *opt, const PopHeader *header
                      double *loss_init_out, double *loss_final_out,
                      int32_t *iters_out);
 
+/* co_optimize_data with the constants and the results in device memory of the
+ * caller (torch CUDA tensors): c_dev (total_c doubles) is read and
+ * c_final_dev, status_dev and the optional loss_init_dev, loss_final_dev,
+ * iters_dev are written device to device; the call returns when they are
+ * complete. Only the programs (nt, nv, ci, metas) come from host memory,
+ * decoded there. No counterpart in the reference: it is the device-I/O step of
+ * the zero-copy in-process route its plan names as the end state
+ * (docs/kernel/INPROCESS_CO_PLAN.md:69-75), for GP loops that keep their
+ * populations' constants on the GPU. A given pointer that is not device
+ * memory of the handle's device, or whose extent runs past its allocation,
+ * returns CO_ERR_DATA before anything is copied; other codes as
+ * co_optimize_data. */
+int co_optimize_data_device(void *handle, const CoOptions *opt, const PopHeader *header,
+                            const int32_t *nt, const float *nv, const int32_t *ci,
+                            const TreeMeta *metas, const double *c_dev,
+                            double *c_final_dev, int32_t *status_dev,
+                            double *loss_init_dev, double *loss_final_dev,
+                            int32_t *iters_dev);
+
 /* Device time of the last fit on the handle, from HIP events recorded on the
  * handle's stream before the first and after the last fit kernel. */
 int co_last_kernel_ms(void *handle, double *fit_ms_out);

@@ -9,7 +9,11 @@ uploads one data set from host arrays and from CUDA tensors, and checks:
   * the fits against both are equal bit for bit;
   * host memory passed as device pointers is refused with CO_ERR_DATA and the
     previous data set stays;
-  * shapes that do not match raise ValueError.
+  * shapes that do not match raise ValueError;
+  * the fit with constants in and results out in device memory
+    (co_optimize_data_device) equals the host-buffer fit bit for bit, and
+    host memory passed as the constants is refused with CO_ERR_DATA before
+    anything is written.
 Prints "torch interop ok" on success, exits non-zero otherwise.
 """
 import ctypes
@@ -54,6 +58,31 @@ def main():
             raise AssertionError("mismatched shapes accepted")
         except ValueError:
             pass
+        # constants in and results out in device memory (co_optimize_data_device)
+        c_dev = torch.from_numpy(pop["c_init"].astype(np.float64)).to(dev)
+        dout = co.optimize_data_device(pop, c_dev, 20)
+        for k in ("c_final", "status", "loss_init", "loss_final", "iters"):
+            assert dout[k].is_cuda, k
+            assert np.array_equal(dout[k].cpu().numpy(), want[k], equal_nan=True), k
+        assert torch.equal(c_dev.cpu(), torch.from_numpy(pop["c_init"].astype(np.float64)))
+        # host memory passed as the constants is refused before anything is
+        # copied (the outputs stay as they were)
+        h = ci._header(pop)
+        o = ci.default_options(max_iter=20)
+        o.lm_order = co.default_order
+        keep = [ci._arr(pop["nt"], np.int32), ci._arr(pop["nv"], np.float32),
+                ci._arr(pop["ci"], np.int32), ci._metas(pop)]
+        C, M = int(pop["total_c"]), int(pop["M"])
+        hc = np.ascontiguousarray(pop["c_init"].astype(np.float64))
+        st = torch.full((M,), -5, dtype=torch.int32, device=dev)
+        cf = torch.full((C,), 7.0, dtype=torch.float64, device=dev)
+        vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        rc = co._lib.co_optimize_data_device(co._handle, ctypes.byref(o), ctypes.byref(h),
+                                             *(k[1] for k in keep),
+                                             hc.ctypes.data_as(ctypes.c_void_p), vp(cf), vp(st),
+                                             None, None, None)
+        assert rc == ci.CO_ERR_DATA, rc
+        assert bool((cf.cpu() == 7.0).all()) and bool((st.cpu() == -5).all())
     finally:
         co.teardown()
     print("torch interop ok", flush=True)
