@@ -186,6 +186,25 @@ def test_high_k_matrix_sums(co, ad_mode, parts):
     assert st >= 0.99
 
 
+@pytest.mark.parametrize("parts", [0, 8])
+def test_high_k_reverse_mixed_matrix_sums(co, parts):
+    """Mixed precision in reverse AD up to K = 16: from K = 15 the fp32
+    Jacobian rows are staged as doubles over the fp32 tape's LDS for the
+    matrix-instruction sums; in-workgroup (parts 0) and on the split path
+    (parts 8, one workgroup per partition)."""
+    pop, _ = synth("C3", 128, 700)
+    K = np.array([int(m[3]) for m in pop["metas"]])
+    assert np.sum(K >= 15) >= 4
+    g, o = _fit_both(co, pop, 12, ad_mode=1, precision=1, partitions=parts)
+    st, d = _report(g, o)
+    hk = K >= 15
+    _say(f"mixed reverse high K, parts {parts}: status agree {st:.4f}; loss rel max "
+         f"{d.max():.3e}; K >= 15 rel max {d[hk].max():.3e}")
+    assert np.mean(d <= 1e-4) >= 0.99
+    assert np.all(d[hk] <= 1e-4)
+    assert st >= 0.98
+
+
 @pytest.mark.parametrize("ad_mode,precision,tail_iter,tail_parts,lm_order", [
     (0, 0, 0, 0, 0), (0, 0, 3, 2, 0), (1, 0, 5, 4, 0), (0, 1, 4, 4, 0), (0, 0, 6, 4, 1),
     (0, 0, -1, 0, 0)])
