@@ -1,7 +1,7 @@
 """Benchmark of the batched LM fitter.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-cpu]
-                    [--rounds R] [--tiled] [--copy-calibration]
+                    [--rounds R] [--tiled] [--copy-calibration] [--configs C3,C4,C5]
 
 Default (the headline metric): one step = one full LM fit (all iterations,
 on-device accept/reject) of the synthetic C2 population: 16,384 seeded
@@ -14,6 +14,14 @@ rounds of fresh 65,536-expression populations (generated untimed), each timed
 end to end from host buffers (upload, 10 mixed-precision iterations,
 read-back), the per-round latency being the step; the round's one target goes
 over as a shared row (pop.bin v2), or tiled per expression with --tiled.
+
+configs: the default (C2) run also measures the other configurations after
+the headline line's own work, each briefly and without a CPU leg -- C3 and C4
+resident (1 warm-up, 2 timed fits), C5 as 2 rounds from host buffers -- and
+adds them as a `configs` block of the same JSON line: per configuration the
+ms per step, fits/s, the dominant launch's kernel, its duration alone and
+beside the other bins, and its algorithmic TFLOP/s against the vector peak.
+`--configs ""` leaves the block out.
 
 roofline: the roof that binds the dominant launch (the K bin whose fit
 kernel runs longest) is VALU issue ("bound": "valu"): its algorithmic flops
@@ -138,9 +146,8 @@ def cpu_baseline(pop, gpu_c_final, repeats=3, target_s=15.0, quality_s=8.0):
     nc = int(np.sum(qpop["metas"][:, 3]))
     serial = ScipyPop(nproc=1)
     try:
-        cache = REPO / "gpurun_out" / "oracle_cache"
         orc = runner.cached_oracle(qpop, lambda p: serial.fit_pop(p)["c_final"],
-                                   lambda c: interp.loss_pop(qpop, c), cache)
+                                   lambda c: interp.loss_pop(qpop, c))
     finally:
         serial.close()
     K = qpop["metas"][:, 3]
@@ -444,6 +451,60 @@ def run_rounds(args, cfg, co, gen):
     return value, float(np.mean(lat)), roof, fit, pop, res
 
 
+def make_gen(cfg, co):
+    """Population generator of a configuration, targets from the device evaluator."""
+    from cusr_amd.benchmark import gen_synth
+
+    def gen(round_index=0):
+        t = time.perf_counter()
+        pop, _ = gen_synth.generate(cfg, lambda p, c, xs: co.evaluate(p, c, xs),
+                                    round_index=round_index)
+        _say(f"generated {cfg.name} round {round_index}: M={pop['M']} N={pop['N']} "
+             f"nodes={pop['total_nodes']} K_max={pop['K_max']} in {time.perf_counter() - t:.1f}s")
+        return pop
+
+    return gen
+
+
+def config_block(co, names, base_args):
+    """The other configurations, measured briefly beside the headline (no CPU
+    leg): C1-C4 resident, 1 warm-up and 2 timed fits; C5 2 rounds from host
+    buffers. Returns {name: summary}."""
+    from cusr_amd.benchmark import gen_synth
+
+    out = {}
+    for name in names:
+        cfg = gen_synth.CONFIGS[name]
+        a = argparse.Namespace(**vars(base_args))
+        a.steps, a.warmup, a.rounds, a.no_e2e = 2, 1, 2, True
+        a.alone_reps, a.partitions, a.copy_calibration, a.tiled = 3, 0, False, False
+        t0 = time.perf_counter()
+        gen = make_gen(cfg, co)
+        if cfg.rounds > 1:
+            value, ms, roof, fit, pop, res = run_rounds(a, cfg, co, gen)
+            steps, what = a.rounds, "rounds from host buffers (upload, fit, read-back)"
+        else:
+            pop = gen()
+            value, ms, roof, fit, res = run_resident(a, cfg, co, pop)
+            steps, what = a.steps, "fits of the HBM-resident population"
+        out[name] = {
+            "workload": workload_text(cfg, pop), "steps": steps, "warmup": 1, "timed": what,
+            "ms_per_step": ms, "value": value, "unit": "fits/s",
+            "dtype": "f64" if cfg.precision == 0 else "f32+f64",
+            "dominant_kernel": roof["kernel"], "dominant_bin": roof["bin"],
+            "dominant_alone_ms": roof["launch_ms"],
+            "dominant_concurrent_ms": roof["launch_ms_concurrent"],
+            "achieved_tflops": roof["achieved"], "peak_tflops": roof["peak"],
+            "frac": roof["frac"],
+            "status_counts": np.bincount(res["status"], minlength=5).tolist(),
+            "mean_iters": float(res["iters"].mean()),
+            "wall_s": time.perf_counter() - t0}
+        _say(f"config {name}: {ms:.2f} ms per step, {value:.0f} fits/s, dominant "
+             f"{roof['kernel']} alone {roof['launch_ms']:.3f} ms, {roof['achieved']:.2f} TFLOP/s")
+        del pop, res
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -462,6 +523,9 @@ def main():
                     help="also run one copy kernel of known size (for rocprofv3 --pmc scaling)")
     ap.add_argument("--alone-reps", type=int, default=3,
                     help="launches of the dominant bin alone (the roofline's duration)")
+    ap.add_argument("--configs", default=None,
+                    help="comma-separated configurations measured briefly after the main "
+                         "one (default: C3,C4,C5 when --config is C2; '' for none)")
     ap.add_argument("--partitions", type=int, default=0,
                     help="point partitions per expression (0: by N and AD mode, co_partitions_for; "
                          "above 4 the split path)")
@@ -479,14 +543,7 @@ def main():
         cfg = gen_synth.scaled(cfg)
         cfg.ad_mode = args.ad_mode
     co = co_inproc.get_inproc_co(0, "ad")
-
-    def gen(round_index=0):
-        t = time.perf_counter()
-        pop, _ = gen_synth.generate(cfg, lambda p, c, xs: co.evaluate(p, c, xs),
-                                    round_index=round_index)
-        _say(f"generated {cfg.name} round {round_index}: M={pop['M']} N={pop['N']} "
-             f"nodes={pop['total_nodes']} K_max={pop['K_max']} in {time.perf_counter() - t:.1f}s")
-        return pop
+    gen = make_gen(cfg, co)
 
     if cfg.rounds > 1:
         value, ms_per_step, roof, fit, pop, res = run_rounds(args, cfg, co, gen)
@@ -501,6 +558,11 @@ def main():
         cpu = cpu_baseline(pop, res["c_final"])
         _say(f"cpu baseline {cpu['value']:.1f} fits/s on {cpu['cores']} cores; quality "
              + json.dumps(cpu["quality"]))
+
+    names = args.configs
+    if names is None:
+        names = "C3,C4,C5" if args.config == "C2" and args.ad_mode is None else ""
+    others = config_block(co, [n for n in names.split(",") if n], args) if names else None
 
     metric = HEADLINE_METRIC if cfg.name == "C2" else \
         f"expressions fitted/sec ({cfg.name}) + achieved HBM GB/s"
@@ -523,6 +585,8 @@ def main():
         "cpu_baseline": cpu,
         "fit": fit,
     }
+    if others:
+        line["configs"] = others
     print(json.dumps(line), flush=True)
 
 

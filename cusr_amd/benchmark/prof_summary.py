@@ -5,12 +5,18 @@
     python -m cusr_amd.benchmark.prof_summary pmc    <run_results.db> [--match lm_fit]
     python -m cusr_amd.benchmark.prof_summary valu   <run_results.db> [--match lm_fit]
            [--out JSON --workload-key KEY] [--last]
+    python -m cusr_amd.benchmark.prof_summary resources [--match lm_] [--resources JSON]
     python -m cusr_amd.benchmark.prof_summary traffic <fetch.db> <write.db> --kernel NAME
            --calib-fetch-bytes F --calib-write-bytes W [--out JSON --workload-key KEY]
            [--last]
 
 trace: per kernel, calls and average / min / max / total duration plus the
-register and grid figures of the dispatch. pmc: per kernel, the average of
+grid of the dispatch and the kernel's registers, spills and scratch bytes per
+lane from the compiler's resource-usage remarks of the build
+(cusr_amd/kernel/kernel_resources.json, written by cusr_amd/build.py; rocpd's
+register figures count the gfx950 VGPR allocation in granules of 4 where the
+hardware allocates 8, so the code object's figure is taken from the build).
+resources: that table for the fit and pass kernels alone. pmc: per kernel, the average of
 every counter per dispatch. valu: the same as JSON, with each kernel's
 dispatch duration (counter runs serialise dispatches). traffic: HBM bytes per dispatch of each matching kernel from
 a FETCH_SIZE run and a WRITE_SIZE run, each scaled by the ratio of the known
@@ -25,6 +31,26 @@ import collections
 import json
 import sqlite3
 import statistics
+from pathlib import Path
+
+RESOURCES = Path(__file__).resolve().parents[1] / "kernel" / "kernel_resources.json"
+
+
+def load_resources(path=None) -> dict:
+    """{demangled kernel name: resource fields} of the build (empty if absent)."""
+    p = Path(path) if path else RESOURCES
+    if not p.exists():
+        return {}
+    return {v["name"]: v for v in json.loads(p.read_text()).values()}
+
+
+def _res_for(res: dict, name: str):
+    if name in res:
+        return res[name]
+    for k, v in res.items():          # rocpd may drop the return type or arguments
+        if name in k or k in name:
+            return v
+    return None
 
 
 def _rows(db, sql):
@@ -35,9 +61,10 @@ def _rows(db, sql):
         con.close()
 
 
-def trace(db, match=None, skip=0, take=None):
+def trace(db, match=None, skip=0, take=None, resources=None):
     """skip / take: per kernel, drop its first `skip` dispatches and keep the
     next `take` (a benchmark's timed steps after its warm-up)."""
+    res = load_resources(resources)
     rows = _rows(db, "select name, duration, vgpr_count, accum_vgpr_count, sgpr_count, "
                      "scratch_size, lds_size, grid_x, workgroup_x from kernels "
                      "order by dispatch_id")
@@ -53,12 +80,36 @@ def trace(db, match=None, skip=0, take=None):
         by[name].append(dur / 1e6)
         meta[name] = (vg, ag, sg, scr, lds, gx // max(wx, 1))
     out = ["| kernel | calls | avg ms | min ms | max ms | total ms | VGPR | AGPR | SGPR "
-           "| scratch B | LDS B | workgroups |", "|" + "---|" * 12]
+           "| VGPR spill | scratch B/lane | waves/SIMD | LDS B | workgroups |", "|" + "---|" * 14]
     for name in sorted(by, key=lambda n: -sum(by[n])):
         d = by[name]
         vg, ag, sg, scr, lds, wg = meta[name]
+        r = _res_for(res, name)
+        if r:
+            vg, ag, sg = r.get("vgpr", vg), r.get("agpr", ag), r.get("sgpr", sg)
+            sp, scr, occ = r.get("vgpr_spill", "?"), r.get("scratch_bytes_per_lane", scr), \
+                r.get("waves_per_simd", "?")
+        else:
+            sp, occ = "?", "?"
         out.append(f"| `{name}` | {len(d)} | {statistics.mean(d):.3f} | {min(d):.3f} | "
-                   f"{max(d):.3f} | {sum(d):.2f} | {vg} | {ag} | {sg} | {scr} | {lds} | {wg} |")
+                   f"{max(d):.3f} | {sum(d):.2f} | {vg} | {ag} | {sg} | {sp} | {scr} | {occ} "
+                   f"| {lds} | {wg} |")
+    return "\n".join(out)
+
+
+def resources_table(match=None, resources=None):
+    """The build's per-kernel registers, spills, scratch and occupancy."""
+    res = load_resources(resources)
+    out = ["| kernel | VGPR | AGPR | SGPR | VGPR spill | SGPR spill | scratch B/lane | "
+           "waves/SIMD | static LDS B |", "|" + "---|" * 9]
+    for name in sorted(res):
+        if match and match not in name:
+            continue
+        r = res[name]
+        out.append(f"| `{name}` | {r.get('vgpr')} | {r.get('agpr')} | {r.get('sgpr')} | "
+                   f"{r.get('vgpr_spill')} | {r.get('sgpr_spill')} | "
+                   f"{r.get('scratch_bytes_per_lane')} | {r.get('waves_per_simd')} | "
+                   f"{r.get('static_lds_bytes')} |")
     return "\n".join(out)
 
 
@@ -158,8 +209,11 @@ def traffic(fetch_db, write_db, kernel, calib_fetch, calib_write, last=False):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["trace", "pmc", "traffic", "valu"])
-    ap.add_argument("dbs", nargs="+")
+    ap.add_argument("mode", choices=["trace", "pmc", "traffic", "valu", "resources"])
+    ap.add_argument("dbs", nargs="*")
+    ap.add_argument("--resources", default=None,
+                    help="trace, resources: the build's kernel_resources.json (default: "
+                         "the one next to the library)")
     ap.add_argument("--match", default=None)
     ap.add_argument("--kernel", default=None)
     ap.add_argument("--calib-fetch-bytes", type=float, default=None)
@@ -177,8 +231,10 @@ def main():
                     help="valu: averages over each kernel's last TAIL dispatches (the "
                          "split path: 1 + max_iter pass launches are one fit of a bin)")
     a = ap.parse_args()
-    if a.mode == "trace":
-        print(trace(a.dbs[0], a.match, a.skip, a.take))
+    if a.mode == "resources":
+        print(resources_table(a.match, a.resources))
+    elif a.mode == "trace":
+        print(trace(a.dbs[0], a.match, a.skip, a.take, a.resources))
     elif a.mode == "pmc":
         print(pmc(a.dbs[0], a.match))
     elif a.mode == "valu":

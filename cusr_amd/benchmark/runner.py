@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import hashlib
 import json
+import os
 import socket
 import time
 from datetime import datetime
@@ -86,7 +87,17 @@ def pop_sha(pop: dict) -> str:
     return h.hexdigest()[:16]
 
 
-def cached_oracle(pop: dict, fit_serial, score, cache_dir, limit: int | None = None) -> dict:
+def default_cache_dir() -> Path:
+    """Where the harness keeps its serial-oracle cache: $CUSR_CACHE_DIR, else
+    $XDG_CACHE_HOME/cusr_amd/oracle, else ~/.cache/cusr_amd/oracle. Outside
+    the repository, so results and scratch folders never hold it."""
+    if os.environ.get("CUSR_CACHE_DIR"):
+        return Path(os.environ["CUSR_CACHE_DIR"])
+    base = os.environ.get("XDG_CACHE_HOME") or str(Path.home() / ".cache")
+    return Path(base) / "cusr_amd" / "oracle"
+
+
+def cached_oracle(pop: dict, fit_serial, score, cache_dir=None, limit: int | None = None) -> dict:
     """The tight serial oracle of a population, cached by (population sha1,
     limit) as the reference caches it by file sha1 (cusr/benchmark/runner.py:
     111-128): fit_serial(pop) -> c_final (a serial fit, reproducible bit for
@@ -95,7 +106,7 @@ def cached_oracle(pop: dict, fit_serial, score, cache_dir, limit: int | None = N
     filled the cache) and cached."""
     if limit is not None:
         pop = popio.slice_pop(pop, limit)
-    cache_dir = Path(cache_dir)
+    cache_dir = Path(cache_dir) if cache_dir is not None else default_cache_dir()
     path = cache_dir / f"oracle_{pop_sha(pop)}_L{limit or 'all'}_serial.npz"
     if path.exists():
         z = np.load(path)

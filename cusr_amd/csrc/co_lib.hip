@@ -1073,6 +1073,10 @@ extern "C" int co_data_upload_device(void *handle, int N, int n_vars, const doub
                   (n_vars > 0 && !on_device(xs_dev, sizeof(double) * (size_t)N * n_vars,
                                             ctx->device))))
         return CO_ERR_DATA;
+    // the caller's producer of xs_dev / y_dev may still be queued on a stream
+    // of its own: every stream of the process drains before the library's
+    // non-blocking streams read that memory
+    CO_HIP(hipDeviceSynchronize());
     ctx->data_N = -1;   // no data set until this upload completes
     if (ctx->on_data) ctx->resident = false;
     const size_t nX = (size_t)N * n_vars;
@@ -1129,6 +1133,10 @@ extern "C" int co_optimize_data_device(void *handle, const CoOptions *opt, const
         (M > 0 && loss_final_dev && !on_device(loss_final_dev, mb, ctx->device)) ||
         (M > 0 && iters_dev && !on_device(iters_dev, ib, ctx->device)))
         return CO_ERR_DATA;
+    // c_dev's producer, and earlier users of the output buffers, may still be
+    // queued on the caller's streams: they finish before the library's
+    // non-blocking streams read or write that memory
+    CO_HIP(hipDeviceSynchronize());
     ctx->dev_io = true;
     const int rc = fit_common(ctx, *opt, h, nt, nv, ci, metas, c_dev, nullptr, nullptr, false,
                               c_final_dev, status_dev, loss_init_dev, loss_final_dev, iters_dev,

@@ -331,9 +331,11 @@ int co_data_upload(void *handle, int N, int n_vars, const double *xs, const doub
 /* co_data_upload from device memory: xs_dev (N * n_vars fp64, row-major) and
  * y_dev (N fp64) are device pointers on the handle's device, such as the data
  * of torch CUDA tensors. They are copied device to device (X transposed on the
- * device), so the data set never crosses PCIe. The caller's data must be
- * complete when called (synchronize the stream that produced it); the
- * library does not keep the pointers. No counterpart in the reference: it is
+ * device), so the data set never crosses PCIe. Before reading them the call
+ * waits for all work the process has queued on the device
+ * (hipDeviceSynchronize), so data written by a kernel still queued on any of
+ * the caller's streams is complete when it is read; the library does not keep
+ * the pointers. No counterpart in the reference: it is
  * the data-residency half of the zero-copy entry its in-process plan
  * describes as the end state (docs/kernel/INPROCESS_CO_PLAN.md:69-75).
  * Returns as co_data_upload, and CO_ERR_DATA when a pointer is not device
@@ -360,7 +362,11 @@ int co_optimize_data(void *handle, const CoOptions *opt, const PopHeader *header
  * c_final_dev, status_dev and the optional loss_init_dev, loss_final_dev,
  * iters_dev are written device to device; the call returns when they are
  * complete. Only the programs (nt, nv, ci, metas) come from host memory,
- * decoded there. No counterpart in the reference: it is the device-I/O step of
+ * decoded there. Before it reads c_dev or writes an output, the call waits for
+ * all work the process has queued on the device (hipDeviceSynchronize): a
+ * producer of c_dev, or a reader of the output buffers, still queued on any
+ * of the caller's streams finishes first, so no stream ordering is left to
+ * the caller. No counterpart in the reference: it is the device-I/O step of
  * the zero-copy in-process route its plan names as the end state
  * (docs/kernel/INPROCESS_CO_PLAN.md:69-75), for GP loops that keep their
  * populations' constants on the GPU. A given pointer that is not device

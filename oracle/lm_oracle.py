@@ -6,13 +6,16 @@ and numpy arrays, and return numpy arrays. Data and constants are fp64.
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 _HERE = Path(__file__).resolve().parent
-_LIB_PATH = _HERE / "liblm_oracle.so"
+# CUSR_ORACLE_LIB names another build of the oracle (the mutation gate,
+# oracle/mutation_gate.py, points the tests at mutant builds)
+_LIB_PATH = Path(os.environ.get("CUSR_ORACLE_LIB") or (_HERE / "liblm_oracle.so"))
 _lib = None
 
 CO_AD_FORWARD, CO_AD_REVERSE = 0, 1

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import lm_oracle
-from tests.helpers import f64, ref_pop, rel_diff, synth
+from tests.helpers import assert_parity, f64, ref_pop, rel_diff, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -25,12 +25,6 @@ def _fit_both(co, pop, max_iter, ad_mode=0, precision=0, partitions=0, **kw):
     o = lm_oracle.fit(pop, max_iter=max_iter, ad_mode=ad_mode, precision=precision,
                       partitions=partitions, **kw)
     return g, o
-
-
-def _report(g, o):
-    st_agree = float(np.mean(g["status"] == o["status"]))
-    d = rel_diff(g["loss_final"], o["loss_final"])
-    return st_agree, d
 
 
 @pytest.mark.parametrize("name,M,N", [("C1", 256, 256), ("C2", 128, 512)])
@@ -53,27 +47,19 @@ def test_eval_matches_oracle(co, name, M, N):
 def test_fit_fp64_c1(co, ad_mode):
     pop, _ = synth("C1", 512, 256)
     g, o = _fit_both(co, pop, 20, ad_mode=ad_mode)
-    st, d = _report(g, o)
-    _say(f"status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
-    assert np.mean(d <= 1e-9) >= 0.999
-    assert st >= 0.999
+    assert_parity(g, o, 1e-9, f"C1 ad={ad_mode}", exact=True)
 
 
 def test_fit_fp64_c2_small(co):
     pop, _ = synth("C2", 256, 1024)
     g, o = _fit_both(co, pop, 50)
-    st, d = _report(g, o)
-    _say(f"status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
-    assert np.mean(d <= 1e-9) >= 0.999
-    assert st >= 0.996
+    assert_parity(g, o, 1e-9, "C2 small", exact=True)
 
 
 def test_fit_mixed_c5_small(co):
     pop, _ = synth("C5", 256, 512)
     g, o = _fit_both(co, pop, 10, precision=1)
-    st, d = _report(g, o)
-    _say(f"mixed: status agree {st:.4f}; loss rel max {d.max():.3e}")
-    assert np.mean(d <= 1e-4) >= 0.99
+    assert_parity(g, o, 1e-4, "C5 small mixed")
 
 
 def test_reference_fixture_recovers_truth(co):
@@ -142,12 +128,8 @@ def test_point_partitions_match_oracle(co, parts, ad_mode, precision):
     granule is ragged and partitions hold different granule counts)."""
     pop, _ = synth("C2", 96, 1000)
     g, o = _fit_both(co, pop, 15, ad_mode=ad_mode, precision=precision, partitions=parts)
-    st, d = _report(g, o)
-    _say(f"partitions {parts}: status agree {st:.4f}; loss rel max {d.max():.3e}; "
-         f"exact {np.mean(d == 0):.4f}")
     tol = 1e-9 if precision == 0 else 1e-4
-    assert np.mean(d <= tol) >= 0.99
-    assert st >= 0.98
+    assert_parity(g, o, tol, f"partitions {parts}", exact=precision == 0)
 
 
 def test_large_n_auto_partitions(co):
@@ -162,14 +144,10 @@ def test_large_n_auto_partitions(co):
     ln = (K >= 1) & (K <= 8)
     assert ((K == 5) | (K == 6)).sum() >= 6 and ((K == 7) | (K == 8)).sum() >= 4
     g, o = _fit_both(co, pop, 20)
-    st, d = _report(g, o)
-    _say(f"large N: status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}; "
-         f"large-N instances exact {np.mean(d[ln] == 0):.4f}; iters {g['iters'][ln].tolist()}")
+    _say(f"large-N instances: iters {g['iters'][ln].tolist()}")
     assert np.mean(g["iters"][ln] >= 2) >= 0.75
-    assert np.array_equal(g["loss_final"][ln], o["loss_final"][ln])
-    assert np.array_equal(g["status"][ln], o["status"][ln])
-    assert np.array_equal(g["c_final"], o["c_final"]) or np.mean(d <= 1e-9) >= 0.95
-    assert st >= 0.95
+    assert_parity(g, o, 1e-9, "large-N instances", exact=True, mask=ln)
+    assert_parity(g, o, 1e-9, "large N", exact=True)
 
 
 @pytest.mark.parametrize("ad_mode,parts", [(1, 0), (0, 0), (1, 2)])
@@ -180,10 +158,7 @@ def test_high_k_matrix_sums(co, ad_mode, parts):
     pop, _ = synth("C3", 128, 700)
     assert pop["K_max"] >= 13
     g, o = _fit_both(co, pop, 15, ad_mode=ad_mode, partitions=parts)
-    st, d = _report(g, o)
-    _say(f"high K: status agree {st:.4f}; loss rel max {d.max():.3e}; exact {np.mean(d == 0):.4f}")
-    assert np.mean(d <= 1e-9) >= 0.99
-    assert st >= 0.99
+    assert_parity(g, o, 1e-9, f"high K ad={ad_mode} parts={parts}", exact=True)
 
 
 @pytest.mark.parametrize("parts", [0, 8])
@@ -196,13 +171,16 @@ def test_high_k_reverse_mixed_matrix_sums(co, parts):
     K = np.array([int(m[3]) for m in pop["metas"]])
     assert np.sum(K >= 15) >= 4
     g, o = _fit_both(co, pop, 12, ad_mode=1, precision=1, partitions=parts)
-    st, d = _report(g, o)
     hk = K >= 15
-    _say(f"mixed reverse high K, parts {parts}: status agree {st:.4f}; loss rel max "
-         f"{d.max():.3e}; K >= 15 rel max {d[hk].max():.3e}")
-    assert np.mean(d <= 1e-4) >= 0.99
-    assert np.all(d[hk] <= 1e-4)
-    assert st >= 0.98
+    assert_parity(g, o, 1e-4, f"mixed reverse parts {parts}")
+    # the staged rows over the fp32 tape: the oracle models the same sums, so
+    # the K >= 15 expressions agree to the bit (a stale column or an LDS
+    # overlap would not)
+    assert_parity(g, o, 1e-4, f"mixed reverse K >= 15 parts {parts}", exact=True, mask=hk)
+    c_off = np.concatenate([[0], np.cumsum(K)])
+    for m in np.nonzero(hk)[0]:
+        a, b = c_off[m], c_off[m + 1]
+        assert np.array_equal(g["c_final"][a:b], o["c_final"][a:b]), m
 
 
 @pytest.mark.parametrize("ad_mode,precision,tail_iter,tail_parts,lm_order", [
@@ -217,22 +195,14 @@ def test_tail_segment_matches_oracle(co, ad_mode, precision, tail_iter, tail_par
     pop, _ = synth("C2", 160, 700)
     g, o = _fit_both(co, pop, 25, ad_mode=ad_mode, precision=precision, tail_iter=tail_iter,
                      tail_partitions=tail_parts, lm_order=lm_order)
-    st, d = _report(g, o)
-    _say(f"tail {tail_iter}/{tail_parts}: status agree {st:.4f}; loss rel max {d.max():.3e}; "
-         f"exact {np.mean(d == 0):.4f}; iters > tail {np.mean(g['iters'] > max(tail_iter, 0)):.2f}")
+    _say(f"iters > tail {np.mean(g['iters'] > max(tail_iter, 0)):.2f}")
     assert np.array_equal(g["iters"] > 0, o["iters"] > 0)
     tol = 1e-9 if precision == 0 else 1e-4
-    assert np.mean(d <= tol) >= 0.99
-    assert st >= 0.98
-    if precision == 0:
-        assert np.mean(g["c_final"] == o["c_final"]) >= 0.97
+    assert_parity(g, o, tol, f"tail {tail_iter}/{tail_parts}", exact=precision == 0)
 
 
 def test_tail_high_k_matrix_sums(co):
     """The tail with the matrix-instruction sums (forward AD, K >= 13)."""
     pop, _ = synth("C3", 96, 700)
     g, o = _fit_both(co, pop, 15, tail_iter=4, tail_partitions=4)
-    st, d = _report(g, o)
-    _say(f"tail high K: status agree {st:.4f}; loss rel max {d.max():.3e}")
-    assert np.mean(d <= 1e-9) >= 0.99
-    assert st >= 0.99
+    assert_parity(g, o, 1e-9, "tail high K", exact=True)

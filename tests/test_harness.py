@@ -70,14 +70,12 @@ def _harness_run(pop, label, c_true=None, nproc=16, repeats=3):
     """run_quality with the GPU (fp64 in process, the CLI) and the scipy port,
     against the serial scipy oracle cached by population hash."""
     import os
-    from pathlib import Path
     from oracle.scipy_pop import ScipyPop
 
     serial = ScipyPop(nproc=1, timeout=300)
     try:
-        cache = Path(os.environ.get("GRAFT_REPO_ROOT", ".")) / "gpurun_out" / "oracle_cache"
         orc = runner.cached_oracle(pop, lambda p: serial.fit_pop(p)["c_final"],
-                                   lambda c: interp.loss_pop(pop, c), cache)
+                                   lambda c: interp.loss_pop(pop, c))
     finally:
         serial.close()
     par = _Scipy(min(nproc, len(os.sched_getaffinity(0))))

@@ -574,3 +574,135 @@ def test_lm_orders_differ_as_the_reference_variants():
     fdg = lm_oracle.fit(pop, max_iter=5, xtol=1e3, lm_order=1, fp64_guard=1)
     assert np.all(fdg["loss_final"][live] <= fdg["loss_init"][live])
     assert np.all(fdg["status"][went_up] == 1)
+
+
+# ------------------------------------------- pins the mutation gate asked for
+
+def _pop1(nt, nv, ci, c0, xs, y):
+    return popio.build_pop([(nt, nv, ci, np.asarray(c0, np.float32))],
+                           np.asarray(xs, np.float32), np.asarray(y, np.float32)[None, :])
+
+
+@pytest.mark.parametrize("G", [3, 4])
+def test_fast_sums_follow_lanes_butterfly_and_partitions(G):
+    """Fast-kernel sums (forward AD, K below the matrix-sum threshold) in the
+    documented order: point i goes to partition (i // 64) mod G and lane
+    i mod 64, which folds its points in ascending order from 0.0 with fma; the
+    lanes of a partition combine at strides 32, 16, ..., 1 (lane l takes
+    p[l] + p[l ^ s]); the partition sums are then added in partition order.
+    Restated with exact rational arithmetic; N = 600 leaves the last granule
+    ragged. With G >= 3 a partition order other than 0, 1, ..., G-1 rounds
+    differently."""
+    pop, _ = synth("C2", 12, 600)
+    x = pop["xs"].astype(np.float64)
+    checked = 0
+    for m in range(pop["M"]):
+        K = int(pop["metas"][m][3])
+        if K < 2:
+            continue
+        off = int(pop["metas"][m][2])
+        c = pop["c_init"][off:off + K].astype(np.float64)
+        y = pop["ym"][m].astype(np.float64)
+        sub = popio.select_pop(pop, [m])
+        J = lm_oracle.jacobian(sub, c=c, xs=x)[0]
+        r = lm_oracle.eval_pop(sub, c=c, xs=x)[0] - y
+        W = 1 + K + K * (K + 1) // 2
+        total = None
+        for g in range(G):
+            lanes = np.zeros((64, W))
+            for i in range(len(r)):
+                if (i // 64) % G != g:
+                    continue
+                a = lanes[i % 64]
+                a[0] = _fma(r[i], r[i], a[0])
+                for j in range(K):
+                    a[1 + j] = _fma(J[i, j], r[i], a[1 + j])
+                q = 1 + K
+                for j1 in range(K):
+                    for j2 in range(j1, K):
+                        a[q] = _fma(J[i, j1], J[i, j2], a[q])
+                        q += 1
+            s = 32
+            while s >= 1:
+                for ln in range(64):
+                    if ln & s:
+                        continue
+                    v = lanes[ln] + lanes[ln ^ s]
+                    lanes[ln] = v
+                    lanes[ln ^ s] = v
+                s //= 2
+            total = lanes[0].copy() if total is None else total + lanes[0]
+        loss, jtj, jtr = lm_oracle.pass_sums(pop, m, c, xs=x, y=y, partitions=G)
+        assert loss == 0.5 * total[0]
+        assert np.array_equal(jtr, total[1:1 + K])
+        iu = np.triu_indices(K)
+        assert np.array_equal(jtj[iu], total[1 + K:])
+        checked += 1
+    assert checked >= 4
+
+
+# MUL(x0, SQRT(MUL(c0, x1))) and MAX with a SQRT(c0) operand, in prefix order
+_OP_MUL, _OP_MAX, _OP_SQRT = 3, 8, 27
+
+
+def test_reverse_zero_adjoint_times_infinite_partial_is_zero():
+    """safe_mul (revad_interp.cuh:45-56): at x0 = x1 = 0 the adjoint of
+    sqrt(c0 x1) is x0 = 0 and its partial 1 / (2 sqrt(0)) is +inf; the
+    reverse sweep's product is 0, so dF/dc0 = 0, where a plain product gives
+    NaN. At (1, 4): x1 / (2 sqrt(c0 x1)) = 4 / (2 sqrt 6)."""
+    pop = _pop1([3, 0, 2, 3, 1, 0], [_OP_MUL, 0, _OP_SQRT, _OP_MUL, 0, 1], [-1, -1, -1, -1, 0, -1],
+                [1.5], [[0.0, 0.0], [1.0, 4.0]], [0.0, 0.0])
+    J = lm_oracle.jacobian(pop, c=np.array([1.5]), xs=pop["xs"].astype(np.float64),
+                           ad_mode=1)[0]
+    assert J[0, 0] == 0.0
+    assert J[1, 0] == pytest.approx(4.0 / (2.0 * math.sqrt(6.0)), rel=1e-15)
+
+
+@pytest.mark.parametrize("ad_mode", [0, 1])
+def test_flat_branch_tangent_is_zero_not_nan(ad_mode):
+    """MAX with one operand on its flat side has partial exactly 0 there, and
+    the operand's derivative is dropped, not multiplied: sqrt(c0) at c0 = 0
+    has an infinite derivative, yet d max(x0, sqrt c0) / dc0 = 0 at x0 = 1
+    (a plain product 0 * inf would be NaN) -- on either side of MAX."""
+    xs, y = [[1.0]], [0.0]
+    for nt, nv, ci in (([3, 0, 2, 1], [_OP_MAX, 0, _OP_SQRT, 0], [-1, -1, -1, 0]),
+                       ([3, 2, 1, 0], [_OP_MAX, _OP_SQRT, 0, 0], [-1, -1, 0, -1])):
+        pop = _pop1(nt, nv, ci, [0.0], xs, y)
+        J = lm_oracle.jacobian(pop, c=np.array([0.0]), xs=np.array(xs), ad_mode=ad_mode)[0]
+        assert J[0, 0] == 0.0, (nt, J)
+
+
+def _linear_pop(c_init):
+    """y = 2 x0 on 24 points (exact in fp32): F = c0 * x0."""
+    x = (np.arange(1, 25, dtype=np.float64) / 8.0)[:, None]
+    return _pop1([3, 1, 0], [_OP_MUL, 0, 0], [-1, 0, -1], [c_init], x, 2.0 * x[:, 0])
+
+
+def test_lm_schedule_closed_form_on_a_linear_model():
+    """F = c x with exact data y = c* x: J = x, r = e x (e = c - c*), so the
+    damped step is -e / (1 + lambda) and e' = e lambda / (1 + lambda). Every
+    step lowers the loss and is accepted, so lambda_k = 1e-3 * 10^-k
+    (batch_lm_ad.cu:456-473, relative damping :149-191). From c = 0 (e = -2):
+    e1 = -2e-3 / 1.001, e2 = e1 1e-4 / 1.0001, e3 = e2 1e-5 / 1.00001, and the
+    third step is below xtol (||delta|| < 1e-6 (||c|| + 1e-6)): converged."""
+    pop = _linear_pop(0.0)
+    e = [-2.0]
+    for k in range(3):
+        lam = 1e-3 * 10.0 ** -k
+        e.append(e[-1] * lam / (1.0 + lam))
+    for it in (1, 2):
+        r = lm_oracle.fit(pop, max_iter=it)
+        assert r["status"][0] == 1 and r["iters"][0] == it        # MAXITER
+        assert r["c_final"][0] - 2.0 == pytest.approx(e[it], rel=1e-9)
+    r = lm_oracle.fit(pop, max_iter=10)
+    assert r["status"][0] == 0 and r["iters"][0] == 3               # CONVERGED
+    assert r["c_final"][0] - 2.0 == pytest.approx(e[3], rel=1e-3)
+
+
+def test_lm_accepts_an_equal_loss():
+    """Started exactly at the minimum (r = 0, J^T r = 0) the step is 0, the
+    trial loss equals the current one and is accepted (accept on <=,
+    batch_lm_ad.cu:456-473): converged after one iteration. Rejecting equal
+    losses would raise lambda 10x per iteration to the 1e12 limit."""
+    r = lm_oracle.fit(_linear_pop(2.0), max_iter=50)
+    assert r["status"][0] == 0 and r["iters"][0] == 1 and r["c_final"][0] == 2.0
