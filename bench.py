@@ -9,7 +9,9 @@ expressions, depth <= 6, <= 31 nodes, K uniform 1..8, D = 3, N = 1,024,
 50 iterations, forward AD, fp64. The population is uploaded before timing
 (inputs resident in HBM); each timed step re-fits it from the same starting
 constants. Prints one JSON line. --config C1/C3/C4 measure the other resident
-configurations the same way; --config C5 runs the GP inner-solver shape: R
+configurations the same way (and G1 / G1F, a GP generation shaped like the
+reference's operon4000_g100 snapshot, with and without its K >= 17 expressions
+that run in the general kernel); --config C5 runs the GP inner-solver shape: R
 rounds of fresh 65,536-expression populations (generated untimed), each timed
 end to end from host buffers (upload, 10 mixed-precision iterations,
 read-back), the per-round latency being the step; the round's one target goes
@@ -510,7 +512,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "G1", "G1F"])
     ap.add_argument("--rounds", type=int, default=3, help="C5 rounds (the spec runs 20)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--ad-mode", type=int, default=None, choices=[0, 1],

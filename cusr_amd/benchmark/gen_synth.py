@@ -8,6 +8,12 @@ with the benchmark's own op sets and shapes:
   C3  8,192 expr, depth<=8, <=63 nodes, K in 4..16, D=4, N=2,048, x~U[-2,2], sigma 0.01, init sd 1.0
   C4  4,096 expr, depth<=6, <=31 nodes, K in 1..8,  D=5, N=100,000, x~U[-3,3], sigma 0.05, init sd 0.5
   C5 65,536 expr per round, depth<=7, <=63 nodes, K in 0..8, D=4, N=2,048, one shared target
+  G1  4,000 expr, depth<=9, <=127 nodes, K in 1..28, D=2, N=1,000: a GP generation shaped
+      like the header of the reference's operon4000_g100 snapshot (M 4,000, N 1,000,
+      n_vars 2, K_max 28, mean K 14.4; cusr/kernel/tests/golden/manifest.json), whose
+      K >= 17 expressions run in the general kernel (not a BASELINE configuration)
+  G1F the same generation with K in 1..16: every expression on the fast kernels, for
+      comparing the general kernel's cost with theirs
 
 Draw order (numpy default_rng(seed)): x for all points; then per expression
 slot: K, the tree shape and ops, the constant/variable leaf assignment,
@@ -62,6 +68,8 @@ CONFIGS = {
     "C4": SynthConfig("C4", 4096, 100000, 5, 6, 31, 1, 8, -3.0, 3.0, 0.05, 0.5, 30, 401),
     "C5": SynthConfig("C5", 65536, 2048, 4, 7, 63, 0, 8, -3.0, 3.0, 0.01, 0.5, 10, 501,
                       precision=1, shared_target=True, rounds=20),
+    "G1": SynthConfig("G1", 4000, 1000, 2, 9, 127, 1, 28, -3.0, 3.0, 0.01, 0.5, 50, 601),
+    "G1F": SynthConfig("G1F", 4000, 1000, 2, 9, 127, 1, 16, -3.0, 3.0, 0.01, 0.5, 50, 601),
 }
 
 

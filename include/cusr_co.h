@@ -218,12 +218,15 @@ static inline int co_tail_resolve(const CoOptions *o, int N, int *tail_parts) {
  * follows the same rule. (Below the thresholds the per-lane sums are
  * faster. In reverse mode the staged rows share the LDS of the tape, which
  * the reverse sweep has consumed by then, so they cost no LDS, and they free
- * the registers of the per-lane sums.) */
+ * the registers of the per-lane sums: from K = 12 the reverse-AD pass kernels
+ * need 106-110 VGPRs instead of the 257-322 the per-lane sums took, which
+ * spilled at two waves per SIMD; measured on MI355X, C3 from K = 11, 13 and
+ * 15 within noise of each other.) */
 #ifndef CO_SUMS_MATRIX_MIN_K
 #define CO_SUMS_MATRIX_MIN_K 13
 #endif
 #ifndef CO_SUMS_MATRIX_MIN_K_REV
-#define CO_SUMS_MATRIX_MIN_K_REV 15
+#define CO_SUMS_MATRIX_MIN_K_REV 12
 #endif
 
 /* --- reference ABI (cusr/kernel/co_lib.h:45-71) ------------------------ */

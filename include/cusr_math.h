@@ -11,21 +11,27 @@
  * rounding by the 1.5*2^52 (1.5*2^23) shift. Callers must compile with
  * -ffp-contract=off so no other operation is fused. Methods (all published):
  *   exp   Cody-Waite reduction x = k ln2 + r, |r| <= ln2/2 (ln2 split into a
- *         32-bit head and a tail), Taylor series of e^r to r^13 (fp32: r^7),
- *         scaling by 2^k through the exponent field, two steps near the ends.
+ *         32-bit head and a tail), e^r = 1 + r (1 + r G(r)) with G the degree-9
+ *         minimax polynomial of (e^r - 1 - r)/r^2 (fp32: degree 4), scaling by
+ *         2^k through the exponent field, two steps near the ends.
  *   log   x = 2^e m, m in (sqrt(1/2), sqrt(2)], f = m - 1, s = f/(2+f),
- *         log(1+f) = f - (f^2/2 - s (f^2/2 + R)), R = 2 s^2/3 + 2 s^4/5 + ...
- *         (the atanh series, rearranged as in Sun's fdlibm e_log.c), to s^23
- *         (fp32: s^13).
+ *         log(1+f) = f - (f^2/2 - s (f^2/2 + R)) with R = z P(z), z = s^2,
+ *         the atanh form rearranged as in Sun's fdlibm e_log.c; P is the
+ *         degree-6 minimax polynomial of (2 atanh(s) - 2s)/(s z) (fp32: 2).
  *   sin/cos  k = rint(x 2/pi), r = x - k pi/2 with pi/2 split into three
- *         doubles subtracted by fma (Cody-Waite); Taylor series on
- *         [-pi/4, pi/4] to r^17 / r^18 (fp32: r^11 / r^12); cos uses the
- *         compensated 1 - z/2 step of fdlibm k_cos.c; quadrant by k mod 4.
- *         For |x| >= 2^50 the reduction is Payne and Hanek's ("Radian
+ *         doubles subtracted by fma (Cody-Waite); on [-pi/4, pi/4]
+ *         sin r = r + r^3 S(z), cos r = 1 - z/2 + z^2 C(z), z = r^2, with S and
+ *         C the degree-5 minimax polynomials of their parts (fp32: 2); cos
+ *         uses the compensated 1 - z/2 step of fdlibm k_cos.c; quadrant by
+ *         k mod 4.
+ *   The minimax coefficients come from cusr_amd/csrc/gen_minimax.py (Remez
+ *         exchange at 60 digits); each polynomial's approximation error is
+ *         below 0.19 x 2^-53 (fp32: 0.22 x 2^-24) relative on its range.
+ *         For |x| >= 2^30 the reduction is Payne and Hanek's ("Radian
  *         reduction for trigonometric functions", SIGNUM Newsletter 18,
  *         1983): x = M 2^E, and only the 192 bits of 2/pi from weight
  *         2^-(E-1) on matter for x 2/pi mod 4, a 53 x 192-bit integer
- *         product. fp32 arguments from 2^21 are reduced in fp64.
+ *         product. fp32 arguments from 2^17 are reduced in fp64.
  *   tan   sin/cos of the same reduction.
  *   sinh, cosh, tanh  Taylor series for |x| < 1 (sinh), exp otherwise.
  *   pow   integral |y| <= 64: binary powering (x^2, x^3 exact when
@@ -148,13 +154,15 @@ CM_FN float cm_pow2if(int k) { return cm_flt((uint32_t)(k + 127) << 23); }
 
 /* ------------------------------------------------------------------- exp */
 
-/* 1/ln2, ln2 head (32 bits), ln2 tail, then 1/13!, 1/12!, ..., 1/2!, 1, 1 */
-CM_TABLE double cm_exp_tab[17] = {
+/* 1/ln2, ln2 head (32 bits), ln2 tail, then G(r) highest degree first
+ * (gen_minimax.py), then 1, 1: Horner over entries 3.. gives 1 + r (1 + r G) */
+#define CM_EXP_N 15
+CM_TABLE double cm_exp_tab[CM_EXP_N] = {
     1.4426950408889634, 0.6931471803691238, 1.9082149288430703e-10,
-    1.6059043836821613e-10, 2.08767569878681e-09, 2.505210838544172e-08,
-    2.755731922398589e-07, 2.7557319223985893e-06, 2.48015873015873e-05,
-    0.0001984126984126984, 0.001388888888888889, 0.008333333333333333,
-    0.041666666666666664, 0.16666666666666666, 0.5, 1.0, 1.0};
+    2.5110039143068074e-08, 2.762007695623653e-07, 2.7557242364947015e-06,
+    2.480152131981927e-05, 0.00019841269886566317, 0.0013888888917198605,
+    0.008333333333322215, 0.04166666666662416, 0.16666666666666674,
+    0.5000000000000001, 1.0, 1.0};
 CM_ACCESSOR(cm_dtab, cm_exp_tab)
 
 CM_FN double cm_exp(double x) {
@@ -169,7 +177,7 @@ CM_FN double cm_exp(double x) {
     double r = CM_FMA(-kf, t[1], xr);
     r = CM_FMA(-kf, t[2], r);
     double p = t[3];
-    for (int i = 4; i < 17; i++) p = CM_HORNER(p, r, t[i]);
+    for (int i = 4; i < CM_EXP_N; i++) p = CM_HORNER(p, r, t[i]);
     int k = (int)kf;
     const int big = k > 1022, small = k < -1020;
     const int ka = big ? k - 2 : (small ? k + 1000 : k);
@@ -178,11 +186,13 @@ CM_FN double cm_exp(double x) {
     return nan ? x : (hi ? CM_INF : (lo ? 0.0 : res));
 }
 
-/* 1/ln2, ln2 head (16 bits), ln2 tail, then 1/7!, ..., 1/2!, 1, 1 */
-CM_TABLE float cm_expf_tab[11] = {
+/* 1/ln2, ln2 head (16 bits), ln2 tail, then G(r) highest degree first
+ * (gen_minimax.py), then 1, 1 */
+#define CM_EXPF_N 10
+CM_TABLE float cm_expf_tab[CM_EXPF_N] = {
     1.4426950216293335f, 0.693145751953125f, 1.4285906217992306e-06f,
-    0.00019841270113829523f, 0.0013888889225199819f, 0.008333333767950535f,
-    0.0416666679084301f, 0.1666666716337204f, 0.5f, 1.0f, 1.0f};
+    0.0013942165533080697f, 0.008363775908946991f, 0.041666362434625626f,
+    0.16666573286056519f, 0.5f, 1.0f, 1.0f};
 CM_ACCESSOR(cm_ftab, cm_expf_tab)
 
 CM_FN float cm_expf(float x) {
@@ -195,7 +205,7 @@ CM_FN float cm_expf(float x) {
     float r = CM_FMAF(-kf, t[1], xr);
     r = CM_FMAF(-kf, t[2], r);
     float p = t[3];
-    for (int i = 4; i < 11; i++) p = CM_HORNERF(p, r, t[i]);
+    for (int i = 4; i < CM_EXPF_N; i++) p = CM_HORNERF(p, r, t[i]);
     int k = (int)kf;
     const int big = k > 126, small = k < -124;
     const int ka = big ? k - 2 : (small ? k + 100 : k);
@@ -206,11 +216,12 @@ CM_FN float cm_expf(float x) {
 
 /* ------------------------------------------------------------------- log */
 
-/* 2/23, 2/21, ..., 2/3, then ln2 head and tail */
-CM_TABLE double cm_log_tab[13] = {
-    0.08695652173913043, 0.09523809523809523, 0.10526315789473684, 0.11764705882352941,
-    0.13333333333333333, 0.15384615384615385, 0.18181818181818182, 0.2222222222222222,
-    0.2857142857142857, 0.4, 0.6666666666666666, 0.6931471803691238, 1.9082149288430703e-10};
+/* P(z) highest degree first (gen_minimax.py), then ln2 head and tail */
+#define CM_LOG_P 7
+CM_TABLE double cm_log_tab[CM_LOG_P + 2] = {
+    0.1461773941368345, 0.15331607753678703, 0.1818289289358215, 0.22222211077310847,
+    0.28571428626371803, 0.39999999999898506, 0.666666666666667,
+    0.6931471803691238, 1.9082149288430703e-10};
 CM_ACCESSOR(cm_dtab, cm_log_tab)
 
 CM_FN double cm_log(double x) {
@@ -229,18 +240,19 @@ CM_FN double cm_log(double x) {
     double z = s * s;
     cm_dtab t = CM_TAB(cm_dtab, cm_log_tab);
     double R = t[0];
-    for (int i = 1; i < 11; i++) R = CM_HORNER(R, z, t[i]);
+    for (int i = 1; i < CM_LOG_P; i++) R = CM_HORNER(R, z, t[i]);
     R = R * z;
     double hfsq = 0.5 * (f * f);
     double dk = (double)e;
-    double res = dk * t[11] - ((hfsq - (s * (hfsq + R) + dk * t[12])) - f);
+    double res = dk * t[CM_LOG_P] - ((hfsq - (s * (hfsq + R) + dk * t[CM_LOG_P + 1])) - f);
     return cm_isnan(x) ? x : (x < 0.0 ? CM_NAN : (x == 0.0 ? -CM_INF : (x == CM_INF ? x : res)));
 }
 
-/* 2/13, ..., 2/3, then ln2 head and tail */
-CM_TABLE float cm_logf_tab[8] = {
-    0.1538461595773697f, 0.1818181872367859f, 0.2222222238779068f, 0.2857142984867096f,
-    0.4000000059604645f, 0.6666666865348816f, 0.693145751953125f, 1.4285906217992306e-06f};
+/* P(z) highest degree first (gen_minimax.py), then ln2 head and tail */
+#define CM_LOGF_P 3
+CM_TABLE float cm_logf_tab[CM_LOGF_P + 2] = {
+    0.29602980613708496f, 0.3998825252056122f, 0.6666668653488159f,
+    0.693145751953125f, 1.4285906217992306e-06f};
 CM_ACCESSOR(cm_ftab, cm_logf_tab)
 
 CM_FN float cm_logf(float x) {
@@ -257,39 +269,42 @@ CM_FN float cm_logf(float x) {
     float z = s * s;
     cm_ftab t = CM_TAB(cm_ftab, cm_logf_tab);
     float R = t[0];
-    for (int i = 1; i < 6; i++) R = CM_HORNERF(R, z, t[i]);
+    for (int i = 1; i < CM_LOGF_P; i++) R = CM_HORNERF(R, z, t[i]);
     R = R * z;
     float hfsq = 0.5f * (f * f);
     float dk = (float)e;
-    float res = dk * t[6] - ((hfsq - (s * (hfsq + R) + dk * t[7])) - f);
+    float res = dk * t[CM_LOGF_P] - ((hfsq - (s * (hfsq + R) + dk * t[CM_LOGF_P + 1])) - f);
     return (x != x) ? x : (x < 0.0f ? CM_NANF : (x == 0.0f ? -CM_INFF : (x == CM_INFF ? x : res)));
 }
 
 /* --------------------------------------------------------------- sin/cos */
 
-/* sin: 1/17!, -1/15!, ..., -1/3!; cos: -1/18!, 1/16!, ..., 1/4!;
- * then 2/pi and pi/2 as three doubles */
-CM_TABLE double cm_trig_tab[20] = {
-    2.8114572543455206e-15, -7.647163731819816e-13, 1.6059043836821613e-10,
-    -2.505210838544172e-08, 2.7557319223985893e-06, -0.0001984126984126984,
-    0.008333333333333333, -0.16666666666666666,
-    -1.5619206968586225e-16, 4.779477332387385e-14, -1.1470745597729725e-11,
-    2.08767569878681e-09, -2.755731922398589e-07, 2.48015873015873e-05,
-    -0.001388888888888889, 0.041666666666666664,
+/* S(z), then C(z), each highest degree first (gen_minimax.py); then 2/pi
+ * and pi/2 as three doubles */
+#define CM_TRIG_S 0
+#define CM_TRIG_C 6
+#define CM_TRIG_N 6
+#define CM_TRIG_2PI 12
+#define CM_TRIG_PIO2 13
+CM_TABLE double cm_trig_tab[16] = {
+    1.591814230329288e-10, -2.505113204602621e-08, 2.75573161036397e-06,
+    -0.00019841269836760975, 0.00833333333333095, -0.16666666666666666,
+    -1.1382639639006937e-11, 2.087614637990424e-09, -2.755731727233302e-07,
+    2.480158729876702e-05, -0.0013888888888887398, 0.041666666666666664,
     0.6366197723675814, 1.5707963267948966, 6.123233995736766e-17, -1.4973849048591698e-33};
 CM_ACCESSOR(cm_dtab, cm_trig_tab)
 
 CM_FN double cm_sin_kernel(double r, cm_dtab t) {
     double z = r * r;
-    double p = t[0];
-    for (int i = 1; i < 8; i++) p = CM_HORNER(p, z, t[i]);
+    double p = t[CM_TRIG_S];
+    for (int i = 1; i < CM_TRIG_N; i++) p = CM_HORNER(p, z, t[CM_TRIG_S + i]);
     return CM_FMA(r * z, p, r);
 }
 
 CM_FN double cm_cos_kernel(double r, cm_dtab t) {
     double z = r * r;
-    double p = t[8];
-    for (int i = 9; i < 16; i++) p = CM_HORNER(p, z, t[i]);
+    double p = t[CM_TRIG_C];
+    for (int i = 1; i < CM_TRIG_N; i++) p = CM_HORNER(p, z, t[CM_TRIG_C + i]);
     double hz = 0.5 * z;
     double w = 1.0 - hz;
     return w + (((1.0 - w) - hz) + z * (z * p));
@@ -310,9 +325,18 @@ CM_TABLE uint64_t cm_two_over_pi[24] = {
 };
 CM_ACCESSOR(cm_utab, cm_two_over_pi)
 
-/* Payne-Hanek reduction of a finite ax >= 2^50: returns r with |r| <= pi/4
+/* Arguments reduced by Payne-Hanek (fp64) and fp32 arguments reduced in fp64.
+ * Below them the Cody-Waite quotient k = rint(x 2/pi) is formed from x 2/pi
+ * rounded once: below 2^30 its ulp is at most 2^-23, so the remainder
+ * exceeds pi/4 by at most 2^-24 pi/2, inside the range the polynomials are
+ * fitted on (widened by 2^-20); in fp32 below 2^17 by at most 2^-8 pi/2
+ * (fitted on a range widened by 1 %). */
+#define CM_PH_MIN 1073741824.0      /* 2^30 */
+#define CM_F64_RED_MINF 131072.0f   /* 2^17 */
+
+/* Payne-Hanek reduction of a finite ax >= 2^30: returns r with |r| <= pi/4
  * and sets *q so that ax = (4n + *q) pi/2 + r. ax = M 2^E with M the 53-bit
- * integer significand (E >= -2). Bits of 2/pi of weight 2^-i with i <= E - 2
+ * integer significand (E >= -22). Bits of 2/pi of weight 2^-i with i <= E - 2
  * add multiples of 4 to ax 2/pi; the 192 bits W from weight 2^-(E-1) on give
  * ax 2/pi = M W 2^-190 (mod 4) with an error below 2^-137. Bits 190..191 of
  * the product are the quadrant, the 128 below the fraction; a fraction
@@ -343,30 +367,31 @@ CM_FN double cm_rem_pio2_huge(double ax, int *q, cm_dtab t) {
     const double fh = (double)gh;
     const double fl = (double)(gh - (int64_t)fh) + (double)(uint64_t)g * 5.421010862427522e-20;
     const double a = fh * 5.421010862427522e-20, bq = fl * 5.421010862427522e-20; /* 2^-64 */
-    const double rh = a * t[17];
-    const double rl = CM_FMA(a, t[17], -rh) + CM_FMA(a, t[18], bq * t[17]);
+    const double rh = a * t[CM_TRIG_PIO2];
+    const double rl = CM_FMA(a, t[CM_TRIG_PIO2], -rh) +
+                      CM_FMA(a, t[CM_TRIG_PIO2 + 1], bq * t[CM_TRIG_PIO2]);
     return rh + rl;
 }
 
-/* x - k pi/2 with k = rint(x 2/pi) for |x| < 2^50 (Cody-Waite, pi/2 in three
+/* x - k pi/2 with k = rint(x 2/pi) for |x| < 2^30 (Cody-Waite, pi/2 in three
  * doubles subtracted by fma); *q = k mod 4. */
 CM_FN double cm_rem_pio2_cw(double x, int *q, cm_dtab t) {
-    double kf = cm_rint_small(x * t[16]);
-    double r = CM_FMA(-kf, t[17], x);
-    r = CM_FMA(-kf, t[18], r);
-    r = CM_FMA(-kf, t[19], r);
+    double kf = cm_rint_small(x * t[CM_TRIG_2PI]);
+    double r = CM_FMA(-kf, t[CM_TRIG_PIO2], x);
+    r = CM_FMA(-kf, t[CM_TRIG_PIO2 + 1], r);
+    r = CM_FMA(-kf, t[CM_TRIG_PIO2 + 2], r);
     double q4 = kf - 4.0 * cm_rint_small(kf * 0.25 - 0.375); /* kf mod 4, in 0..3 */
     *q = (int)q4;
     return r;
 }
 
 /* sin and cos of x from one argument reduction: NaN and +-inf give NaN
- * (through the reduction of 0 and a final select); |x| >= 2^50 takes the
+ * (through the reduction of 0 and a final select); |x| >= 2^30 takes the
  * Payne-Hanek reduction; the quadrant swaps and negates. */
 CM_FN void cm_sincos(double x, double *s, double *c) {
     const double ax = cm_fabs(x);
     const int bad = !(ax < CM_INF);
-    const int huge = !bad && ax >= 1125899906842624.0; /* 2^50 */
+    const int huge = !bad && ax >= CM_PH_MIN;
     const double xr = (bad || huge) ? 0.0 : x;
     cm_dtab t = CM_TAB(cm_dtab, cm_trig_tab);
     int q;
@@ -390,52 +415,55 @@ CM_FN double cm_sin(double x) { double s, c; cm_sincos(x, &s, &c); return s; }
 CM_FN double cm_cos(double x) { double s, c; cm_sincos(x, &s, &c); return c; }
 CM_FN double cm_tan(double x) { double s, c; cm_sincos(x, &s, &c); return s / c; }
 
-/* sin: -1/11!, ..., -1/3!; cos: 1/12!, ..., 1/4!; then 2/pi and pi/2 as
- * three floats */
-CM_TABLE float cm_trigf_tab[14] = {
-    -2.5052107943679403e-08f, 2.7557318844628753e-06f, -0.00019841270113829523f,
-    0.008333333767950535f, -0.1666666716337204f,
-    2.0876755879584152e-09f, -2.755731998149713e-07f, 2.4801587642286904e-05f,
-    -0.0013888889225199819f, 0.0416666679084301f,
+/* S(z), then C(z), each highest degree first (gen_minimax.py); then 2/pi
+ * and pi/2 as three floats */
+#define CM_TRIGF_S 0
+#define CM_TRIGF_C 3
+#define CM_TRIGF_N 3
+#define CM_TRIGF_2PI 6
+#define CM_TRIGF_PIO2 7
+CM_TABLE float cm_trigf_tab[10] = {
+    -0.00019582953245844692f, 0.008332725614309311f, -0.166666641831398f,
+    2.4542972823837772e-05f, -0.0013888280373066664f, 0.0416666641831398f,
     0.6366197466850281f, 1.5707963705062866f, -4.371138828673793e-08f, -1.7151245100058819e-15f};
 CM_ACCESSOR(cm_ftab, cm_trigf_tab)
 
 CM_FN float cm_sin_kernelf(float r, cm_ftab t) {
     float z = r * r;
-    float p = t[0];
-    for (int i = 1; i < 5; i++) p = CM_HORNERF(p, z, t[i]);
+    float p = t[CM_TRIGF_S];
+    for (int i = 1; i < CM_TRIGF_N; i++) p = CM_HORNERF(p, z, t[CM_TRIGF_S + i]);
     return CM_FMAF(r * z, p, r);
 }
 
 CM_FN float cm_cos_kernelf(float r, cm_ftab t) {
     float z = r * r;
-    float p = t[5];
-    for (int i = 6; i < 10; i++) p = CM_HORNERF(p, z, t[i]);
+    float p = t[CM_TRIGF_C];
+    for (int i = 1; i < CM_TRIGF_N; i++) p = CM_HORNERF(p, z, t[CM_TRIGF_C + i]);
     float hz = 0.5f * z;
     float w = 1.0f - hz;
     return w + (((1.0f - w) - hz) + z * (z * p));
 }
 
-/* fp32 sin and cos; arguments from 2^21 on are reduced in fp64 (exact
+/* fp32 sin and cos; arguments from 2^17 on are reduced in fp64 (exact
  * widening, then the fp64 reduction) and the reduced argument rounded to
  * fp32. */
 CM_FN void cm_sincosf(float x, float *s, float *c) {
     const float ax = cm_fabsf(x);
     const int bad = !(ax < CM_INFF);
-    const int huge = !bad && ax >= 2097152.0f; /* 2^21 */
+    const int huge = !bad && ax >= CM_F64_RED_MINF;
     const float xr = (bad || huge) ? 0.0f : x;
     cm_ftab t = CM_TAB(cm_ftab, cm_trigf_tab);
-    float kf = cm_rint_smallf(xr * t[10]);
-    float r = CM_FMAF(-kf, t[11], xr);
-    r = CM_FMAF(-kf, t[12], r);
-    r = CM_FMAF(-kf, t[13], r);
+    float kf = cm_rint_smallf(xr * t[CM_TRIGF_2PI]);
+    float r = CM_FMAF(-kf, t[CM_TRIGF_PIO2], xr);
+    r = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 1], r);
+    r = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 2], r);
     float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
     int q = (int)q4;
     if (huge) {
         cm_dtab td = CM_TAB(cm_dtab, cm_trig_tab);
         const double axd = (double)ax;
         int qh;
-        const double rd = axd >= 1125899906842624.0 ? cm_rem_pio2_huge(axd, &qh, td)
+        const double rd = axd >= CM_PH_MIN ? cm_rem_pio2_huge(axd, &qh, td)
                                                     : cm_rem_pio2_cw(axd, &qh, td);
         r = (float)(x < 0.0f ? -rd : rd);
         q = (x < 0.0f ? -qh : qh) & 3;
@@ -480,7 +508,7 @@ CM_FN void cm_exp_v(const double *x, double *res) {
         r[p] = CM_FMA(-kf[p], t[2], r[p]);
         q[p] = t[3];
     }
-    _Pragma("unroll") for (int i = 4; i < 17; i++) CM_FORP q[p] = CM_HORNER(q[p], r[p], t[i]);
+    _Pragma("unroll") for (int i = 4; i < CM_EXP_N; i++) CM_FORP q[p] = CM_HORNER(q[p], r[p], t[i]);
     CM_FORP {
         const int k = (int)kf[p];
         const int big = k > 1022, small = k < -1020;
@@ -510,12 +538,12 @@ CM_FN void cm_log_v(const double *x, double *res) {
     }
     cm_dtab t = CM_TAB(cm_dtab, cm_log_tab);
     CM_FORP R[p] = t[0];
-    _Pragma("unroll") for (int i = 1; i < 11; i++) CM_FORP R[p] = CM_HORNER(R[p], z[p], t[i]);
+    _Pragma("unroll") for (int i = 1; i < CM_LOG_P; i++) CM_FORP R[p] = CM_HORNER(R[p], z[p], t[i]);
     CM_FORP {
         const double Rz = R[p] * z[p];
         const double hfsq = 0.5 * (f[p] * f[p]);
-        const double v =
-            dk[p] * t[11] - ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[12])) - f[p]);
+        const double v = dk[p] * t[CM_LOG_P] -
+                         ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[CM_LOG_P + 1])) - f[p]);
         res[p] = cm_isnan(x[p]) ? x[p]
                  : (x[p] < 0.0 ? CM_NAN : (x[p] == 0.0 ? -CM_INF : (x[p] == CM_INF ? x[p] : v)));
     }
@@ -529,7 +557,7 @@ CM_FN void cm_sincos_v(const double *x, double *so, double *co) {
     CM_FORP {
         const double ax = cm_fabs(x[p]);
         bad[p] = !(ax < CM_INF);
-        huge[p] = !bad[p] && ax >= 1125899906842624.0; /* 2^50 */
+        huge[p] = !bad[p] && ax >= CM_PH_MIN;
         any_huge |= huge[p];
         const double xr = (bad[p] || huge[p]) ? 0.0 : x[p];
         r[p] = cm_rem_pio2_cw(xr, &q[p], t);
@@ -544,12 +572,12 @@ CM_FN void cm_sincos_v(const double *x, double *so, double *co) {
     }
     CM_FORP {
         z[p] = r[p] * r[p];
-        ps[p] = t[0];
-        pc[p] = t[8];
+        ps[p] = t[CM_TRIG_S];
+        pc[p] = t[CM_TRIG_C];
     }
-    _Pragma("unroll") for (int i = 1; i < 8; i++) CM_FORP {
-        ps[p] = CM_HORNER(ps[p], z[p], t[i]);
-        pc[p] = CM_HORNER(pc[p], z[p], t[8 + i]);
+    _Pragma("unroll") for (int i = 1; i < CM_TRIG_N; i++) CM_FORP {
+        ps[p] = CM_HORNER(ps[p], z[p], t[CM_TRIG_S + i]);
+        pc[p] = CM_HORNER(pc[p], z[p], t[CM_TRIG_C + i]);
     }
     CM_FORP {
         const double sr = CM_FMA(r[p] * z[p], ps[p], r[p]);
@@ -580,7 +608,7 @@ CM_FN void cm_expf_v(const float *x, float *res) {
         r[p] = CM_FMAF(-kf[p], t[2], r[p]);
         q[p] = t[3];
     }
-    _Pragma("unroll") for (int i = 4; i < 11; i++) CM_FORP q[p] = CM_HORNERF(q[p], r[p], t[i]);
+    _Pragma("unroll") for (int i = 4; i < CM_EXPF_N; i++) CM_FORP q[p] = CM_HORNERF(q[p], r[p], t[i]);
     CM_FORP {
         const int k = (int)kf[p];
         const int big = k > 126, small = k < -124;
@@ -610,11 +638,12 @@ CM_FN void cm_logf_v(const float *x, float *res) {
     }
     cm_ftab t = CM_TAB(cm_ftab, cm_logf_tab);
     CM_FORP R[p] = t[0];
-    _Pragma("unroll") for (int i = 1; i < 6; i++) CM_FORP R[p] = CM_HORNERF(R[p], z[p], t[i]);
+    _Pragma("unroll") for (int i = 1; i < CM_LOGF_P; i++) CM_FORP R[p] = CM_HORNERF(R[p], z[p], t[i]);
     CM_FORP {
         const float Rz = R[p] * z[p];
         const float hfsq = 0.5f * (f[p] * f[p]);
-        const float v = dk[p] * t[6] - ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[7])) - f[p]);
+        const float v = dk[p] * t[CM_LOGF_P] -
+                        ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[CM_LOGF_P + 1])) - f[p]);
         res[p] = (x[p] != x[p]) ? x[p]
                  : (x[p] < 0.0f ? CM_NANF
                                 : (x[p] == 0.0f ? -CM_INFF : (x[p] == CM_INFF ? x[p] : v)));
@@ -629,13 +658,13 @@ CM_FN void cm_sincosf_v(const float *x, float *so, float *co) {
     CM_FORP {
         const float ax = cm_fabsf(x[p]);
         bad[p] = !(ax < CM_INFF);
-        huge[p] = !bad[p] && ax >= 2097152.0f; /* 2^21 */
+        huge[p] = !bad[p] && ax >= CM_F64_RED_MINF;
         any_huge |= huge[p];
         const float xr = (bad[p] || huge[p]) ? 0.0f : x[p];
-        const float kf = cm_rint_smallf(xr * t[10]);
-        float rr = CM_FMAF(-kf, t[11], xr);
-        rr = CM_FMAF(-kf, t[12], rr);
-        rr = CM_FMAF(-kf, t[13], rr);
+        const float kf = cm_rint_smallf(xr * t[CM_TRIGF_2PI]);
+        float rr = CM_FMAF(-kf, t[CM_TRIGF_PIO2], xr);
+        rr = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 1], rr);
+        rr = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 2], rr);
         const float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
         q[p] = (int)q4;
         r[p] = rr;
@@ -645,7 +674,7 @@ CM_FN void cm_sincosf_v(const float *x, float *so, float *co) {
         CM_FORP if (huge[p]) {
             const double axd = (double)cm_fabsf(x[p]);
             int qh;
-            const double rd = axd >= 1125899906842624.0 ? cm_rem_pio2_huge(axd, &qh, td)
+            const double rd = axd >= CM_PH_MIN ? cm_rem_pio2_huge(axd, &qh, td)
                                                         : cm_rem_pio2_cw(axd, &qh, td);
             r[p] = (float)(x[p] < 0.0f ? -rd : rd);
             q[p] = (x[p] < 0.0f ? -qh : qh) & 3;
@@ -653,12 +682,12 @@ CM_FN void cm_sincosf_v(const float *x, float *so, float *co) {
     }
     CM_FORP {
         z[p] = r[p] * r[p];
-        ps[p] = t[0];
-        pc[p] = t[5];
+        ps[p] = t[CM_TRIGF_S];
+        pc[p] = t[CM_TRIGF_C];
     }
-    _Pragma("unroll") for (int i = 1; i < 5; i++) CM_FORP {
-        ps[p] = CM_HORNERF(ps[p], z[p], t[i]);
-        pc[p] = CM_HORNERF(pc[p], z[p], t[5 + i]);
+    _Pragma("unroll") for (int i = 1; i < CM_TRIGF_N; i++) CM_FORP {
+        ps[p] = CM_HORNERF(ps[p], z[p], t[CM_TRIGF_S + i]);
+        pc[p] = CM_HORNERF(pc[p], z[p], t[CM_TRIGF_C + i]);
     }
     CM_FORP {
         const float sr = CM_FMAF(r[p] * z[p], ps[p], r[p]);

@@ -142,9 +142,9 @@ DEVICE_MUTANTS = [
 
 # (table, index) of the coefficient each coefficient mutant scales: a term
 # whose change moves the function by well over an ulp somewhere on its
-# reduced range (the degree-4 term of exp, the z^3 term of log's series)
-COEFFICIENT_MUTANTS = {"exp-coefficient": ("cm_exp_tab", 12),
-                       "log-coefficient": ("cm_log_tab", 8)}
+# reduced range (the r^4 term of exp's polynomial, the z^3 term of log's R)
+COEFFICIENT_MUTANTS = {"exp-coefficient": ("cm_exp_tab", 10),
+                       "log-coefficient": ("cm_log_tab", 4)}
 
 
 def _coefficient_edit(text: str, table: str, index: int):

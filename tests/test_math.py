@@ -131,3 +131,42 @@ def test_huge_arguments_reduced_exactly(name, ulp):
     x32 = _sym(RNG.uniform(1, 2, 20000) * 2.0 ** RNG.uniform(21, 127, 20000)).astype(np.float32)
     got32 = f(name, x32.astype(np.float64), fp32=True)
     assert _ulps(got32, getattr(np, name)(x32.astype(np.float64)), np.float32).max() <= ulp + 1
+
+
+@pytest.mark.parametrize("name", ["sin", "cos"])
+def test_reduction_quotient_rounding_ranges(name):
+    """Below the Payne-Hanek (fp64, 2^30) and fp64-reduction (fp32, 2^17)
+    thresholds the quotient k = rint(x 2/pi) comes from x 2/pi rounded once,
+    so the remainder can pass pi/4 by up to 2^-24 pi/2 (fp32: 2^-8 pi/2); the
+    polynomials are fitted on ranges widened for it. Dense arguments where
+    that rounding is largest keep sin/cos within 1 ulp (fp32: 2)."""
+    f = lm_oracle.math_fn
+    x = _sym(RNG.uniform(1, 2, 40000) * 2.0 ** RNG.uniform(20, 30, 40000))
+    assert _ulps(f(name, x), getattr(np, name)(x), np.float64).max() <= 1
+    x32 = _sym(RNG.uniform(1, 2, 40000) * 2.0 ** RNG.uniform(10, 17, 40000)).astype(np.float32)
+    got = f(name, x32.astype(np.float64), fp32=True)
+    assert _ulps(got, getattr(np, name)(x32.astype(np.float64)), np.float32).max() <= 2
+
+
+def test_p_wide_forms_equal_scalar(tmp_path):
+    """The interpreter evaluates exp, log, sin and cos P points at a time
+    (cm_*_v<P> of include/cusr_math.h); each element must get the scalar
+    function's bits, which the CPU oracle uses. tests/pwide_check.hip,
+    compiled for the host with the device flags, compares both on 1.6 M
+    random, huge, tiny, subnormal and special arguments for P = 1, 2, 4 in
+    both precisions."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    src = Path(__file__).resolve().parent / "pwide_check.hip"
+    exe = tmp_path / "pwide_check"
+    subprocess.run([hipcc, "-x", "hip", "--offload-arch=gfx950", "-O2", "-std=c++17",
+                    "-ffp-contract=off", "-fno-fast-math", "-Xclang", "-target-feature",
+                    "-Xclang", "-packed-fp32-ops", str(src), "-o", str(exe)],
+                   check=True, capture_output=True, timeout=300)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "pwide ok" in r.stdout, r.stdout[-2000:]

@@ -289,11 +289,11 @@ def test_general_sums_are_one_chain_per_entry(kind, ad_mode, G):
     assert checked >= 4
 
 
-@pytest.mark.parametrize("K", [15, 16])
+@pytest.mark.parametrize("K", [12, 14, 15, 16])
 def test_reverse_high_k_sums_are_one_chain_per_entry(K):
     """Fast-kernel expressions in reverse AD with K >= CO_SUMS_MATRIX_MIN_K_REV
-    (15): every J^T J entry is one fused multiply-add chain over the points in
-    ascending order (the matrix instruction's order); with K = 15, r^2 and
+    (12): every J^T J entry is one fused multiply-add chain over the points in
+    ascending order (the matrix instruction's order); with K < 16, r^2 and
     J^T r too (r is a column of the product), with K = 16 they keep the lane
     order (lane l folds points l, l+64, ... from 0.0; lanes combine with
     strides 32..1). Restated with exact rational arithmetic, so the lane order
