@@ -7,14 +7,16 @@
  * to send a trajectory to another minimum.
  *
  * Only IEEE-exact building blocks are used: +, -, *, /, sqrt, fma (all
- * correctly rounded on both sides), exponent bit manipulation, and integer
- * rounding by the 1.5*2^52 (1.5*2^23) shift. Callers must compile with
- * -ffp-contract=off so no other operation is fused. Methods (all published):
+ * correctly rounded on both sides), rint, frexp and ldexp (exact, ldexp
+ * correctly rounded where its result is subnormal), exponent bit
+ * manipulation, and integer rounding by the 1.5*2^52 (1.5*2^23) shift.
+ * Callers must compile with -ffp-contract=off so no other operation is fused.
+ * Methods (all published):
  *   exp   Cody-Waite reduction x = k ln2 + r, |r| <= ln2/2 (ln2 split into a
  *         32-bit head and a tail), e^r = 1 + r (1 + r G(r)) with G the degree-9
  *         minimax polynomial of (e^r - 1 - r)/r^2 (fp32: degree 4), scaling by
- *         2^k through the exponent field, two steps near the ends.
- *   log   x = 2^e m, m in (sqrt(1/2), sqrt(2)], f = m - 1, s = f/(2+f),
+ *         2^k with ldexp.
+ *   log   x = 2^e m (frexp), m in (sqrt(1/2), sqrt(2)], f = m - 1, s = f/(2+f),
  *         log(1+f) = f - (f^2/2 - s (f^2/2 + R)) with R = z P(z), z = s^2,
  *         the atanh form rearranged as in Sun's fdlibm e_log.c; P is the
  *         degree-6 minimax polynomial of (2 atanh(s) - 2s)/(s z) (fp32: 2).
@@ -148,9 +150,15 @@ CM_FN float cm_rint_smallf(float t) {
     return v - shift;
 }
 
-/* 2^k for a normal exponent k in [-1022, 1023] */
-CM_FN double cm_pow2i(int k) { return cm_dbl((uint64_t)(k + 1023) << 52); }
-CM_FN float cm_pow2if(int k) { return cm_flt((uint32_t)(k + 127) << 23); }
+/* rint (ties to even), x 2^k and frexp: the hardware's v_rndne, v_ldexp and
+ * v_frexp_mant / v_frexp_exp on the device, the C library's on the host; each
+ * is exact (ldexp rounds once where the result is subnormal), so both sides
+ * get the same bits. */
+#define CM_RINT(x) __builtin_rint(x)
+#define CM_LDEXP(x, k) __builtin_ldexp((x), (k))
+#define CM_LDEXPF(x, k) __builtin_ldexpf((x), (k))
+#define CM_FREXP(x, e) __builtin_frexp((x), (e))
+#define CM_FREXPF(x, e) __builtin_frexpf((x), (e))
 
 /* ------------------------------------------------------------------- exp */
 
@@ -165,24 +173,24 @@ CM_TABLE double cm_exp_tab[CM_EXP_N] = {
     0.5000000000000001, 1.0, 1.0};
 CM_ACCESSOR(cm_dtab, cm_exp_tab)
 
+/* |x| at most this: no overflow, underflow or NaN, so no final select */
+#define CM_EXP_PLAIN 709.782712893384
+#define CM_EXP_LO -745.1332191019412
+
 CM_FN double cm_exp(double x) {
     /* branch-free: out-of-range and NaN arguments reduce 0 and are selected
-     * at the end; the scaling by 2^k is split in two outside the normal range */
+     * at the end */
     const int nan = cm_isnan(x);
-    const int hi = x > 709.782712893384;
-    const int lo = x < -745.1332191019412;
+    const int hi = x > CM_EXP_PLAIN;
+    const int lo = x < CM_EXP_LO;
     const double xr = (nan || hi || lo) ? 0.0 : x;
     cm_dtab t = CM_TAB(cm_dtab, cm_exp_tab);
-    double kf = cm_rint_small(xr * t[0]);
+    double kf = CM_RINT(xr * t[0]);
     double r = CM_FMA(-kf, t[1], xr);
     r = CM_FMA(-kf, t[2], r);
     double p = t[3];
     for (int i = 4; i < CM_EXP_N; i++) p = CM_HORNER(p, r, t[i]);
-    int k = (int)kf;
-    const int big = k > 1022, small = k < -1020;
-    const int ka = big ? k - 2 : (small ? k + 1000 : k);
-    double res = p * cm_pow2i(ka);
-    res = big ? res * 4.0 : (small ? res * cm_pow2i(-1000) : res);
+    const double res = CM_LDEXP(p, (int)kf);
     return nan ? x : (hi ? CM_INF : (lo ? 0.0 : res));
 }
 
@@ -195,10 +203,13 @@ CM_TABLE float cm_expf_tab[CM_EXPF_N] = {
     0.16666573286056519f, 0.5f, 1.0f, 1.0f};
 CM_ACCESSOR(cm_ftab, cm_expf_tab)
 
+#define CM_EXPF_PLAIN 88.72283f
+#define CM_EXPF_LO -103.97208f
+
 CM_FN float cm_expf(float x) {
     const int nan = x != x;
-    const int hi = x > 88.72283f;
-    const int lo = x < -103.97208f;
+    const int hi = x > CM_EXPF_PLAIN;
+    const int lo = x < CM_EXPF_LO;
     const float xr = (nan || hi || lo) ? 0.0f : x;
     cm_ftab t = CM_TAB(cm_ftab, cm_expf_tab);
     float kf = cm_rint_smallf(xr * t[0]);
@@ -206,11 +217,7 @@ CM_FN float cm_expf(float x) {
     r = CM_FMAF(-kf, t[2], r);
     float p = t[3];
     for (int i = 4; i < CM_EXPF_N; i++) p = CM_HORNERF(p, r, t[i]);
-    int k = (int)kf;
-    const int big = k > 126, small = k < -124;
-    const int ka = big ? k - 2 : (small ? k + 100 : k);
-    float res = p * cm_pow2if(ka);
-    res = big ? res * 4.0f : (small ? res * cm_pow2if(-100) : res);
+    const float res = CM_LDEXPF(p, (int)kf);
     return nan ? x : (hi ? CM_INFF : (lo ? 0.0f : res));
 }
 
@@ -225,16 +232,13 @@ CM_TABLE double cm_log_tab[CM_LOG_P + 2] = {
 CM_ACCESSOR(cm_dtab, cm_log_tab)
 
 CM_FN double cm_log(double x) {
-    /* branch-free: subnormals are scaled by 2^54 through a select; NaN,
-     * negative, zero and +inf arguments are selected at the end */
-    const int sub = x > 0.0 && x < 2.2250738585072014e-308;
-    const double xs = sub ? x * 18014398509481984.0 : x; /* 2^54 */
-    uint64_t u = cm_bits(xs);
-    int e = (int)((u >> 52) & 0x7ff) - (sub ? 54 : 0) - 1023;
-    double m = cm_dbl((u & 0x000fffffffffffffULL) | 0x3ff0000000000000ULL);
-    const int up = m > 1.4142135623730951;
-    m = up ? m * 0.5 : m;
-    e = up ? e + 1 : e;
+    /* branch-free: NaN, negative, zero and +inf arguments are selected at the
+     * end; frexp's m in [1/2, 1) is doubled below sqrt(1/2) */
+    int e;
+    double m = CM_FREXP(x, &e);
+    const int dn = m <= 0.7071067811865476;
+    m = dn ? m + m : m;
+    e = dn ? e - 1 : e;
     double f = m - 1.0;
     double s = f / (2.0 + f);
     double z = s * s;
@@ -256,14 +260,11 @@ CM_TABLE float cm_logf_tab[CM_LOGF_P + 2] = {
 CM_ACCESSOR(cm_ftab, cm_logf_tab)
 
 CM_FN float cm_logf(float x) {
-    const int sub = x > 0.0f && x < 1.17549435e-38f;
-    const float xs = sub ? x * 33554432.0f : x; /* 2^25 */
-    uint32_t u = cm_bitsf(xs);
-    int e = (int)((u >> 23) & 0xff) - (sub ? 25 : 0) - 127;
-    float m = cm_flt((u & 0x007fffffu) | 0x3f800000u);
-    const int up = m > 1.4142135381698608f;
-    m = up ? m * 0.5f : m;
-    e = up ? e + 1 : e;
+    int e;
+    float m = CM_FREXPF(x, &e);
+    const int dn = m <= 0.70710676908493042f;
+    m = dn ? m + m : m;
+    e = dn ? e - 1 : e;
     float f = m - 1.0f;
     float s = f / (2.0f + f);
     float z = s * s;
@@ -380,8 +381,7 @@ CM_FN double cm_rem_pio2_cw(double x, int *q, cm_dtab t) {
     double r = CM_FMA(-kf, t[CM_TRIG_PIO2], x);
     r = CM_FMA(-kf, t[CM_TRIG_PIO2 + 1], r);
     r = CM_FMA(-kf, t[CM_TRIG_PIO2 + 2], r);
-    double q4 = kf - 4.0 * cm_rint_small(kf * 0.25 - 0.375); /* kf mod 4, in 0..3 */
-    *q = (int)q4;
+    *q = (int)kf & 3;                           /* kf mod 4, |kf| < 2^30 */
     return r;
 }
 
@@ -457,8 +457,7 @@ CM_FN void cm_sincosf(float x, float *s, float *c) {
     float r = CM_FMAF(-kf, t[CM_TRIGF_PIO2], xr);
     r = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 1], r);
     r = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 2], r);
-    float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
-    int q = (int)q4;
+    int q = (int)kf & 3;
     if (huge) {
         cm_dtab td = CM_TAB(cm_dtab, cm_trig_tab);
         const double axd = (double)ax;
@@ -484,53 +483,59 @@ CM_FN float cm_tanf(float x) { float s, c; cm_sincosf(x, &s, &c); return s / c; 
 /* ----------------------------------------------- P-wide forms (HIP only) */
 
 /* The interpreter evaluates an operator for P points per lane at once. These
- * forms run exactly the operations of cm_exp, cm_log, cm_sincos, cm_expf,
- * cm_logf and cm_sincosf, in the same order, on each of the P elements (so
- * every element gets the bits of the scalar function), but interleaved
- * statement by statement: the P polynomial chains are independent, and the
- * coefficient table is loaded once for the P elements instead of once per
- * element. */
+ * forms give each of the P elements the bits of the scalar function (cm_exp,
+ * cm_log, cm_sincos, cm_expf, cm_logf, cm_sincosf), interleaved statement by
+ * statement: the P polynomial chains are independent, and the coefficient
+ * table is loaded once for the P elements instead of once per element. When
+ * every argument of the wavefront is ordinary (a finite argument of exp that
+ * neither overflows nor underflows, a positive finite argument of log, a
+ * trigonometric argument below the Payne-Hanek range) one uniform branch skips
+ * the special-value selects, which then would pass every value through
+ * unchanged; otherwise the wavefront runs the operations of the scalar
+ * function with its selects. */
 #if defined(__cplusplus) && (defined(__HIPCC__) || defined(__HIP__))
 #define CM_FORP _Pragma("unroll") for (int p = 0; p < P; ++p)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define CM_ANY(v) (__builtin_amdgcn_ballot_w64((v) != 0) != 0)
+#else
+#define CM_ANY(v) ((v) != 0)
+#endif
 
 template <int P>
 CM_FN void cm_exp_v(const double *x, double *res) {
+    int odd = 0;
+    CM_FORP odd |= !(cm_fabs(x[p]) <= CM_EXP_PLAIN);
+    if (CM_ANY(odd)) {
+        CM_FORP res[p] = cm_exp(x[p]);
+        return;
+    }
     cm_dtab t = CM_TAB(cm_dtab, cm_exp_tab);
-    int nan[P], hi[P], lo[P];
     double kf[P], r[P], q[P];
     CM_FORP {
-        nan[p] = cm_isnan(x[p]);
-        hi[p] = x[p] > 709.782712893384;
-        lo[p] = x[p] < -745.1332191019412;
-        const double xr = (nan[p] || hi[p] || lo[p]) ? 0.0 : x[p];
-        kf[p] = cm_rint_small(xr * t[0]);
-        r[p] = CM_FMA(-kf[p], t[1], xr);
+        kf[p] = CM_RINT(x[p] * t[0]);
+        r[p] = CM_FMA(-kf[p], t[1], x[p]);
         r[p] = CM_FMA(-kf[p], t[2], r[p]);
         q[p] = t[3];
     }
     _Pragma("unroll") for (int i = 4; i < CM_EXP_N; i++) CM_FORP q[p] = CM_HORNER(q[p], r[p], t[i]);
-    CM_FORP {
-        const int k = (int)kf[p];
-        const int big = k > 1022, small = k < -1020;
-        const int ka = big ? k - 2 : (small ? k + 1000 : k);
-        double v = q[p] * cm_pow2i(ka);
-        v = big ? v * 4.0 : (small ? v * cm_pow2i(-1000) : v);
-        res[p] = nan[p] ? x[p] : (hi[p] ? CM_INF : (lo[p] ? 0.0 : v));
-    }
+    CM_FORP res[p] = CM_LDEXP(q[p], (int)kf[p]);
 }
 
 template <int P>
 CM_FN void cm_log_v(const double *x, double *res) {
+    int odd = 0;
+    CM_FORP odd |= !(x[p] > 0.0 && x[p] < CM_INF);
+    if (CM_ANY(odd)) {
+        CM_FORP res[p] = cm_log(x[p]);
+        return;
+    }
     double f[P], s[P], z[P], R[P], dk[P];
     CM_FORP {
-        const int sub = x[p] > 0.0 && x[p] < 2.2250738585072014e-308;
-        const double xs = sub ? x[p] * 18014398509481984.0 : x[p]; /* 2^54 */
-        const uint64_t u = cm_bits(xs);
-        int e = (int)((u >> 52) & 0x7ff) - (sub ? 54 : 0) - 1023;
-        double m = cm_dbl((u & 0x000fffffffffffffULL) | 0x3ff0000000000000ULL);
-        const int up = m > 1.4142135623730951;
-        m = up ? m * 0.5 : m;
-        e = up ? e + 1 : e;
+        int e;
+        double m = CM_FREXP(x[p], &e);
+        const int dn = m <= 0.7071067811865476;
+        m = dn ? m + m : m;
+        e = dn ? e - 1 : e;
         f[p] = m - 1.0;
         s[p] = f[p] / (2.0 + f[p]);
         z[p] = s[p] * s[p];
@@ -542,34 +547,23 @@ CM_FN void cm_log_v(const double *x, double *res) {
     CM_FORP {
         const double Rz = R[p] * z[p];
         const double hfsq = 0.5 * (f[p] * f[p]);
-        const double v = dk[p] * t[CM_LOG_P] -
-                         ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[CM_LOG_P + 1])) - f[p]);
-        res[p] = cm_isnan(x[p]) ? x[p]
-                 : (x[p] < 0.0 ? CM_NAN : (x[p] == 0.0 ? -CM_INF : (x[p] == CM_INF ? x[p] : v)));
+        res[p] = dk[p] * t[CM_LOG_P] -
+                 ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[CM_LOG_P + 1])) - f[p]);
     }
 }
 
 template <int P>
 CM_FN void cm_sincos_v(const double *x, double *so, double *co) {
+    int odd = 0;
+    CM_FORP odd |= !(cm_fabs(x[p]) < CM_PH_MIN);
+    if (CM_ANY(odd)) {
+        CM_FORP cm_sincos(x[p], &so[p], &co[p]);
+        return;
+    }
     cm_dtab t = CM_TAB(cm_dtab, cm_trig_tab);
-    int bad[P], q[P], huge[P], any_huge = 0;
+    int q[P];
     double r[P], z[P], ps[P], pc[P];
-    CM_FORP {
-        const double ax = cm_fabs(x[p]);
-        bad[p] = !(ax < CM_INF);
-        huge[p] = !bad[p] && ax >= CM_PH_MIN;
-        any_huge |= huge[p];
-        const double xr = (bad[p] || huge[p]) ? 0.0 : x[p];
-        r[p] = cm_rem_pio2_cw(xr, &q[p], t);
-    }
-    if (any_huge) { /* one branch for the P points; the reduction rarely runs */
-        CM_FORP if (huge[p]) {
-            int qh;
-            const double rh = cm_rem_pio2_huge(cm_fabs(x[p]), &qh, t);
-            r[p] = x[p] < 0.0 ? -rh : rh;
-            q[p] = (x[p] < 0.0 ? -qh : qh) & 3;
-        }
-    }
+    CM_FORP r[p] = cm_rem_pio2_cw(x[p], &q[p], t);
     CM_FORP {
         z[p] = r[p] * r[p];
         ps[p] = t[CM_TRIG_S];
@@ -584,53 +578,48 @@ CM_FN void cm_sincos_v(const double *x, double *so, double *co) {
         const double hz = 0.5 * z[p];
         const double w = 1.0 - hz;
         const double cr = w + (((1.0 - w) - hz) + z[p] * (z[p] * pc[p]));
-        double sv = (q[p] & 1) ? cr : sr;
-        double cv = (q[p] & 1) ? sr : cr;
-        sv = (q[p] & 2) ? -sv : sv;
-        cv = ((q[p] + 1) & 2) ? -cv : cv;
-        so[p] = bad[p] ? CM_NAN : sv;
-        co[p] = bad[p] ? CM_NAN : cv;
+        const double sv = (q[p] & 1) ? cr : sr;
+        const double cv = (q[p] & 1) ? sr : cr;
+        so[p] = (q[p] & 2) ? -sv : sv;
+        co[p] = ((q[p] + 1) & 2) ? -cv : cv;
     }
 }
 
 template <int P>
 CM_FN void cm_expf_v(const float *x, float *res) {
+    int odd = 0;
+    CM_FORP odd |= !(cm_fabsf(x[p]) <= CM_EXPF_PLAIN);
+    if (CM_ANY(odd)) {
+        CM_FORP res[p] = cm_expf(x[p]);
+        return;
+    }
     cm_ftab t = CM_TAB(cm_ftab, cm_expf_tab);
-    int nan[P], hi[P], lo[P];
     float kf[P], r[P], q[P];
     CM_FORP {
-        nan[p] = x[p] != x[p];
-        hi[p] = x[p] > 88.72283f;
-        lo[p] = x[p] < -103.97208f;
-        const float xr = (nan[p] || hi[p] || lo[p]) ? 0.0f : x[p];
-        kf[p] = cm_rint_smallf(xr * t[0]);
-        r[p] = CM_FMAF(-kf[p], t[1], xr);
+        kf[p] = cm_rint_smallf(x[p] * t[0]);
+        r[p] = CM_FMAF(-kf[p], t[1], x[p]);
         r[p] = CM_FMAF(-kf[p], t[2], r[p]);
         q[p] = t[3];
     }
     _Pragma("unroll") for (int i = 4; i < CM_EXPF_N; i++) CM_FORP q[p] = CM_HORNERF(q[p], r[p], t[i]);
-    CM_FORP {
-        const int k = (int)kf[p];
-        const int big = k > 126, small = k < -124;
-        const int ka = big ? k - 2 : (small ? k + 100 : k);
-        float v = q[p] * cm_pow2if(ka);
-        v = big ? v * 4.0f : (small ? v * cm_pow2if(-100) : v);
-        res[p] = nan[p] ? x[p] : (hi[p] ? CM_INFF : (lo[p] ? 0.0f : v));
-    }
+    CM_FORP res[p] = CM_LDEXPF(q[p], (int)kf[p]);
 }
 
 template <int P>
 CM_FN void cm_logf_v(const float *x, float *res) {
+    int odd = 0;
+    CM_FORP odd |= !(x[p] > 0.0f && x[p] < CM_INFF);
+    if (CM_ANY(odd)) {
+        CM_FORP res[p] = cm_logf(x[p]);
+        return;
+    }
     float f[P], s[P], z[P], R[P], dk[P];
     CM_FORP {
-        const int sub = x[p] > 0.0f && x[p] < 1.17549435e-38f;
-        const float xs = sub ? x[p] * 33554432.0f : x[p]; /* 2^25 */
-        const uint32_t u = cm_bitsf(xs);
-        int e = (int)((u >> 23) & 0xff) - (sub ? 25 : 0) - 127;
-        float m = cm_flt((u & 0x007fffffu) | 0x3f800000u);
-        const int up = m > 1.4142135381698608f;
-        m = up ? m * 0.5f : m;
-        e = up ? e + 1 : e;
+        int e;
+        float m = CM_FREXPF(x[p], &e);
+        const int dn = m <= 0.70710676908493042f;
+        m = dn ? m + m : m;
+        e = dn ? e - 1 : e;
         f[p] = m - 1.0f;
         s[p] = f[p] / (2.0f + f[p]);
         z[p] = s[p] * s[p];
@@ -642,43 +631,28 @@ CM_FN void cm_logf_v(const float *x, float *res) {
     CM_FORP {
         const float Rz = R[p] * z[p];
         const float hfsq = 0.5f * (f[p] * f[p]);
-        const float v = dk[p] * t[CM_LOGF_P] -
-                        ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[CM_LOGF_P + 1])) - f[p]);
-        res[p] = (x[p] != x[p]) ? x[p]
-                 : (x[p] < 0.0f ? CM_NANF
-                                : (x[p] == 0.0f ? -CM_INFF : (x[p] == CM_INFF ? x[p] : v)));
+        res[p] = dk[p] * t[CM_LOGF_P] -
+                 ((hfsq - (s[p] * (hfsq + Rz) + dk[p] * t[CM_LOGF_P + 1])) - f[p]);
     }
 }
 
 template <int P>
 CM_FN void cm_sincosf_v(const float *x, float *so, float *co) {
+    int odd = 0;
+    CM_FORP odd |= !(cm_fabsf(x[p]) < CM_F64_RED_MINF);
+    if (CM_ANY(odd)) {
+        CM_FORP cm_sincosf(x[p], &so[p], &co[p]);
+        return;
+    }
     cm_ftab t = CM_TAB(cm_ftab, cm_trigf_tab);
-    int bad[P], q[P], huge[P], any_huge = 0;
+    int q[P];
     float r[P], z[P], ps[P], pc[P];
     CM_FORP {
-        const float ax = cm_fabsf(x[p]);
-        bad[p] = !(ax < CM_INFF);
-        huge[p] = !bad[p] && ax >= CM_F64_RED_MINF;
-        any_huge |= huge[p];
-        const float xr = (bad[p] || huge[p]) ? 0.0f : x[p];
-        const float kf = cm_rint_smallf(xr * t[CM_TRIGF_2PI]);
-        float rr = CM_FMAF(-kf, t[CM_TRIGF_PIO2], xr);
+        const float kf = cm_rint_smallf(x[p] * t[CM_TRIGF_2PI]);
+        float rr = CM_FMAF(-kf, t[CM_TRIGF_PIO2], x[p]);
         rr = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 1], rr);
-        rr = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 2], rr);
-        const float q4 = kf - 4.0f * cm_rint_smallf(kf * 0.25f - 0.375f);
-        q[p] = (int)q4;
-        r[p] = rr;
-    }
-    if (any_huge) { /* one branch for the P points; the reduction rarely runs */
-        cm_dtab td = CM_TAB(cm_dtab, cm_trig_tab);
-        CM_FORP if (huge[p]) {
-            const double axd = (double)cm_fabsf(x[p]);
-            int qh;
-            const double rd = axd >= CM_PH_MIN ? cm_rem_pio2_huge(axd, &qh, td)
-                                                        : cm_rem_pio2_cw(axd, &qh, td);
-            r[p] = (float)(x[p] < 0.0f ? -rd : rd);
-            q[p] = (x[p] < 0.0f ? -qh : qh) & 3;
-        }
+        r[p] = CM_FMAF(-kf, t[CM_TRIGF_PIO2 + 2], rr);
+        q[p] = (int)kf & 3;
     }
     CM_FORP {
         z[p] = r[p] * r[p];
@@ -694,15 +668,14 @@ CM_FN void cm_sincosf_v(const float *x, float *so, float *co) {
         const float hz = 0.5f * z[p];
         const float w = 1.0f - hz;
         const float cr = w + (((1.0f - w) - hz) + z[p] * (z[p] * pc[p]));
-        float sv = (q[p] & 1) ? cr : sr;
-        float cv = (q[p] & 1) ? sr : cr;
-        sv = (q[p] & 2) ? -sv : sv;
-        cv = ((q[p] + 1) & 2) ? -cv : cv;
-        so[p] = bad[p] ? CM_NANF : sv;
-        co[p] = bad[p] ? CM_NANF : cv;
+        const float sv = (q[p] & 1) ? cr : sr;
+        const float cv = (q[p] & 1) ? sr : cr;
+        so[p] = (q[p] & 2) ? -sv : sv;
+        co[p] = ((q[p] + 1) & 2) ? -cv : cv;
     }
 }
 #undef CM_FORP
+#undef CM_ANY
 #endif
 
 /* ------------------------------------------------------ hyperbolic, pow */

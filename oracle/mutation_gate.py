@@ -122,10 +122,10 @@ DEVICE_MUTANTS = [
      "case OP_SIN: CUSR_MATH_V(sincos_v, a + c0, r + c0, d + c0); break;",
      "case OP_SIN: CUSR_MATH_V(sincos_v, a + c0, r + c0, d + c0); CUSR_FOR_P d[p] = -d[p]; break;",
      0, "d sin(a)/da = -cos(a) on the device", "c1 or c2_small"),
-    ("dev-div-partials-swapped", "cusr_amd/csrc/lm_device.h",
-     "CUSR_FOR_P { o[p] = l[p] / rv[p]; d1[p] = one / rv[p]; d2[p] = -(o[p] * d1[p]); }",
-     "CUSR_FOR_P { o[p] = l[p] / rv[p]; d2[p] = one / rv[p]; d1[p] = -(o[p] * d2[p]); }",
-     0, "the partials of l / r exchanged on the device", "c1 or c2_small"),
+    ("dev-pdiv-partials-swapped", "cusr_amd/csrc/lm_device.h",
+     "            d1[p] = prot ? zero : inv;\n            d2[p] = prot ? zero : -(q * inv);",
+     "            d2[p] = prot ? zero : inv;\n            d1[p] = prot ? zero : -(q * inv);",
+     0, "the partials of the protected l / r exchanged on the device", "c1 or c2_small"),
     ("dev-adjoint-seed", "cusr_amd/csrc/lm_device.h",
      "CUSR_FOR_P accadj[p] = R(1);", "CUSR_FOR_P accadj[p] = R(2);", 0,
      "the device's reverse sweep starts from adjoint 2", "c1"),

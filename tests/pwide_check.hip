@@ -33,8 +33,8 @@ static double arg(int i) {
     const double s = (next_u64() & 1) ? -1.0 : 1.0;
     switch (i % 4) {
     case 0: return s * uni01() * 10.0;
-    case 1: return s * (1.0 + uni01()) * cm_pow2i((int)(uni01() * 2040.0) - 1020);
-    case 2: return s * (1.0 + uni01()) * cm_pow2i((int)(uni01() * 40.0));
+    case 1: return s * CM_LDEXP(1.0 + uni01(), (int)(uni01() * 2040.0) - 1020);
+    case 2: return s * CM_LDEXP(1.0 + uni01(), (int)(uni01() * 40.0));
     default: {
         uint64_t b = next_u64();   // any bit pattern
         return cm_dbl(b);

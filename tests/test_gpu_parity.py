@@ -121,6 +121,46 @@ def test_operators_bit_exact(co, precision):
     assert not bad
 
 
+def _edge_inputs():
+    """fp64 arguments at the special ranges of the elementary functions: exp's
+    overflow and subnormal-result ends, log's subnormal, zero, negative and
+    infinite arguments, trigonometric arguments near multiples of pi/2, at the
+    Payne-Hanek switch (2^30) and huge, fp32's reduction switch (2^17), NaN."""
+    rng = np.random.default_rng(11)
+    v = [0.0, -0.0, np.inf, -np.inf, np.nan, 5e-324, -5e-324, 1e-310, 2.2250738585072014e-308,
+         np.nextafter(2.2250738585072014e-308, 0), 1.0, -1.0, np.nextafter(1.0, 2),
+         np.nextafter(1.0, 0), 2.0 ** 30, np.nextafter(2.0 ** 30, 0), 2.0 ** 17,
+         np.nextafter(2.0 ** 17, 0), 1e22, -1e22, 1e300, 20.0, np.nextafter(20.0, 30)]
+    v += list(rng.uniform(-746.0, -706.0, 600)) + list(rng.uniform(706.0, 711.0, 200))
+    v += list(rng.uniform(87.0, 89.5, 100)) + list(rng.uniform(-105.0, -86.0, 200))
+    v += list(np.ldexp(rng.uniform(0.5, 1.0, 300), rng.integers(-1074, -1020, 300)))
+    v += list(np.ldexp(rng.uniform(0.5, 1.0, 200), rng.integers(-149, -120, 200)))
+    k = rng.integers(-10 ** 6, 10 ** 6, 400).astype(np.float64)
+    v += list(k * (np.pi / 2) + rng.uniform(-1e-6, 1e-6, 400))
+    v += list(rng.uniform(-1.0, 1.0, 200) * 2.0 ** rng.integers(16, 64, 200))
+    x = np.asarray(v, np.float64)
+    return np.concatenate([x, -x])
+
+
+@pytest.mark.parametrize("precision", [0, 1])
+def test_operators_edge_values_bit_exact(co, precision):
+    """The unary operators at the special ranges of exp, log, sin and cos,
+    fp64 inputs (fp32 in mixed precision), device vs oracle: identical bits."""
+    from cusr_amd.benchmark import popio
+    unary = [14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 33, 34, 35]
+    x = _edge_inputs()
+    xs = np.stack([x, np.ones_like(x)], axis=1)
+    trees = [([2, 0], [f, 0], [-1, -1], []) for f in unary]
+    pop = popio.build_pop(trees, xs.astype(np.float32), np.zeros((len(trees), len(x))))
+    _say(f"edge values precision={precision} N={len(x)}")
+    yg = co.evaluate(pop, np.zeros(1), xs, precision=precision)
+    yo = lm_oracle.eval_pop(pop, c=np.zeros(1), xs=xs, precision=precision)
+    same = (yg == yo) | (np.isnan(yg) & np.isnan(yo))
+    bad = [(unary[m], int(np.sum(~same[m]))) for m in range(len(unary)) if not same[m].all()]
+    _say(f"mismatching ops (id, count): {bad}")
+    assert not bad
+
+
 @pytest.mark.parametrize("parts,ad_mode,precision", [(2, 0, 0), (4, 0, 0), (4, 1, 0), (2, 0, 1)])
 def test_point_partitions_match_oracle(co, parts, ad_mode, precision):
     """Several wavefronts per expression: granule g of 64 points goes to

@@ -13,3 +13,12 @@ def test_mutants_are_killed():
     assert sorted(r[0] for r in rows) == sorted(names)
     survivors = [r[0] for r in rows if not r[2]]
     assert not survivors, survivors
+
+
+def test_every_mutant_anchor_is_in_the_sources():
+    """Each mutant's edit still finds its text (a source change that moves an
+    anchor would make the gate stop at build time)."""
+    for name, rel, old, _new, occ, *_rest in mutation_gate.MUTANTS + mutation_gate.DEVICE_MUTANTS:
+        if old is None:
+            continue
+        assert (mutation_gate.REPO / rel).read_text().count(old) > occ, name
