@@ -495,16 +495,33 @@ CUSR_SCALE_ASM(float, "v_mul_f32", "v_mov_b32")
 #undef CUSR_Z
 #undef CUSR_IN
 
-// Entries J..K-1 of the tangent rows, one asm block per entry.
+// Entries J..K-1 of the tangent rows, one asm block per entry. For K > 8 the
+// entries go in groups of 8 behind one test of the group's mask bits, so a
+// range costs the tests of the groups it touches instead of K tests (the
+// general kernel's K = 32 chain: 64 bit tests per multiplicative step).
 template <int K, int J, typename R, int P>
 __device__ __forceinline__ void scale_entries(R *T, const R *d, const uint64_t *z, uint32_t m,
-                                              uint32_t sel) {
-    if constexpr (J < K) {
+                                              uint32_t sel);
+template <int K, int J, int E, typename R, int P>
+__device__ __forceinline__ void scale_group(R *T, const R *d, const uint64_t *z, uint32_t m,
+                                            uint32_t sel) {
+    if constexpr (J < E) {
         R t[P];
         CUSR_FOR_P t[p] = T[p * K + J];
         ScaleAsm<R, P>::template run<J>(t, d, z, m, sel);
         CUSR_FOR_P T[p * K + J] = t[p];
-        scale_entries<K, J + 1, R, P>(T, d, z, m, sel);
+        scale_group<K, J + 1, E, R, P>(T, d, z, m, sel);
+    }
+}
+template <int K, int J, typename R, int P>
+__device__ __forceinline__ void scale_entries(R *T, const R *d, const uint64_t *z, uint32_t m,
+                                              uint32_t sel) {
+    if constexpr (K <= 8) {
+        scale_group<K, J, K, R, P>(T, d, z, m, sel);
+    } else if constexpr (J < K) {
+        constexpr int E = (J + 8 < K) ? J + 8 : K;
+        if ((m >> J) & 0xffu) scale_group<K, J, E, R, P>(T, d, z, m, sel);
+        scale_entries<K, E, R, P>(T, d, z, m, sel);
     }
 }
 
