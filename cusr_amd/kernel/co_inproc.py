@@ -58,7 +58,7 @@ def co_partitions_for_n(N: int) -> int:
         while g < CO_MAX_SPLIT and g * 2 * 4096 <= N:
             g *= 2
         return g
-    return 4 if N >= 16384 else (2 if N >= 1024 else 1)
+    return 4 if N >= 16384 else (2 if N >= 512 else 1)
 
 
 def co_partitions_for(N: int, ad_mode: int = 0) -> int:

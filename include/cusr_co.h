@@ -134,9 +134,12 @@ typedef struct CoOptions {
  * is 0: 64-point granule g belongs to partition g mod G, each partition is
  * summed by its own wavefront, so long expressions use several wavefronts.
  * A function of N only, so an expression fits the same alone or in any
- * population. Measured on MI355X: two partitions from N = 1,024 shorten the
+ * population. Measured on MI355X: two partitions from N = 512 shorten the
  * slowest expressions of a K bin, which set its duration (C2 -11 %, C3
- * -20 %, C5 even); four pay off only for long expressions. From
+ * -20 %, C5 even), and give a bin of few expressions twice the wavefronts (a
+ * GP generation of 4,000 expressions at N = 1,000, whose fast K bins hold
+ * 150-500 expressions each: 103.5 -> 76.4 ms per fit); four pay off only for
+ * long expressions (C2 +27 %). From
  * CO_SPLIT_MIN_N points an expression's passes spread over G = N / 4,096
  * (rounded down to a power of two, 16 to CO_MAX_SPLIT) workgroups, whose
  * partition sums meet in HBM and are added in partition order by a step
@@ -153,7 +156,7 @@ static inline int co_partitions_for_n(int N) {
         while (g < CO_MAX_SPLIT && (long)g * 2 * 4096 <= (long)N) g *= 2;
         return g;
     }
-    return N >= 16384 ? 4 : (N >= 1024 ? 2 : 1);
+    return N >= 16384 ? 4 : (N >= 512 ? 2 : 1);
 }
 
 /* Point partitions when CoOptions.partitions is 0, by N and the AD mode.
