@@ -369,6 +369,37 @@ typedef hipError_t (*Launcher)(int, unsigned, size_t, hipStream_t, const FitArgs
 // descriptors of a range are in launch order (decode_population /
 // decode_range): a population decoded in several ranges has its bins planned
 // range by range.
+
+// The split path's step launch for a bin: the fast bins (K = 1..CO_FAST_MAX_K,
+// every expression of that K) take the instance whose solve is unrolled for
+// their K, the general bin and K = 0 the runtime-K one.
+template <int KS>
+static void launch_step_k(unsigned n, hipStream_t s, const FitArgs &fa, int mixed) {
+    lm_step_kernel<KS><<<n, kLanes, 0, s>>>(fa, mixed);
+}
+static void launch_step(int bin, unsigned n, hipStream_t s, const FitArgs &fa, int mixed) {
+    static_assert(CO_FAST_MAX_K == 16, "one step instance per fast K");
+    switch (bin) {
+    case 1: launch_step_k<1>(n, s, fa, mixed); break;
+    case 2: launch_step_k<2>(n, s, fa, mixed); break;
+    case 3: launch_step_k<3>(n, s, fa, mixed); break;
+    case 4: launch_step_k<4>(n, s, fa, mixed); break;
+    case 5: launch_step_k<5>(n, s, fa, mixed); break;
+    case 6: launch_step_k<6>(n, s, fa, mixed); break;
+    case 7: launch_step_k<7>(n, s, fa, mixed); break;
+    case 8: launch_step_k<8>(n, s, fa, mixed); break;
+    case 9: launch_step_k<9>(n, s, fa, mixed); break;
+    case 10: launch_step_k<10>(n, s, fa, mixed); break;
+    case 11: launch_step_k<11>(n, s, fa, mixed); break;
+    case 12: launch_step_k<12>(n, s, fa, mixed); break;
+    case 13: launch_step_k<13>(n, s, fa, mixed); break;
+    case 14: launch_step_k<14>(n, s, fa, mixed); break;
+    case 15: launch_step_k<15>(n, s, fa, mixed); break;
+    case 16: launch_step_k<16>(n, s, fa, mixed); break;
+    default: launch_step_k<0>(n, s, fa, mixed); break;
+    }
+}
+
 struct FitRun {
     struct Segment {
         int parts, it_end, resume;
@@ -596,7 +627,7 @@ struct FitRun {
                 fk.resume = 0;
                 for (int r = 0; r < rounds; ++r) {
                     CO_LAUNCH_HIP(launch_pass(b.bin, (unsigned)b.cnt * parts, b.lds[0], ks, fk));
-                    lm_step_kernel<<<b.cnt, kLanes, 0, ks>>>(fk, mixed ? 1 : 0);
+                    launch_step(b.bin, (unsigned)b.cnt, ks, fk, mixed ? 1 : 0);
                     CO_LAUNCH_HIP(hipGetLastError());
                 }
             } else {

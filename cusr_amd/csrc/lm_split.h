@@ -128,6 +128,11 @@ lm_pass_kernel(FitArgs fa) {
 // One LM step of one expression (a wavefront): the G partition sums of its
 // pending pass added in partition order, then fit_one's decisions. The state
 // row is worked on in LDS and written back.
+// KS > 0: every expression of the launch has K = KS (a fast kernel's bin), and
+// the solve is damped_solve<KS>, unrolled in registers; KS = 0: the runtime-K
+// solve in LDS (the general bin). Both give the same bits; the unrolled one has
+// no chain of LDS round trips (C3's step launches: the solves of K <= 16).
+template <int KS>
 __global__ void __launch_bounds__(kLanes) lm_step_kernel(FitArgs fa, int mixed) {
     __shared__ double s_new[sums_width(CO_MAX_K)];
     __shared__ double s_cur[sums_width(CO_MAX_K)];
@@ -139,7 +144,7 @@ __global__ void __launch_bounds__(kLanes) lm_step_kernel(FitArgs fa, int mixed) 
     double *sv = fa.state + (size_t)e.y_row * fa.state_stride;
     const int kind = (int)uni(sv[kSpPending]);
     if (kind == SP_NONE) return;
-    const int K = e.K;
+    const int K = KS > 0 ? KS : e.K;
     const int G = fa.parts;
     const bool audit = kind == SP_AUDIT_CUR || kind == SP_AUDIT_INIT;
     const int W = (audit || K == 0) ? 1 : sums_width(K);
@@ -219,7 +224,19 @@ __global__ void __launch_bounds__(kLanes) lm_step_kernel(FitArgs fa, int mixed) 
         double dn = 0.0, cn = 0.0;
         while (st == ST_RUN && it < fa.max_iter) {
             ++it;
-            if (!damped_solve_rt(s_cur, lambda, K, L, lane)) {
+            bool solved;
+            if constexpr (KS > 0) {
+                double delta[KS];
+                solved = damped_solve<KS>(s_cur, lambda, delta);
+                if (solved && lane == 0) {
+#pragma unroll
+                    for (int j = 0; j < KS; ++j) L[KS * KS + j] = delta[j];
+                }
+                wave_sync_lds();
+            } else {
+                solved = damped_solve_rt(s_cur, lambda, K, L, lane);
+            }
+            if (!solved) {
                 lambda = lambda * 10.0;
                 if (lambda > 1e12) st = ST_CHOL;
                 continue;
