@@ -495,10 +495,12 @@ CUSR_SCALE_ASM(float, "v_mul_f32", "v_mov_b32")
 #undef CUSR_Z
 #undef CUSR_IN
 
-// Entries J..K-1 of the tangent rows, one asm block per entry. For K > 8 the
-// entries go in groups of 8 behind one test of the group's mask bits, so a
-// range costs the tests of the groups it touches instead of K tests (the
-// general kernel's K = 32 chain: 64 bit tests per multiplicative step).
+// Entries J..K-1 of the tangent rows, one asm block per entry. From K = 5 the
+// entries go in groups (of 4 up to K = 8, of 8 beyond) behind one test of the
+// group's mask bits, so a range costs the tests of the groups it touches
+// instead of K tests (the general kernel's K = 32 chain: 64 bit tests per
+// multiplicative step; G1 121.0 -> 103.8 ms; groups of 4 at K = 5..8: C4
+// 144.3 -> 141.6 ms, C2 -0.5 %).
 template <int K, int J, typename R, int P>
 __device__ __forceinline__ void scale_entries(R *T, const R *d, const uint64_t *z, uint32_t m,
                                               uint32_t sel);
@@ -516,11 +518,13 @@ __device__ __forceinline__ void scale_group(R *T, const R *d, const uint64_t *z,
 template <int K, int J, typename R, int P>
 __device__ __forceinline__ void scale_entries(R *T, const R *d, const uint64_t *z, uint32_t m,
                                               uint32_t sel) {
-    if constexpr (K <= 8) {
+    constexpr int GS = K > 8 ? 8 : 4;
+    constexpr unsigned GM = (1u << GS) - 1u;
+    if constexpr (K <= 4) {
         scale_group<K, J, K, R, P>(T, d, z, m, sel);
     } else if constexpr (J < K) {
-        constexpr int E = (J + 8 < K) ? J + 8 : K;
-        if ((m >> J) & 0xffu) scale_group<K, J, E, R, P>(T, d, z, m, sel);
+        constexpr int E = (J + GS < K) ? J + GS : K;
+        if ((m >> J) & GM) scale_group<K, J, E, R, P>(T, d, z, m, sel);
         scale_entries<K, E, R, P>(T, d, z, m, sel);
     }
 }
