@@ -482,6 +482,50 @@ template <typename R, int P> struct ScaleAsm;
                                CUSR_Z(3), CUSR_Z(4), CUSR_Z(5), CUSR_Z(6), CUSR_Z(7) : "scc");           \
         }                                                                                        \
     };
+#define CUSR_PLAIN_ASM(R, MUL)                                                                   \
+    template <> struct PlainAsm<R, 1> {                                                          \
+        template <int J>                                                                         \
+        static __device__ __forceinline__ void run(R *t, const R *d, uint32_t m) {               \
+            __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_SKIP_TAIL                      \
+                             : CUSR_T(0) : [m] "s"(m), [j] "n"(J), CUSR_D(0) : "scc");            \
+        }                                                                                        \
+    };                                                                                           \
+    template <> struct PlainAsm<R, 2> {                                                          \
+        template <int J>                                                                         \
+        static __device__ __forceinline__ void run(R *t, const R *d, uint32_t m) {               \
+            __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_MUL(MUL, 1) CUSR_SKIP_TAIL     \
+                             : CUSR_T(0), CUSR_T(1) : [m] "s"(m), [j] "n"(J), CUSR_D(0), CUSR_D(1) \
+                             : "scc");                                                           \
+        }                                                                                        \
+    };                                                                                           \
+    template <> struct PlainAsm<R, 4> {                                                          \
+        template <int J>                                                                         \
+        static __device__ __forceinline__ void run(R *t, const R *d, uint32_t m) {               \
+            __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_MUL(MUL, 1) CUSR_MUL(MUL, 2)   \
+                                 CUSR_MUL(MUL, 3) CUSR_SKIP_TAIL                                 \
+                             : CUSR_T(0), CUSR_T(1), CUSR_T(2), CUSR_T(3)                        \
+                             : [m] "s"(m), [j] "n"(J), CUSR_D(0), CUSR_D(1), CUSR_D(2), CUSR_D(3) \
+                             : "scc");                                                           \
+        }                                                                                        \
+    };                                                                                           \
+    template <> struct PlainAsm<R, 8> {                                                          \
+        template <int J>                                                                         \
+        static __device__ __forceinline__ void run(R *t, const R *d, uint32_t m) {               \
+            __asm__ volatile(CUSR_SKIP_HEAD CUSR_MUL(MUL, 0) CUSR_MUL(MUL, 1) CUSR_MUL(MUL, 2)   \
+                                 CUSR_MUL(MUL, 3) CUSR_MUL(MUL, 4) CUSR_MUL(MUL, 5)              \
+                                     CUSR_MUL(MUL, 6) CUSR_MUL(MUL, 7) CUSR_SKIP_TAIL            \
+                             : CUSR_T(0), CUSR_T(1), CUSR_T(2), CUSR_T(3), CUSR_T(4), CUSR_T(5), \
+                               CUSR_T(6), CUSR_T(7)                                              \
+                             : [m] "s"(m), [j] "n"(J), CUSR_D(0), CUSR_D(1), CUSR_D(2), CUSR_D(3), \
+                               CUSR_D(4), CUSR_D(5), CUSR_D(6), CUSR_D(7) : "scc");              \
+        }                                                                                        \
+    };
+// PlainAsm<R, P>::run<J>: the same block without the select rule (operators
+// that are not flat-branch ones: no lane masks and no test of sel per entry).
+template <typename R, int P> struct PlainAsm;
+CUSR_PLAIN_ASM(double, "v_mul_f64")
+CUSR_PLAIN_ASM(float, "v_mul_f32")
+#undef CUSR_PLAIN_ASM
 CUSR_SCALE_ASM(double, "v_mul_f64", "v_mov_b64")
 CUSR_SCALE_ASM(float, "v_mul_f32", "v_mov_b32")
 #undef CUSR_SCALE_ASM
@@ -515,6 +559,28 @@ __device__ __forceinline__ void scale_group(R *T, const R *d, const uint64_t *z,
         scale_group<K, J + 1, E, R, P>(T, d, z, m, sel);
     }
 }
+template <int K, int J, int E, typename R, int P>
+__device__ __forceinline__ void plain_group(R *T, const R *d, uint32_t m) {
+    if constexpr (J < E) {
+        R t[P];
+        CUSR_FOR_P t[p] = T[p * K + J];
+        PlainAsm<R, P>::template run<J>(t, d, m);
+        CUSR_FOR_P T[p * K + J] = t[p];
+        plain_group<K, J + 1, E, R, P>(T, d, m);
+    }
+}
+template <int K, int J, typename R, int P>
+__device__ __forceinline__ void plain_entries(R *T, const R *d, uint32_t m) {
+    constexpr int GS = K > 8 ? 8 : 4;
+    constexpr unsigned GM = (1u << GS) - 1u;
+    if constexpr (K <= 4) {
+        plain_group<K, J, K, R, P>(T, d, m);
+    } else if constexpr (J < K) {
+        constexpr int E = (J + GS < K) ? J + GS : K;
+        if ((m >> J) & GM) plain_group<K, J, E, R, P>(T, d, m);
+        plain_entries<K, E, R, P>(T, d, m);
+    }
+}
 template <int K, int J, typename R, int P>
 __device__ __forceinline__ void scale_entries(R *T, const R *d, const uint64_t *z, uint32_t m,
                                               uint32_t sel) {
@@ -539,12 +605,16 @@ __device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, co
     } else {   // hi up to 32: the shift is formed in 64 bits
         mask = (uint32_t)(((uint64_t)1 << hi) - 1u) & ~(uint32_t)(((uint64_t)1 << lo) - 1u);
     }
-    // the flat-branch lane masks are only read by the select rule: no
-    // vector-to-scalar transfer on the other operators' steps
-    uint64_t zm[P];
-    CUSR_FOR_P zm[p] = 0;
-    if (sel) CUSR_FOR_P zm[p] = __builtin_amdgcn_ballot_w64(z[p]);
-    scale_entries<K, 0, R, P>(T, d, zm, mask, sel ? 1u : 0u);
+    // one uniform test of sel: the select rule's lane masks (a vector-to-scalar
+    // transfer) and its per-entry test only on the flat-branch operators'
+    // steps (C2 -3.5 %, C4 -3.3 %)
+    if (sel) {
+        uint64_t zm[P];
+        CUSR_FOR_P zm[p] = __builtin_amdgcn_ballot_w64(z[p]);
+        scale_entries<K, 0, R, P>(T, d, zm, mask, 1u);
+    } else {
+        plain_entries<K, 0, R, P>(T, d, mask);
+    }
 }
 
 // T[p*K + k] += v[p] for a wave-uniform k, the add in the branch of entry k.
