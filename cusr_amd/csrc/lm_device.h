@@ -304,15 +304,31 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
 
 // Value o = l op rv and partials d1 = do/dl, d2 = do/drv for P points.
 // want_d2 false skips log(l) of POW when no constant is on the right.
-template <typename R, int P>
+// UNIT false leaves the partials that are exactly 1 (ADD's two, SUB's left)
+// unset: the forward sweep never reads them, and a register left unset on
+// that branch is not copied into at every ADD step. (The flat flags z1, z2
+// keep their defaults: a lane mask left unset on a branch is merged with the
+// execution mask at the join, which costs more than clearing it.)
+template <typename R, int P, bool UNIT = true>
 __device__ __forceinline__ void binary_p(int f, const R *l, const R *rv, bool want_d2, R *o,
                                          R *d1, R *d2, bool *z1, bool *z2) {
     typedef Fn<R> F;
     const R one = R(1), zero = R(0);
     CUSR_FOR_P { z1[p] = false; z2[p] = false; }
     switch (f) {
-    case OP_ADD: CUSR_FOR_P { o[p] = l[p] + rv[p]; d1[p] = one; d2[p] = one; } break;
-    case OP_SUB: CUSR_FOR_P { o[p] = l[p] - rv[p]; d1[p] = one; d2[p] = -one; } break;
+    case OP_ADD:
+        CUSR_FOR_P {
+            o[p] = l[p] + rv[p];
+            if constexpr (UNIT) { d1[p] = one; d2[p] = one; }
+        }
+        break;
+    case OP_SUB:
+        CUSR_FOR_P {
+            o[p] = l[p] - rv[p];
+            if constexpr (UNIT) d1[p] = one;
+            d2[p] = -one;
+        }
+        break;
     case OP_MUL: CUSR_FOR_P { o[p] = l[p] * rv[p]; d1[p] = rv[p]; d2[p] = l[p]; } break;
     // d(l/r)/dr = -(l/r) * (1/r): one division for the value, one for 1/r
     case OP_DIV: case OP_LOOSE_DIV:
@@ -677,20 +693,22 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
         const int ak = F::akind(ins), ai = F::aidx(ins);
         R a[P], b[P], o[P], d1[P], d2[P];
         bool z1[P], z2[P];
+        const bool bin = F::binary(ins);
+        // the right operand first: the accumulator is then dead once the left
+        // one is fetched, and the left operand can share its registers
+        if (bin) fetch<R, P>(F::bkind(ins), F::bidx(ins), acc, w, cs, lane, b);
         fetch<R, P>(ak, ai, acc, w, cs, lane, a);
         const int lo = F::lo(ins), mid = F::mid(ins), hi = F::hi(ins);
-        if (F::binary(ins)) {
-            const int bk = F::bkind(ins), bi = F::bidx(ins);
-            fetch<R, P>(bk, bi, acc, w, cs, lane, b);
-            binary_p<R, P>(fid, a, b, JAC == 2 || mid < hi, o, d1, d2, z1, z2);
+        if (bin) {
+            binary_p<R, P, JAC != 1>(fid, a, b, JAC == 2 || mid < hi, o, d1, d2, z1, z2);
             if constexpr (JAC == 2) {
                 const int t = F::tape(ins), ta = F::tape_a(ins);
                 if (ta) CUSR_FOR_P lds_at<R, P>(w.tape, t, p, lane) = d1[p];
                 if (F::tape_b(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, t + ta, p, lane) = d2[p];
             }
         } else {
+            // d2 and z2 stay unset: the decoder never sets scale_b on a unary step
             unary_p<R, P, math_chunk<K, R, P, JAC>()>(fid, a, o, d1, z1);
-            CUSR_FOR_P { d2[p] = d1[p]; z2[p] = z1[p]; }   // unused: scale_b is never set
             if constexpr (JAC == 2) {
                 if (F::tape_a(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, F::tape(ins), p, lane) = d1[p];
             }
@@ -705,12 +723,16 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
             if (F::scale_a(ins)) scale_range<K, R, P>(T, lo, mid, d1, z1, sel);
             if (F::scale_b(ins)) scale_range<K, R, P>(T, mid, hi, d2, z2, sel);
         }
-        if (F::toslot(ins)) {
+        // the decoder spills a value only when its sibling subtree runs next,
+        // and that subtree's first instruction reads leaves only: the old
+        // accumulator is dead after a spill, so it takes o either way and the
+        // loop carries one accumulator (no second copy for the loop's exit)
+        const bool spill = F::toslot(ins);
+        if (spill) {
             const int di = F::didx(ins);
             CUSR_FOR_P lds_at<R, P>(w.slot, di, p, lane) = o[p];
-        } else {
-            CUSR_FOR_P acc[p] = o[p];
         }
+        CUSR_FOR_P acc[p] = o[p];
     }
 }
 
