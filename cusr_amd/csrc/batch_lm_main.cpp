@@ -2,7 +2,7 @@
 // (cusr/kernel/batch_lm_ad.cu:196-551):
 //
 //   batch_lm_ad <pop.bin> [out_dir] [--max-iter N] [--quiet] [--rev] [--mixed]
-//               [--profile]
+//               [--trust-region | --pivot-floor] [--profile]
 //
 // Reads pop.bin v1 and the v2 extension (float64 payloads, shared target;
 // include/pop_format.h).
@@ -12,6 +12,10 @@
 //   [batch-lm] 总耗时 <seconds> 秒 (<trees/s> trees/s, M_prob=<M>)
 // Exit status: 0 ok, 1 load or device failure, 2 beyond device bounds.
 // --rev / --mixed select reverse AD / mixed precision (extensions).
+// --trust-region is the reference's batch_lm_ad_tr build (-DTRUST_REGION,
+// cusr/kernel/Makefile:57-63): absolute damping A_jj + lambda from lambda 1e-4,
+// a pivot <= 0 replaced by lambda; --pivot-floor its -DPIVOT_FLOOR ablation
+// (relative damping, a pivot below 1e-9f raised to it).
 // --profile prints one machine-readable line whatever --quiet says, with the
 // fields of the reference's -DPROFILE build that a caller compares against
 // (batch_lm_ad.cu:553-575): PROFILE_JSON {"M","N","load_ms","setup_ms",
@@ -124,20 +128,24 @@ double seconds() {
 
 int main(int argc, char **argv) {
     if (argc < 2) {
-        fprintf(stderr, "usage: %s <pop.bin> [out_dir] [--max-iter N] [--quiet] [--rev] [--mixed]\n",
+        fprintf(stderr,
+                "usage: %s <pop.bin> [out_dir] [--max-iter N] [--quiet] [--rev] [--mixed] "
+                "[--trust-region | --pivot-floor] [--profile]\n",
                 argv[0]);
         return 1;
     }
     const double t0 = seconds();
     const char *pop_path = argv[1];
     std::string out_dir;
-    int max_iter = 50, quiet = 0, rev = 0, mixed = 0, profile = 0;
+    int max_iter = 50, quiet = 0, rev = 0, mixed = 0, profile = 0, damping = CO_DAMP_RELATIVE;
     for (int i = 2; i < argc; i++) {
         if (!strcmp(argv[i], "--max-iter") && i + 1 < argc) max_iter = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--quiet")) quiet = 1;
         else if (!strcmp(argv[i], "--rev")) rev = 1;
         else if (!strcmp(argv[i], "--mixed")) mixed = 1;
         else if (!strcmp(argv[i], "--profile")) profile = 1;
+        else if (!strcmp(argv[i], "--trust-region")) damping = CO_DAMP_TRUST_REGION;
+        else if (!strcmp(argv[i], "--pivot-floor")) damping = CO_DAMP_PIVOT_FLOOR;
         else if (argv[i][0] != '-') out_dir = argv[i];
     }
     if (out_dir.empty()) {
@@ -180,6 +188,8 @@ int main(int argc, char **argv) {
     opt.max_iter = max_iter;
     opt.ad_mode = rev ? CO_AD_REVERSE : CO_AD_FORWARD;
     opt.precision = mixed ? CO_PREC_MIXED : CO_PREC_FP64;
+    opt.damping = damping;
+    if (damping == CO_DAMP_TRUST_REGION) opt.lambda0 = CO_TRUST_REGION_LAMBDA0;
     // a float32 (v1) population fits as the reference's fp32 fit does: no
     // constant beyond the fp32 range; a float64 (v2) one in full fp64
     opt.f32_range = (pop_flags(&h) & POP_FLAG_F64) ? 0 : 1;

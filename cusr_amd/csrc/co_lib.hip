@@ -424,6 +424,8 @@ struct FitRun {
         if (opt.max_iter < 0) return CO_ERR_NULLARG;
         if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
             return CO_ERR_NULLARG;
+        if (opt.damping < CO_DAMP_RELATIVE || opt.damping > CO_DAMP_PIVOT_FLOOR)
+            return CO_ERR_NULLARG;
         if (opt.tail_iter < -1 || (opt.tail_partitions != 0 && opt.tail_partitions != 1 &&
                                    opt.tail_partitions != 2 && opt.tail_partitions != 4))
             return CO_ERR_NULLARG;
@@ -454,6 +456,7 @@ struct FitRun {
         fa.shared_y = ctx->shared_y ? 1 : 0;
         fa.f32_range = opt.f32_range ? 1 : 0;
         fa.lm_order = opt.lm_order;
+        fa.damp = opt.damping;
         fa.lambda0 = opt.lambda0;
         fa.xtol = opt.xtol;
         fa.psum = nullptr;
@@ -869,6 +872,8 @@ int fit_common(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int32_t
     if (opt.precision != CO_PREC_FP64 && opt.precision != CO_PREC_MIXED) return CO_ERR_NULLARG;
     if (opt.max_iter < 0) return CO_ERR_NULLARG;
     if (opt.lm_order != CO_ORDER_IMPROVE_FIRST && opt.lm_order != CO_ORDER_CONVERGE_FIRST)
+        return CO_ERR_NULLARG;
+    if (opt.damping < CO_DAMP_RELATIVE || opt.damping > CO_DAMP_PIVOT_FLOOR)
         return CO_ERR_NULLARG;
     const int nr = pipe_ranges(opt, h);
     if (nr > 1) {

@@ -1184,11 +1184,32 @@ __device__ __forceinline__ void data_pass_gen(const PassArgs &a, const WaveLds<R
 
 // ------------------------------------------------------------ the solve
 
-// Relative-damped Cholesky solve of (J^T J + lambda diag(J^T J)) delta = -J^T r
-// from pass sums s (cusr/kernel/batch_lm_ad.cu:149-191); false when a pivot is
-// <= 0. Every lane computes the same result.
+// The damping variants of the solve (cusr/kernel/batch_lm_ad.cu:149-172):
+// the damped diagonal, and the rule for a pivot s_j (false: the step fails).
+// CO_DAMP_RELATIVE: A_jj (1 + lambda), fail on s_j <= 0; CO_DAMP_TRUST_REGION:
+// A_jj + lambda, s_j <= 0 becomes lambda; CO_DAMP_PIVOT_FLOOR: A_jj (1 + lambda),
+// s_j below CO_PIVOT_FLOOR_EPS becomes it. A NaN pivot passes every rule (and
+// its NaN step is a non-finite trial).
+__device__ __forceinline__ double damp_diag(double a, double lambda, int damp) {
+    return damp == CO_DAMP_TRUST_REGION ? a + lambda : a * (1.0 + lambda);
+}
+__device__ __forceinline__ bool damp_pivot(double &sj, double lambda, int damp) {
+    if (damp == CO_DAMP_TRUST_REGION) {
+        if (sj <= 0.0) sj = lambda;
+    } else if (damp == CO_DAMP_PIVOT_FLOOR) {
+        if (sj < CO_PIVOT_FLOOR_EPS) sj = CO_PIVOT_FLOOR_EPS;
+    } else if (sj <= 0.0) {
+        return false;
+    }
+    return true;
+}
+
+// Damped Cholesky solve of (J^T J + damping) delta = -J^T r from pass sums s
+// (cusr/kernel/batch_lm_ad.cu:149-191) under damping variant damp; false when
+// the pivot rule fails the step. Every lane computes the same result.
 template <int K>
-__device__ __forceinline__ bool damped_solve(const double *s, double lambda, double (&delta)[K]) {
+__device__ __forceinline__ bool damped_solve(const double *s, double lambda, int damp,
+                                             double (&delta)[K]) {
     double L[K][K];
     double b[K];
 #pragma unroll
@@ -1199,7 +1220,7 @@ __device__ __forceinline__ bool damped_solve(const double *s, double lambda, dou
             // upper-triangle element (j, i): row j starts at j*K - j*(j-1)/2
             L[i][j] = s[1 + K + j * K - (j * (j - 1)) / 2 + (i - j)];
         }
-        L[i][i] = L[i][i] * (1.0 + lambda);
+        L[i][i] = damp_diag(L[i][i], lambda, damp);
     }
     bool ok = true;
 #pragma unroll
@@ -1207,7 +1228,7 @@ __device__ __forceinline__ bool damped_solve(const double *s, double lambda, dou
         double sj = L[j][j];
 #pragma unroll
         for (int k = 0; k < j; ++k) sj = fma(-L[j][k], L[j][k], sj);
-        if (sj <= 0.0) ok = false;
+        if (!damp_pivot(sj, lambda, damp)) ok = false;
         const double dj = ::sqrt(sj);
         L[j][j] = dj;
 #pragma unroll
@@ -1244,15 +1265,15 @@ __device__ __forceinline__ bool damped_solve(const double *s, double lambda, dou
 // exactly the arithmetic of damped_solve: column j's pivot is computed by
 // every lane, the entries below it by lane i; the substitutions run on every
 // lane with L read by broadcast. The solution is left in L[K*K .. K*K+K).
-__device__ __forceinline__ bool damped_solve_rt(const double *s, double lambda, int K, double *L,
-                                                int lane) {
+__device__ __forceinline__ bool damped_solve_rt(const double *s, double lambda, int damp, int K,
+                                                double *L, int lane) {
     double *b = L + K * K;   // right-hand side, then the solution (LDS, K doubles)
     // L[i][j] = upper-triangle element (j, i) of J^T J for j <= i; diagonal damped
     if (lane < K) {
         const int i = lane;
         for (int j = 0; j <= i; ++j) {
             double v = s[1 + K + j * K - (j * (j - 1)) / 2 + (i - j)];
-            if (j == i) v = v * (1.0 + lambda);
+            if (j == i) v = damp_diag(v, lambda, damp);
             L[i * K + j] = v;
         }
         b[i] = -s[1 + i];
@@ -1263,7 +1284,7 @@ __device__ __forceinline__ bool damped_solve_rt(const double *s, double lambda, 
     for (int j = 0; j < K; ++j) {
         double sj = L[j * K + j];
         for (int k = 0; k < j; ++k) sj = fma(-L[j * K + k], L[j * K + k], sj);
-        if (sj <= 0.0) ok = false;
+        if (!damp_pivot(sj, lambda, damp)) ok = false;
         const double dj = ::sqrt(sj);
         if (lane > j && lane < K) {
             const int i = lane;
@@ -1296,9 +1317,9 @@ __device__ __forceinline__ bool damped_solve_rt(const double *s, double lambda, 
 }
 
 template <int K>
-__device__ __forceinline__ bool damped_solve_lds(const double *s, double lambda, double (&delta)[K],
-                                                 double *L, int lane) {
-    if (!damped_solve_rt(s, lambda, K, L, lane)) return false;
+__device__ __forceinline__ bool damped_solve_lds(const double *s, double lambda, int damp,
+                                                 double (&delta)[K], double *L, int lane) {
+    if (!damped_solve_rt(s, lambda, damp, K, L, lane)) return false;
 #pragma unroll
     for (int i = 0; i < K; ++i) delta[i] = L[K * K + i];
     return true;
@@ -1318,6 +1339,7 @@ struct FitArgs {
     double *loss_final;     // [M] out
     int32_t *iters;         // [M] out
     int N, D, max_iter, guard, lm_order;
+    int damp;               // CO_DAMP_* of the solve
     int shared_y;           // 1: Y is one row [N] shared by every expression
     int f32_range;          // 1: constants and losses held to the fp32 range
     double lambda0, xtol;
@@ -1459,11 +1481,11 @@ __device__ __forceinline__ void fit_one(const FitArgs &fa, const ExprDesc &e, do
             double delta[GEN ? 1 : K];
             bool solved;
             if constexpr (GEN)
-                solved = damped_solve_rt(s_cur, lambda, Kr, lds_l, lane);
+                solved = damped_solve_rt(s_cur, lambda, fa.damp, Kr, lds_l, lane);
             else if constexpr (matrix_sums<K, AD>())
-                solved = damped_solve_lds<K>(s_cur, lambda, delta, lds_l, lane);
+                solved = damped_solve_lds<K>(s_cur, lambda, fa.damp, delta, lds_l, lane);
             else
-                solved = damped_solve<K>(s_cur, lambda, delta);
+                solved = damped_solve<K>(s_cur, lambda, fa.damp, delta);
             if (!solved) {
                 lambda = lambda * 10.0;
                 if (lambda > 1e12) st = ST_CHOL;

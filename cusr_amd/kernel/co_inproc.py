@@ -71,6 +71,10 @@ def co_partitions_for(N: int, ad_mode: int = 0) -> int:
 CO_AD_FORWARD, CO_AD_REVERSE = 0, 1
 CO_PREC_FP64, CO_PREC_MIXED = 0, 1
 CO_ORDER_IMPROVE_FIRST, CO_ORDER_CONVERGE_FIRST = 0, 1
+# damped-solve variants (cusr_co.h CoOptions.damping; cusr/kernel/batch_lm_ad.cu:149-172)
+CO_DAMP_RELATIVE, CO_DAMP_TRUST_REGION, CO_DAMP_PIVOT_FLOOR = 0, 1, 2
+CO_PIVOT_FLOOR_EPS = float(np.float32(1e-9))          # the reference's 1e-9f
+CO_TRUST_REGION_LAMBDA0 = float(np.float32(1e-4))     # its trust-region start
 POP_FLAG_F64, POP_FLAG_SHARED_Y = 1, 2
 # external statuses (include/pop_format.h, cusr/kernel/lm_core.cuh:46-56)
 STATUS_CONVERGED, STATUS_MAXITER, STATUS_FAIL_NAN, STATUS_K0_SKIP, STATUS_FAIL_CHOLESKY = 0, 1, 2, 3, 4
@@ -119,7 +123,7 @@ class CoOptions(ctypes.Structure):
                 ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
                 ("lm_order", ctypes.c_int32), ("tail_iter", ctypes.c_int32),
                 ("tail_partitions", ctypes.c_int32), ("f32_range", ctypes.c_int32),
-                ("reserved", ctypes.c_int32 * 2)]
+                ("damping", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 assert ctypes.sizeof(PopHeader) == 64
@@ -384,13 +388,16 @@ class InProcessCO:
     def optimize_ex(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                     precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                     fp64_guard: bool = True, partitions: int = 0, lm_order: int | None = None,
+                    damping: int = CO_DAMP_RELATIVE,
                     tail_iter: int = 0, tail_partitions: int = 0, f32_range: bool = False,
                     c_init=None, xs=None, ym=None) -> dict:
         """fp64 fit; c_init/xs/ym override the pop's (fp32) arrays when given.
         partitions: point partitions per expression (0: by N). lm_order: None
         keeps the library's default (CO_ORDER_IMPROVE_FIRST for the ad
-        library, CO_ORDER_CONVERGE_FIRST for fd). f32_range: trial constants
-        held in fp32 and losses in its range, as co_optimize fits."""
+        library, CO_ORDER_CONVERGE_FIRST for fd). damping: the solve's variant
+        (CO_DAMP_RELATIVE, CO_DAMP_TRUST_REGION with lambda0 typically
+        CO_TRUST_REGION_LAMBDA0, CO_DAMP_PIVOT_FLOOR). f32_range: trial
+        constants held in fp32 and losses in its range, as co_optimize fits."""
         self._check()
         M, C = int(pop["M"]), int(pop["total_c"])
         h = _header(pop)
@@ -400,6 +407,7 @@ class InProcessCO:
                             tail_iter=int(tail_iter), tail_partitions=int(tail_partitions),
                             f32_range=1 if f32_range else 0)
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
+        o.damping = int(damping)
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
         ci, pci = _arr(pop["ci"], np.int32)
@@ -514,6 +522,7 @@ class InProcessCO:
     def optimize_data(self, pop: dict, max_iter: int = 50, *, ad_mode: int = CO_AD_FORWARD,
                       precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                       fp64_guard: bool = True, partitions: int = 0, lm_order: int | None = None,
+                      damping: int = CO_DAMP_RELATIVE,
                     tail_iter: int = 0, tail_partitions: int = 0, f32_range: bool = False,
                       c_init=None) -> dict:
         """optimize_ex against the uploaded data set: pop's xs and ym are not
@@ -527,6 +536,7 @@ class InProcessCO:
                             tail_iter=int(tail_iter), tail_partitions=int(tail_partitions),
                             f32_range=1 if f32_range else 0)
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
+        o.damping = int(damping)
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
         ci, pci = _arr(pop["ci"], np.int32)
@@ -553,6 +563,7 @@ class InProcessCO:
                              ad_mode: int = CO_AD_FORWARD, precision: int = CO_PREC_FP64,
                              lambda0: float = 1e-3, xtol: float = 1e-6, fp64_guard: bool = True,
                              partitions: int = 0, lm_order: int | None = None,
+                             damping: int = CO_DAMP_RELATIVE,
                              f32_range: bool = False) -> dict:
         """optimize_data with the constants and results on the device
         (co_optimize_data_device): c_init is a float64 CUDA tensor of
@@ -574,6 +585,7 @@ class InProcessCO:
                             fp64_guard=1 if fp64_guard else 0, partitions=int(partitions),
                             f32_range=1 if f32_range else 0)
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
+        o.damping = int(damping)
         nt, pnt = _arr(pop["nt"], np.int32)
         nv, pnv = _arr(pop["nv"], np.float32)
         ci, pci = _arr(pop["ci"], np.int32)
@@ -599,7 +611,8 @@ class InProcessCO:
                      precision: int = CO_PREC_FP64, lambda0: float = 1e-3, xtol: float = 1e-6,
                      fp64_guard: bool = True, outputs: bool = True, partitions: int = 0,
                      tail_iter: int = 0, tail_partitions: int = 0, f32_range: bool = False,
-                     lm_order: int | None = None, static_scratch: bool = False):
+                     lm_order: int | None = None,
+                     damping: int = CO_DAMP_RELATIVE, static_scratch: bool = False):
         """Fit the uploaded population again; outputs=False leaves results on the
         device. static_scratch: co_fit_resident_static, the same fit with its
         scratch in the library's fixed device array (no device allocation)."""
@@ -613,6 +626,7 @@ class InProcessCO:
                             tail_iter=int(tail_iter), tail_partitions=int(tail_partitions),
                             f32_range=1 if f32_range else 0)
         o.lm_order = self.default_order if lm_order is None else int(lm_order)
+        o.damping = int(damping)
         if not outputs:
             rc = fn(self._handle, ctypes.byref(o), None, None, None, None, None)
             if rc != CO_OK:

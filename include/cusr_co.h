@@ -124,11 +124,30 @@ typedef struct CoOptions {
                            constants kept (cusr/kernel/batch_lm_ad.cu:437-443).
                            co_optimize and the CLI on float32 files set it;
                            default 0 */
-    int32_t reserved[2];
+    int32_t damping;    /* the damped solve's variant (cusr/kernel/batch_lm_ad.cu:
+                           149-172, chosen there by -DTRUST_REGION / -DPIVOT_FLOOR):
+                           CO_DAMP_RELATIVE (default): A_jj (1 + lambda), a
+                           pivot <= 0 fails the step;
+                           CO_DAMP_TRUST_REGION (the reference's batch_lm_ad_tr,
+                           cusr/kernel/Makefile:57-63): A_jj + lambda, a pivot
+                           <= 0 is replaced by lambda; the reference starts
+                           that variant at lambda 1e-4 (batch_lm_ad.cu:301-306),
+                           which the caller sets in lambda0;
+                           CO_DAMP_PIVOT_FLOOR: A_jj (1 + lambda), a pivot
+                           below CO_PIVOT_FLOOR_EPS is raised to it */
+    int32_t reserved;
 } CoOptions;
 
 #define CO_ORDER_IMPROVE_FIRST 0
 #define CO_ORDER_CONVERGE_FIRST 1
+
+#define CO_DAMP_RELATIVE 0
+#define CO_DAMP_TRUST_REGION 1
+#define CO_DAMP_PIVOT_FLOOR 2
+/* the reference's PIVOT_FLOOR_EPS, the fp32 constant 1e-9f
+ * (cusr/kernel/batch_lm_ad.cu:80-82), held exactly in fp64 */
+#define CO_PIVOT_FLOOR_EPS ((double)1e-9f)
+#define CO_TRUST_REGION_LAMBDA0 ((double)1e-4f)
 
 /* Point partitions of an expression with N points when CoOptions.partitions
  * is 0: 64-point granule g belongs to partition g mod G, each partition is

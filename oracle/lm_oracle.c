@@ -578,22 +578,33 @@ static int orc_partitions(const CoOptions *o, int N) {
 
 /* ------------------------------------------------------------- the solve */
 
-/* Relative-damped Cholesky solve (batch_lm_ad.cu:149-191): A = JtJ with
- * A_jj *= (1 + lambda), b = -Jtr; a pivot s <= 0 fails the step.
+/* Damped Cholesky solve (batch_lm_ad.cu:149-191): A = JtJ, b = -Jtr, under
+ * the damping variant of batch_lm_ad.cu:152-172 (its -DTRUST_REGION and
+ * -DPIVOT_FLOOR builds): CO_DAMP_RELATIVE A_jj *= (1 + lambda) and a pivot
+ * s <= 0 fails the step; CO_DAMP_TRUST_REGION A_jj += lambda and a pivot
+ * s <= 0 is replaced by lambda; CO_DAMP_PIVOT_FLOOR A_jj *= (1 + lambda) and a
+ * pivot below CO_PIVOT_FLOOR_EPS is raised to it.
  * Returns 0 and delta, or -1. */
-static int orc_solve(int K, const double *jtj, const double *jtr, double lambda,
+static int orc_solve(int K, const double *jtj, const double *jtr, double lambda, int damp,
                      double *delta) {
     double L[ORC_MAXK * ORC_MAXK];
     double b[ORC_MAXK];
     for (int i = 0; i < K; i++) {
         b[i] = -jtr[i];
         for (int j = 0; j <= i; j++) L[i * K + j] = jtj[j * K + i];
-        L[i * K + i] = L[i * K + i] * (1.0 + lambda);
+        if (damp == CO_DAMP_TRUST_REGION) L[i * K + i] = L[i * K + i] + lambda;
+        else L[i * K + i] = L[i * K + i] * (1.0 + lambda);
     }
     for (int j = 0; j < K; j++) {
         double s = L[j * K + j];
         for (int k = 0; k < j; k++) s = fma(-L[j * K + k], L[j * K + k], s);
-        if (s <= 0.0) return -1;
+        if (damp == CO_DAMP_TRUST_REGION) {
+            if (s <= 0.0) s = lambda;
+        } else if (damp == CO_DAMP_PIVOT_FLOOR) {
+            if (s < CO_PIVOT_FLOOR_EPS) s = CO_PIVOT_FLOOR_EPS;
+        } else if (s <= 0.0) {
+            return -1;
+        }
         double dj = sqrt(s);
         L[j * K + j] = dj;
         for (int i = j + 1; i < K; i++) {
@@ -662,7 +673,7 @@ static void orc_fit_one(const CoOptions *o, const Tree *t, int N, int D, const d
     while (st == 0 && it < o->max_iter) {
         it++;
         G = (T1 && it > T1) ? G2 : G1;
-        if (orc_solve(K, cur->jtj, cur->jtr, lambda, delta) != 0) {
+        if (orc_solve(K, cur->jtj, cur->jtr, lambda, o->damping, delta) != 0) {
             lambda = lambda * 10.0;
             if (lambda > 1e12) st = 4;
             continue;
@@ -843,9 +854,9 @@ int orc_jacobian(const PopHeader *h, const int32_t *nt, const float *nv, const i
 
 /* The damped solve alone, for tests against a textbook Cholesky. */
 int orc_solve_api(int K, const double *jtj_upper, const double *jtr, double lambda,
-                  double *delta) {
+                  int damping, double *delta) {
     if (K < 1 || K > ORC_MAXK) return CO_ERR_BOUNDS;
-    return orc_solve(K, jtj_upper, jtr, lambda, delta);
+    return orc_solve(K, jtj_upper, jtr, lambda, damping, delta);
 }
 
 /* The canonical pass alone: loss, Jtr and the JtJ upper triangle of one

@@ -20,6 +20,10 @@ _lib = None
 
 CO_AD_FORWARD, CO_AD_REVERSE = 0, 1
 CO_PREC_FP64, CO_PREC_MIXED = 0, 1
+# damped-solve variants (include/cusr_co.h CoOptions.damping)
+CO_DAMP_RELATIVE, CO_DAMP_TRUST_REGION, CO_DAMP_PIVOT_FLOOR = 0, 1, 2
+CO_PIVOT_FLOOR_EPS = float(np.float32(1e-9))
+CO_TRUST_REGION_LAMBDA0 = float(np.float32(1e-4))
 
 
 class PopHeader(ctypes.Structure):
@@ -35,7 +39,7 @@ class CoOptions(ctypes.Structure):
                 ("fp64_guard", ctypes.c_int32), ("partitions", ctypes.c_int32),
                 ("lm_order", ctypes.c_int32), ("tail_iter", ctypes.c_int32),
                 ("tail_partitions", ctypes.c_int32), ("f32_range", ctypes.c_int32),
-                ("reserved", ctypes.c_int32 * 2)]
+                ("damping", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 def build() -> None:
@@ -78,7 +82,7 @@ def _prog(pop):
 
 def options(ad_mode=CO_AD_FORWARD, precision=CO_PREC_FP64, max_iter=50,
             lambda0=1e-3, xtol=1e-6, fp64_guard=1, partitions=0, lm_order=0,
-            tail_iter=0, tail_partitions=0, f32_range=0) -> CoOptions:
+            tail_iter=0, tail_partitions=0, f32_range=0, damping=0) -> CoOptions:
     o = CoOptions()
     o.struct_size = ctypes.sizeof(CoOptions)
     o.ad_mode, o.precision, o.max_iter = ad_mode, precision, max_iter
@@ -87,6 +91,7 @@ def options(ad_mode=CO_AD_FORWARD, precision=CO_PREC_FP64, max_iter=50,
     o.lm_order = lm_order
     o.tail_iter, o.tail_partitions = tail_iter, tail_partitions
     o.f32_range = f32_range
+    o.damping = damping
     return o
 
 
@@ -151,14 +156,15 @@ def jacobian(pop, c=None, xs=None, ad_mode=CO_AD_FORWARD):
     return J[:, :, :KM]
 
 
-def solve(jtj, jtr, lam):
-    """Damped Cholesky step of the oracle; None when a pivot fails."""
+def solve(jtj, jtr, lam, damping=0):
+    """Damped Cholesky step of the oracle under damping variant `damping`
+    (CoOptions.damping); None when the pivot rule fails the step."""
     K = len(jtr)
     a, pa = _p(np.triu(jtj), np.float64)
     b, pb = _p(jtr, np.float64)
     d = np.zeros(K)
     rc = lib().orc_solve_api(ctypes.c_int(K), pa, pb, ctypes.c_double(lam),
-                             d.ctypes.data_as(ctypes.c_void_p))
+                             ctypes.c_int(damping), d.ctypes.data_as(ctypes.c_void_p))
     return None if rc != 0 else d
 
 

@@ -81,12 +81,20 @@ MUTANTS = [
      "accept = tri->loss <= cur->loss;", "accept = tri->loss < cur->loss;", 0,
      "an equal loss rejected"),
     ("pivot-zero-accepted", "oracle/lm_oracle.c",
-     "if (s <= 0.0) return -1;", "if (s < 0.0) return -1;", 0,
+     "} else if (s <= 0.0) {\n            return -1;",
+     "} else if (s < 0.0) {\n            return -1;", 0,
      "a zero pivot does not fail the solve"),
     ("damping-absolute", "oracle/lm_oracle.c",
-     "L[i * K + i] = L[i * K + i] * (1.0 + lambda);",
-     "L[i * K + i] = L[i * K + i] + lambda;", 0,
+     "else L[i * K + i] = L[i * K + i] * (1.0 + lambda);",
+     "else L[i * K + i] = L[i * K + i] + lambda;", 0,
      "absolute instead of relative damping"),
+    ("trust-region-diagonal", "oracle/lm_oracle.c",
+     "if (damp == CO_DAMP_TRUST_REGION) L[i * K + i] = L[i * K + i] + lambda;",
+     "if (damp == CO_DAMP_TRUST_REGION) L[i * K + i] = L[i * K + i] * (1.0 + lambda);", 0,
+     "relative instead of absolute damping in the trust-region variant"),
+    ("trust-region-rescue", "oracle/lm_oracle.c",
+     "if (s <= 0.0) s = lambda;", "if (s <= 0.0) s = 2.0 * lambda;", 0,
+     "a trust-region pivot <= 0 replaced by 2 lambda"),
     ("guard-ignores-worse", "oracle/lm_oracle.c",
      "if (!isfinite(lf) || (isfinite(li) && lf > li)) {",
      "if (!isfinite(lf)) {", 0,

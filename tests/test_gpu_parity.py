@@ -246,3 +246,49 @@ def test_tail_high_k_matrix_sums(co):
     pop, _ = synth("C3", 96, 700)
     g, o = _fit_both(co, pop, 15, tail_iter=4, tail_partitions=4)
     assert_parity(g, o, 1e-9, "tail high K", exact=True)
+
+
+@pytest.mark.parametrize("damping", [1, 2])
+@pytest.mark.parametrize("case", ["fast", "reverse", "matrix", "split", "general", "mixed"])
+def test_damping_variants_match_oracle(co, damping, case):
+    """CoOptions.damping -- trust region (absolute damping, a pivot <= 0
+    replaced by lambda) and the pivot floor (cusr/kernel/batch_lm_ad.cu:149-172)
+    -- in every solve of the device: the register solve of the fast kernels
+    (forward and reverse AD), the LDS solve of the matrix-sum bins, the split
+    path's step kernel, the general kernel and a mixed-precision fit. Final
+    constants, losses and statuses equal the oracle's (fp64) or agree to the
+    mixed tolerance, and the variant changes the fit (against the oracle's
+    relative damping), so its own rule is what is compared."""
+    from tests.general_pops import general_pop
+    lam0 = lm_oracle.CO_TRUST_REGION_LAMBDA0 if damping == 1 else 1e-3
+    kw = dict(damping=damping, lambda0=lam0)
+    prec = 1 if case == "mixed" else 0
+    if case == "fast":
+        pop, _ = synth("C2", 256, 512)
+    elif case == "reverse":
+        pop, _ = synth("C2", 128, 512)
+        kw["ad_mode"] = 1
+    elif case == "matrix":
+        pop, _ = synth("C3", 96, 700)
+        assert pop["K_max"] >= 13
+    elif case == "split":
+        pop, _ = synth("C3", 64, 1024)
+        kw["partitions"] = 8
+    elif case == "general":
+        pop, _ = general_pop("highk", 32, 700)
+    else:
+        pop, _ = synth("C5", 128, 512)
+    g, o = _fit_both(co, pop, 30, precision=prec, **kw)
+    assert_parity(g, o, 1e-9 if prec == 0 else 1e-4, f"damping {damping} {case}",
+                  exact=prec == 0)
+    rel = lm_oracle.fit(pop, max_iter=30, precision=prec,
+                        **{k: v for k, v in kw.items() if k not in ("damping", "lambda0")})
+    assert not np.array_equal(o["c_final"], rel["c_final"])
+
+
+def test_damping_out_of_range_refused(co):
+    from cusr_amd.kernel import co_inproc as ci
+    pop, _ = synth("C1", 8, 64)
+    with pytest.raises(ci.COError) as e:
+        co.optimize_ex(pop, 5, damping=3)
+    assert e.value.code == ci.CO_ERR_NULLARG

@@ -221,6 +221,71 @@ def test_damped_solve_rejects_non_positive_pivot():
     assert lm_oracle.solve(jtj, np.array([1.0, 1.0]), 0.0) is None
 
 
+@pytest.mark.parametrize("K", [1, 3, 7])
+def test_trust_region_solve_matches_textbook(K):
+    """Absolute damping (batch_lm_ad.cu:153-154): (JtJ + lambda I) delta = -Jtr,
+    against LU; relative and absolute damping differ unless diag(JtJ) = 1."""
+    rng = np.random.default_rng(100 + K)
+    J = rng.standard_normal((3 * K + 4, K)) * rng.uniform(0.1, 10.0, K)
+    jtj, jtr = J.T @ J, rng.standard_normal(K)
+    for lam in (1e-4, 1e-1, 10.0):
+        want = np.linalg.solve(jtj + lam * np.eye(K), -jtr)
+        got = lm_oracle.solve(jtj, jtr, lam, damping=lm_oracle.CO_DAMP_TRUST_REGION)
+        assert np.allclose(got, want, rtol=1e-9, atol=1e-12)
+        rel = lm_oracle.solve(jtj, jtr, lam, damping=lm_oracle.CO_DAMP_RELATIVE)
+        assert not np.allclose(got, rel, rtol=1e-6)
+
+
+def _schur_pivot(A, j):
+    """The j-th Cholesky pivot of A as a Schur complement (no elimination)."""
+    if j == 0:
+        return A[0, 0]
+    return A[j, j] - A[j, :j] @ np.linalg.solve(A[:j, :j], A[:j, j])
+
+
+@pytest.mark.parametrize("damping", ["trust", "floor"])
+def test_pivot_rescue_is_a_diagonal_shift(damping):
+    """A rescued pivot s_j (batch_lm_ad.cu:162-169) is the factor of A with
+    A_jj raised by (replacement - s_j): the step solves that shifted system.
+    Trust region replaces s_j <= 0 by lambda, the pivot floor raises s_j below
+    1e-9f to 1e-9f; the indefinite pair needs a rescue under both rules."""
+    tr = damping == "trust"
+    mode = lm_oracle.CO_DAMP_TRUST_REGION if tr else lm_oracle.CO_DAMP_PIVOT_FLOOR
+    eps = float(np.float32(1e-9))
+    assert lm_oracle.CO_PIVOT_FLOOR_EPS == eps
+    cases = [(np.array([[2.0, 0.0, 1.0], [0.0, 0.0, 0.0], [1.0, 0.0, 3.0]]),
+              np.array([1.0, -2.0, 0.5])),                      # dead constant 1
+             (np.array([[1.0, 2.0], [2.0, 4.0]]), np.array([1.0, 1.0])),   # collinear
+             (np.array([[1.0, 2.0], [2.0, 1.0]]), np.array([0.3, -1.0]))]  # indefinite
+    lam, total = 0.25, 0
+    for jtj, jtr in cases:
+        K = len(jtr)
+        A = jtj.copy()
+        if tr:
+            A[np.diag_indices(K)] += lam
+        else:
+            A[np.diag_indices(K)] *= 1.0 + lam
+        shifted, rescued, nonpos = A.copy(), 0, False
+        for j in range(K):
+            s = _schur_pivot(shifted, j)
+            if (tr and s <= 0.0) or (not tr and s < eps):
+                shifted[j, j] += (lam if tr else eps) - s
+                rescued += 1
+                nonpos |= s <= 0.0
+        got = lm_oracle.solve(jtj, jtr, lam, damping=mode)
+        want = np.linalg.solve(shifted, -jtr)
+        assert got is not None
+        # a floored pivot leaves the system ill-conditioned: LU and Cholesky
+        # then agree to about cond(A) ulps
+        tol = max(1e-8, 1e-14 * np.linalg.cond(shifted))
+        assert np.allclose(got, want, rtol=tol, atol=1e-12), (jtj, got, want)
+        total += rescued
+        # where the floor rescues a pivot <= 0, the relative rule fails the step
+        if not tr and nonpos:
+            assert lm_oracle.solve(jtj, jtr, lam) is None
+    assert total >= 1
+
+
 def test_pass_sums_match_textbook():
     pop, _ = synth("C2", 8, 300)
     x = pop["xs"].astype(np.float64)
@@ -697,6 +762,42 @@ def test_lm_schedule_closed_form_on_a_linear_model():
     r = lm_oracle.fit(pop, max_iter=10)
     assert r["status"][0] == 0 and r["iters"][0] == 3               # CONVERGED
     assert r["c_final"][0] - 2.0 == pytest.approx(e[3], rel=1e-3)
+
+
+def test_trust_region_schedule_closed_form_on_a_linear_model():
+    """The linear model above under trust-region damping (batch_lm_ad.cu:
+    153-154, lambda from 1e-4, :301-306): the step is -e S / (S + lambda) with
+    S = sum x^2 = 4900 / 64, so e' = e lambda / (S + lambda), lambda_k = 1e-4 10^-k."""
+    pop = _linear_pop(0.0)
+    S = 4900.0 / 64.0
+    e = [-2.0]
+    for k in range(2):
+        lam = lm_oracle.CO_TRUST_REGION_LAMBDA0 * 10.0 ** -k
+        e.append(e[-1] * lam / (S + lam))
+    for it in (1, 2):
+        r = lm_oracle.fit(pop, max_iter=it, damping=lm_oracle.CO_DAMP_TRUST_REGION,
+                          lambda0=lm_oracle.CO_TRUST_REGION_LAMBDA0)
+        assert r["status"][0] == 1 and r["iters"][0] == it
+        assert r["c_final"][0] - 2.0 == pytest.approx(e[it], rel=1e-9)
+
+
+def test_dead_constant_fails_relative_and_not_trust_region():
+    """F = c0 x0 + c1 (x0 - x0): c1's Jacobian column is exactly 0. Relative
+    damping leaves its pivot 0 at every lambda, so no step is taken and lambda
+    runs past 1e12 (FAIL_CHOLESKY, status 4); trust region damps it to lambda
+    (its step is 0, Jtr_1 = 0) and c0 converges as in the linear model; the
+    pivot floor raises it to 1e-9f, with the same zero step."""
+    x = (np.arange(1, 25, dtype=np.float64) / 8.0)[:, None]
+    _ADD, _SUB = 1, 2
+    pop = _pop1([3, 3, 1, 0, 3, 1, 3, 0, 0], [_ADD, _OP_MUL, 0, 0, _OP_MUL, 0, _SUB, 0, 0],
+                [-1, -1, 0, -1, -1, 1, -1, -1, -1], [0.0, 0.5], x, 2.0 * x[:, 0])
+    rel = lm_oracle.fit(pop, max_iter=50)
+    assert rel["status"][0] == 4 and np.array_equal(rel["c_final"][:2], [0.0, 0.5])
+    for mode, lam0 in ((lm_oracle.CO_DAMP_TRUST_REGION, lm_oracle.CO_TRUST_REGION_LAMBDA0),
+                       (lm_oracle.CO_DAMP_PIVOT_FLOOR, 1e-3)):
+        r = lm_oracle.fit(pop, max_iter=50, damping=mode, lambda0=lam0)
+        assert r["status"][0] == 0, mode
+        assert r["c_final"][0] == pytest.approx(2.0, abs=1e-9) and r["c_final"][1] == 0.5
 
 
 def test_lm_accepts_an_equal_loss():
