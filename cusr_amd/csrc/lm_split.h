@@ -227,14 +227,18 @@ __global__ void __launch_bounds__(kLanes) lm_step_kernel(FitArgs fa, int mixed) 
             bool solved;
             if constexpr (KS > 0) {
                 double delta[KS];
-                solved = damped_solve<KS>(s_cur, lambda, fa.damp, delta);
+                solved = fa.damp == CO_DAMP_RELATIVE
+                             ? damped_solve<KS, true>(s_cur, lambda, 0, delta)
+                             : damped_solve<KS, false>(s_cur, lambda, fa.damp, delta);
                 if (solved && lane == 0) {
 #pragma unroll
                     for (int j = 0; j < KS; ++j) L[KS * KS + j] = delta[j];
                 }
                 wave_sync_lds();
             } else {
-                solved = damped_solve_rt(s_cur, lambda, fa.damp, K, L, lane);
+                solved = fa.damp == CO_DAMP_RELATIVE
+                             ? damped_solve_rt<true>(s_cur, lambda, 0, K, L, lane)
+                             : damped_solve_rt<false>(s_cur, lambda, fa.damp, K, L, lane);
             }
             if (!solved) {
                 lambda = lambda * 10.0;

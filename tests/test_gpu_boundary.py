@@ -136,6 +136,30 @@ def test_cli_blobs_and_completion_line(tmp_path, exe, order):
     assert bad.returncode == 1
 
 
+@pytest.mark.parametrize("flag,damping", [("--trust-region", 1), ("--pivot-floor", 2)])
+def test_cli_damping_flags(tmp_path, flag, damping):
+    """--trust-region is the reference's batch_lm_ad_tr build (absolute damping
+    from lambda 1e-4f, cusr/kernel/Makefile:57-63, batch_lm_ad.cu:152-172,
+    301-306); --pivot-floor its -DPIVOT_FLOOR build: the blobs equal the
+    oracle's fit under the same variant."""
+    pop, _ = synth("C2", 64, 128)
+    path = tmp_path / "pop.bin"
+    popio.save_pop_bin(pop, path)
+    _say(f"cli batch_lm_ad {flag}")
+    r = subprocess.run([str(KDIR / "batch_lm_ad"), str(path), str(tmp_path), "--max-iter", "15",
+                        flag], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    status = np.fromfile(tmp_path / "status.bin", np.int32)
+    c_final = np.fromfile(tmp_path / "c_final.bin", np.float32)
+    lam0 = lm_oracle.CO_TRUST_REGION_LAMBDA0 if damping == 1 else 1e-3
+    o = ci.narrow_fp32(pop, lm_oracle.fit(pop, max_iter=15, f32_range=1, damping=damping,
+                                          lambda0=lam0))
+    _say(f"cli {flag}: statuses equal {np.mean(status == o['status']):.4f}; constants equal "
+         f"{np.mean(c_final == o['c_final']):.4f}")
+    assert np.array_equal(status, o["status"])
+    assert np.array_equal(c_final, o["c_final"])
+
+
 def _shared_target(M=96, N=256, seed=9):
     pop, _ = synth("C1", M, N)
     y = np.random.default_rng(seed).normal(size=N).astype(np.float32)
