@@ -489,10 +489,17 @@ struct FitRun {
     // The kernel launched first on a stream takes the machine first and so
     // ends first, so each stream's next bin is the next largest; this beats
     // balancing estimated costs over the streams (C2 12.15 -> 11.66 ms, C4
-    // 173 -> 170 ms, C3 139.7 -> 137.8 ms on an MI355X).
+    // 173 -> 170 ms, C3 139.7 -> 137.8 ms on an MI355X). A general bin of at
+    // least a sixteenth of the range's expressions is the exception: one
+    // wavefront per expression at one point per lane, it outlasts any fast bin
+    // many times over, so it gets stream 0 to itself and the fast bins are
+    // dealt over the other three (a GP-generation population, a fifth of it
+    // general: the fast bins dealt behind it on stream 0 had waited for it,
+    // 74.6 ms per fit against the general bin's 45 ms).
     int plan_range(int p0, int p1, LaunchPlan *lp, int *nl_out, int *kmax_out) const {
         const Plan &plan = ctx->plan;
         int nl = 0, kmax = 0, pos = p0;
+        bool gen_alone = false;
         for (int i = 0; i < CO_BINS; ++i) {
             const int bin = i == 0 ? CO_GENERAL_BIN : CO_FAST_MAX_K - (i - 1);
             const bool gen = bin == CO_GENERAL_BIN;
@@ -511,7 +518,8 @@ struct FitRun {
             if (b.cnt == 0) continue;
             if (!rev) b.tape = 0;
             if (b.kmax > kmax) kmax = b.kmax;
-            b.stream = nl % kStreams;
+            if (gen) gen_alone = (long)b.cnt * 16 >= (long)(p1 - p0) && b.cnt < p1 - p0;
+            b.stream = !gen_alone ? nl % kStreams : (gen ? 0 : 1 + (nl - 1) % (kStreams - 1));
             // per-wavefront areas, then the partition sums; fewer wavefronts per
             // workgroup (each summing several partitions) when LDS is short. The
             // split path's pass workgroups are one wavefront with no partition
