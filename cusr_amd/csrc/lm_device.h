@@ -219,11 +219,10 @@ template <> struct Fn<float> {
 #define CUSR_MATH_V(fn, ...) \
     _Pragma("unroll") for (int c0 = 0; c0 < P; c0 += MC) F::template fn<MC>(__VA_ARGS__)
 template <typename R, int P, int MC = P>
-__device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) {
+__device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, uint64_t *zm) {
     typedef Fn<R> F;
     static_assert(P % MC == 0, "math chunks must divide the points per lane");
     const R one = R(1), zero = R(0), two = R(2);
-    CUSR_FOR_P z[p] = false;
     switch (f) {
     case OP_SIN: CUSR_MATH_V(sincos_v, a + c0, r + c0, d + c0); break;
     case OP_COS: {
@@ -280,7 +279,7 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
             const bool flat = a[p] > R(20);
             r[p] = flat ? F::cexp_cap : e[p];
             d[p] = flat ? zero : e[p];
-            z[p] = flat;
+            zm[p] = __builtin_amdgcn_ballot_w64(flat);
         }
         break;
     }
@@ -306,15 +305,19 @@ __device__ __forceinline__ void unary_p(int f, const R *a, R *r, R *d, bool *z) 
 // want_d2 false skips log(l) of POW when no constant is on the right.
 // UNIT false leaves the partials that are exactly 1 (ADD's two, SUB's left)
 // unset: the forward sweep never reads them, and a register left unset on
-// that branch is not copied into at every ADD step. (The flat flags z1, z2
-// keep their defaults: a lane mask left unset on a branch is merged with the
-// execution mask at the join, which costs more than clearing it.)
+// that branch is not copied into at every ADD step.
+// The flat-branch lanes (the points whose partial is a flat branch: zero, not
+// d * tangent) leave as wave-uniform masks m1, m2 (bit = lane), set only by
+// the operators the decoder marks sel (MAX, MIN, the comparisons, PDIV; CEXP
+// in unary_p) and read only on their steps. As uniform scalars they need no
+// default: per-lane flags left unset on the other operators' branches were
+// merged with the execution mask at the join, and clearing them instead cost
+// 2P scalar moves on every step.
 template <typename R, int P, bool UNIT = true>
 __device__ __forceinline__ void binary_p(int f, const R *l, const R *rv, bool want_d2, R *o,
-                                         R *d1, R *d2, bool *z1, bool *z2) {
+                                         R *d1, R *d2, uint64_t *m1, uint64_t *m2) {
     typedef Fn<R> F;
     const R one = R(1), zero = R(0);
-    CUSR_FOR_P { z1[p] = false; z2[p] = false; }
     switch (f) {
     case OP_ADD:
         CUSR_FOR_P {
@@ -343,8 +346,7 @@ __device__ __forceinline__ void binary_p(int f, const R *l, const R *rv, bool wa
             o[p] = prot ? one : q;
             d1[p] = prot ? zero : inv;
             d2[p] = prot ? zero : -(q * inv);
-            z1[p] = prot;
-            z2[p] = prot;
+            m1[p] = m2[p] = __builtin_amdgcn_ballot_w64(prot);
         }
         break;
     case OP_POW:
@@ -369,8 +371,8 @@ __device__ __forceinline__ void binary_p(int f, const R *l, const R *rv, bool wa
             o[p] = F::max_(l[p], rv[p]);
             d1[p] = ge ? one : zero;
             d2[p] = ge ? zero : one;
-            z1[p] = !ge;
-            z2[p] = ge;
+            m1[p] = __builtin_amdgcn_ballot_w64(!ge);
+            m2[p] = __builtin_amdgcn_ballot_w64(ge);
         }
         break;
     case OP_MIN:
@@ -379,21 +381,41 @@ __device__ __forceinline__ void binary_p(int f, const R *l, const R *rv, bool wa
             o[p] = F::min_(l[p], rv[p]);
             d1[p] = le ? one : zero;
             d2[p] = le ? zero : one;
-            z1[p] = !le;
-            z2[p] = le;
+            m1[p] = __builtin_amdgcn_ballot_w64(!le);
+            m2[p] = __builtin_amdgcn_ballot_w64(le);
         }
         break;
     case OP_LT:
-        CUSR_FOR_P { o[p] = (l[p] < rv[p]) ? one : zero; d1[p] = zero; d2[p] = zero; z1[p] = true; z2[p] = true; }
+        CUSR_FOR_P {
+            o[p] = (l[p] < rv[p]) ? one : zero;
+            d1[p] = zero;
+            d2[p] = zero;
+            m1[p] = m2[p] = __builtin_amdgcn_ballot_w64(true);
+        }
         break;
     case OP_GT:
-        CUSR_FOR_P { o[p] = (l[p] > rv[p]) ? one : zero; d1[p] = zero; d2[p] = zero; z1[p] = true; z2[p] = true; }
+        CUSR_FOR_P {
+            o[p] = (l[p] > rv[p]) ? one : zero;
+            d1[p] = zero;
+            d2[p] = zero;
+            m1[p] = m2[p] = __builtin_amdgcn_ballot_w64(true);
+        }
         break;
     case OP_LE:
-        CUSR_FOR_P { o[p] = (l[p] <= rv[p]) ? one : zero; d1[p] = zero; d2[p] = zero; z1[p] = true; z2[p] = true; }
+        CUSR_FOR_P {
+            o[p] = (l[p] <= rv[p]) ? one : zero;
+            d1[p] = zero;
+            d2[p] = zero;
+            m1[p] = m2[p] = __builtin_amdgcn_ballot_w64(true);
+        }
         break;
     case OP_GE:
-        CUSR_FOR_P { o[p] = (l[p] >= rv[p]) ? one : zero; d1[p] = zero; d2[p] = zero; z1[p] = true; z2[p] = true; }
+        CUSR_FOR_P {
+            o[p] = (l[p] >= rv[p]) ? one : zero;
+            d1[p] = zero;
+            d2[p] = zero;
+            m1[p] = m2[p] = __builtin_amdgcn_ballot_w64(true);
+        }
         break;
     default: CUSR_FOR_P { o[p] = zero; d1[p] = zero; d2[p] = zero; } break;
     }
@@ -613,7 +635,7 @@ __device__ __forceinline__ void scale_entries(R *T, const R *d, const uint64_t *
 
 // T[p*K + j] *= d[p] for j in [lo, hi); with sel, zero where z[p] instead.
 template <int K, typename R, int P>
-__device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, const bool *z,
+__device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, const uint64_t *zm,
                                             bool sel) {
     uint32_t mask;
     if constexpr (K < 32) {
@@ -625,8 +647,6 @@ __device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, co
     // transfer) and its per-entry test only on the flat-branch operators'
     // steps (C2 -3.5 %, C4 -3.3 %)
     if (sel) {
-        uint64_t zm[P];
-        CUSR_FOR_P zm[p] = __builtin_amdgcn_ballot_w64(z[p]);
         scale_entries<K, 0, R, P>(T, d, zm, mask, 1u);
     } else {
         plain_entries<K, 0, R, P>(T, d, mask);
@@ -692,7 +712,7 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
         const int fid = F::fid(ins);
         const int ak = F::akind(ins), ai = F::aidx(ins);
         R a[P], b[P], o[P], d1[P], d2[P];
-        bool z1[P], z2[P];
+        uint64_t z1[P], z2[P];
         const bool bin = F::binary(ins);
         // the right operand first: the accumulator is then dead once the left
         // one is fetched, and the left operand can share its registers
