@@ -101,26 +101,45 @@ typedef const __attribute__((address_space(4))) uint64_t *ProgPtr;
 
 // The two program formats of program.h, read by the same interpreter: one
 // 64-bit word per instruction for the fast kernels, two for the general one.
+// The word's halves ride beside it as opaque copies: the compiler then tests
+// a flag above bit 31 with one 32-bit bit test (on the 64-bit word it folds
+// the same test into a mask and a 64-bit compare), and the operator's arity
+// is tested twice, before the operand fetch and at the operator, each a bit
+// test and a branch of its own (one flag kept live between them became a
+// 64-bit lane mask, set and tested against exec at each use).
+struct FastWord {
+    uint64_t w;
+    uint32_t l;   // low half, for the second arity test
+    uint32_t h;   // w >> 32
+};
 struct FastFmt {
-    typedef uint64_t W;
-    static __device__ __forceinline__ W load(ProgPtr p, int pc) { return p[pc]; }
-    static __device__ __forceinline__ int fid(W w) { return ins_fid(w); }
-    static __device__ __forceinline__ int binary(W w) { return ins_binary(w); }
-    static __device__ __forceinline__ int akind(W w) { return ins_akind(w); }
-    static __device__ __forceinline__ int aidx(W w) { return ins_aidx(w); }
-    static __device__ __forceinline__ int bkind(W w) { return ins_bkind(w); }
-    static __device__ __forceinline__ int bidx(W w) { return ins_bidx(w); }
-    static __device__ __forceinline__ int toslot(W w) { return ins_toslot(w); }
-    static __device__ __forceinline__ int didx(W w) { return ins_didx(w); }
-    static __device__ __forceinline__ int lo(W w) { return ins_lo(w); }
-    static __device__ __forceinline__ int mid(W w) { return ins_mid(w); }
-    static __device__ __forceinline__ int hi(W w) { return ins_hi(w); }
-    static __device__ __forceinline__ int tape(W w) { return ins_tape(w); }
-    static __device__ __forceinline__ int sel(W w) { return ins_sel(w); }
-    static __device__ __forceinline__ int scale_a(W w) { return ins_scale_a(w); }
-    static __device__ __forceinline__ int scale_b(W w) { return ins_scale_b(w); }
-    static __device__ __forceinline__ int tape_a(W w) { return ins_tape_a(w); }
-    static __device__ __forceinline__ int tape_b(W w) { return ins_tape_b(w); }
+    typedef FastWord W;
+    static __device__ __forceinline__ W load(ProgPtr p, int pc) {
+        W r;
+        r.w = p[pc];
+        r.l = (uint32_t)r.w;
+        r.h = (uint32_t)(r.w >> 32);
+        __asm__("" : "+s"(r.l), "+s"(r.h));
+        return r;
+    }
+    static __device__ __forceinline__ int binary_op(W w) { return (int)((w.l >> 6) & 1u); }
+    static __device__ __forceinline__ int fid(W w) { return ins_fid(w.w); }
+    static __device__ __forceinline__ int binary(W w) { return ins_binary(w.w); }
+    static __device__ __forceinline__ int akind(W w) { return ins_akind(w.w); }
+    static __device__ __forceinline__ int aidx(W w) { return ins_aidx(w.w); }
+    static __device__ __forceinline__ int bkind(W w) { return ins_bkind(w.w); }
+    static __device__ __forceinline__ int bidx(W w) { return ins_bidx(w.w); }
+    static __device__ __forceinline__ int toslot(W w) { return ins_toslot(w.w); }
+    static __device__ __forceinline__ int didx(W w) { return ins_didx(w.w); }
+    static __device__ __forceinline__ int lo(W w) { return ins_lo(w.w); }
+    static __device__ __forceinline__ int mid(W w) { return ins_mid(w.w); }
+    static __device__ __forceinline__ int hi(W w) { return (int)((w.h >> 2) & 31u); }
+    static __device__ __forceinline__ int tape(W w) { return (int)((w.h >> 7) & 255u); }
+    static __device__ __forceinline__ int sel(W w) { return (int)((w.h >> 15) & 1u); }
+    static __device__ __forceinline__ int scale_a(W w) { return (int)((w.h >> 16) & 1u); }
+    static __device__ __forceinline__ int scale_b(W w) { return (int)((w.h >> 17) & 1u); }
+    static __device__ __forceinline__ int tape_a(W w) { return (int)((w.h >> 18) & 1u); }
+    static __device__ __forceinline__ int tape_b(W w) { return (int)((w.h >> 19) & 1u); }
 };
 struct WideFmt {
     typedef Wide W;
@@ -132,6 +151,7 @@ struct WideFmt {
     }
     static __device__ __forceinline__ int fid(W w) { return wins_fid(w.a); }
     static __device__ __forceinline__ int binary(W w) { return wins_binary(w.a); }
+    static __device__ __forceinline__ int binary_op(W w) { return wins_binary(w.a); }
     static __device__ __forceinline__ int akind(W w) { return wins_akind(w.a); }
     static __device__ __forceinline__ int aidx(W w) { return wins_aidx(w.a); }
     static __device__ __forceinline__ int bkind(W w) { return wins_bkind(w.a); }
@@ -713,14 +733,17 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
         const int ak = F::akind(ins), ai = F::aidx(ins);
         R a[P], b[P], o[P], d1[P], d2[P];
         uint64_t z1[P], z2[P];
-        const bool bin = F::binary(ins);
         // the right operand first: the accumulator is then dead once the left
         // one is fetched, and the left operand can share its registers
-        if (bin) fetch<R, P>(F::bkind(ins), F::bidx(ins), acc, w, cs, lane, b);
+        if (F::binary(ins)) fetch<R, P>(F::bkind(ins), F::bidx(ins), acc, w, cs, lane, b);
         fetch<R, P>(ak, ai, acc, w, cs, lane, a);
         const int lo = F::lo(ins), mid = F::mid(ins), hi = F::hi(ins);
-        if (bin) {
-            binary_p<R, P, JAC != 1>(fid, a, b, JAC == 2 || mid < hi, o, d1, d2, z1, z2);
+        if (F::binary_op(ins)) {
+            // POW's log(l) only where its right partial is read: the tape, or a
+            // scaled right range (the decoder sets scale_b exactly where
+            // hi > mid and the partial is not unit)
+            binary_p<R, P, JAC != 1>(fid, a, b, JAC == 2 || (JAC == 1 && F::scale_b(ins)), o, d1,
+                                     d2, z1, z2);
             if constexpr (JAC == 2) {
                 const int t = F::tape(ins), ta = F::tape_a(ins);
                 if (ta) CUSR_FOR_P lds_at<R, P>(w.tape, t, p, lane) = d1[p];

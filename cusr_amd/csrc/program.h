@@ -90,13 +90,16 @@ static inline __host__ __device__ int ins_toslot(uint64_t w) { return (int)((w >
 static inline __host__ __device__ int ins_didx(uint64_t w) { return (int)((w >> 20) & 15u); }
 static inline __host__ __device__ int ins_lo(uint64_t w) { return (int)((w >> 24) & 31u); }
 static inline __host__ __device__ int ins_mid(uint64_t w) { return (int)((w >> 29) & 31u); }
-static inline __host__ __device__ int ins_hi(uint64_t w) { return (int)((w >> 34) & 31u); }
-static inline __host__ __device__ int ins_tape(uint64_t w) { return (int)((w >> 39) & 255u); }
-static inline __host__ __device__ int ins_sel(uint64_t w) { return (int)((w >> 47) & 1u); }
-static inline __host__ __device__ int ins_scale_a(uint64_t w) { return (int)((w >> 48) & 1u); }
-static inline __host__ __device__ int ins_scale_b(uint64_t w) { return (int)((w >> 49) & 1u); }
-static inline __host__ __device__ int ins_tape_a(uint64_t w) { return (int)((w >> 50) & 1u); }
-static inline __host__ __device__ int ins_tape_b(uint64_t w) { return (int)((w >> 51) & 1u); }
+// fields above bit 31 are read from the high half alone: a 64-bit mask test
+// costs the device an extra scalar compare per field
+static inline __host__ __device__ uint32_t ins_w1(uint64_t w) { return (uint32_t)(w >> 32); }
+static inline __host__ __device__ int ins_hi(uint64_t w) { return (int)((ins_w1(w) >> 2) & 31u); }
+static inline __host__ __device__ int ins_tape(uint64_t w) { return (int)((ins_w1(w) >> 7) & 255u); }
+static inline __host__ __device__ int ins_sel(uint64_t w) { return (int)((ins_w1(w) >> 15) & 1u); }
+static inline __host__ __device__ int ins_scale_a(uint64_t w) { return (int)((ins_w1(w) >> 16) & 1u); }
+static inline __host__ __device__ int ins_scale_b(uint64_t w) { return (int)((ins_w1(w) >> 17) & 1u); }
+static inline __host__ __device__ int ins_tape_a(uint64_t w) { return (int)((ins_w1(w) >> 18) & 1u); }
+static inline __host__ __device__ int ins_tape_b(uint64_t w) { return (int)((ins_w1(w) >> 19) & 1u); }
 
 // wide-format fields (word 0 a, word 1 b)
 struct Wide {
@@ -110,11 +113,11 @@ static inline __host__ __device__ int wins_bkind(uint64_t a) { return (int)((a >
 static inline __host__ __device__ int wins_bidx(uint64_t a) { return (int)((a >> 19) & 255u); }
 static inline __host__ __device__ int wins_toslot(uint64_t a) { return (int)((a >> 27) & 1u); }
 static inline __host__ __device__ int wins_didx(uint64_t a) { return (int)((a >> 28) & 255u); }
-static inline __host__ __device__ int wins_sel(uint64_t a) { return (int)((a >> 36) & 1u); }
-static inline __host__ __device__ int wins_scale_a(uint64_t a) { return (int)((a >> 37) & 1u); }
-static inline __host__ __device__ int wins_scale_b(uint64_t a) { return (int)((a >> 38) & 1u); }
-static inline __host__ __device__ int wins_tape_a(uint64_t a) { return (int)((a >> 39) & 1u); }
-static inline __host__ __device__ int wins_tape_b(uint64_t a) { return (int)((a >> 40) & 1u); }
+static inline __host__ __device__ int wins_sel(uint64_t a) { return (int)((ins_w1(a) >> 4) & 1u); }
+static inline __host__ __device__ int wins_scale_a(uint64_t a) { return (int)((ins_w1(a) >> 5) & 1u); }
+static inline __host__ __device__ int wins_scale_b(uint64_t a) { return (int)((ins_w1(a) >> 6) & 1u); }
+static inline __host__ __device__ int wins_tape_a(uint64_t a) { return (int)((ins_w1(a) >> 7) & 1u); }
+static inline __host__ __device__ int wins_tape_b(uint64_t a) { return (int)((ins_w1(a) >> 8) & 1u); }
 static inline __host__ __device__ int wins_lo(uint64_t b) { return (int)(b & 255u); }
 static inline __host__ __device__ int wins_mid(uint64_t b) { return (int)((b >> 8) & 255u); }
 static inline __host__ __device__ int wins_hi(uint64_t b) { return (int)((b >> 16) & 255u); }
