@@ -669,7 +669,11 @@ __device__ __forceinline__ void scale_range(R *T, int lo, int hi, const R *d, co
     if (sel) {
         scale_entries<K, 0, R, P>(T, d, zm, mask, 1u);
     } else {
-        plain_entries<K, 0, R, P>(T, d, mask);
+        // an opaque copy: both paths open with the same group test, which the
+        // compiler otherwise forms once above the branch as a 64-bit lane mask
+        uint32_t m = mask;
+        __asm__("" : "+s"(m));
+        plain_entries<K, 0, R, P>(T, d, m);
     }
 }
 
@@ -737,7 +741,6 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
         // one is fetched, and the left operand can share its registers
         if (F::binary(ins)) fetch<R, P>(F::bkind(ins), F::bidx(ins), acc, w, cs, lane, b);
         fetch<R, P>(ak, ai, acc, w, cs, lane, a);
-        const int lo = F::lo(ins), mid = F::mid(ins), hi = F::hi(ins);
         if (F::binary_op(ins)) {
             // POW's log(l) only where its right partial is read: the tape, or a
             // scaled right range (the decoder sets scale_b exactly where
@@ -762,9 +765,13 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
             // sets scale_a / scale_b only where a partial is not exactly 1
             // (not for ADD, SUB's left operand or the identity) and the
             // range is non-empty, and sel for the flat-branch operators
-            const bool sel = F::sel(ins);
-            if (F::scale_a(ins)) scale_range<K, R, P>(T, lo, mid, d1, z1, sel);
-            if (F::scale_b(ins)) scale_range<K, R, P>(T, mid, hi, d2, z2, sel);
+            // the fields are read at each site: formed once before both, they
+            // were computed on every step and the select flag was kept live
+            // as a 64-bit lane mask
+            if (F::scale_a(ins))
+                scale_range<K, R, P>(T, F::lo(ins), F::mid(ins), d1, z1, F::sel(ins));
+            if (F::scale_b(ins))
+                scale_range<K, R, P>(T, F::mid(ins), F::hi(ins), d2, z2, F::sel(ins));
         }
         // the decoder spills a value only when its sibling subtree runs next,
         // and that subtree's first instruction reads leaves only: the old
