@@ -712,15 +712,18 @@ __device__ __forceinline__ void add_tangent(R *T, int k, const R *v) {
 template <typename R, int P>
 __device__ __forceinline__ void fetch(int kind, int idx, const R *acc, const WaveLds<R, P> &w,
                                       const double *cs, int lane, R *out) {
+    // the running value first (one test), then bit 0 of the kind: a variable
+    // or a spilled value, one per-lane LDS read from the row's base chosen
+    // by bit 1 without a branch; else a constant. Bit tests, unlike equality
+    // tests, are not merged into a balanced compare tree.
     if (kind == OPD_ACC) {
         CUSR_FOR_P out[p] = acc[p];
-    } else if (kind == OPD_VAR) {
-        CUSR_FOR_P out[p] = lds_at<R, P>(w.x, idx, p, lane);
-    } else if (kind == OPD_CONST) {
+    } else if (kind & 1) {
+        R *base = (kind & 2) ? w.slot : w.x;
+        CUSR_FOR_P out[p] = lds_at<R, P>(base, idx, p, lane);
+    } else {
         const R c = (R)cs[idx];
         CUSR_FOR_P out[p] = c;
-    } else {
-        CUSR_FOR_P out[p] = lds_at<R, P>(w.slot, idx, p, lane);
     }
 }
 
