@@ -142,6 +142,7 @@ struct Ctx {
     void *static_scratch = nullptr;   // this device's address of `scratch`
     HostBuf<uint64_t> h_prog;
     HostBuf<ExprDesc> h_desc;
+    HostBuf<char> h_stage;   // page-locked copies of small host inputs (upload_data)
     std::vector<double> h_c, h_li, h_lf, h_c0;   // co_optimize: fp64 results, c_init
     std::vector<float> h_li32, h_lf32;
 };
@@ -253,12 +254,18 @@ int grow_buffers(Ctx *ctx, const PopHeader *h, size_t words, bool in32, bool on_
     const size_t nX = on_data ? 0 : (size_t)N * D;
     const size_t nY = on_data ? 0 : shared_y ? (size_t)N : (size_t)M * N;
     const size_t esz = in32 ? 4 : 8;
-    CO_GROW(ctx->prog, sizeof(uint64_t) * words);
+    // the program words and constants vary from population to population: a
+    // quarter of headroom, so a slightly larger next population (a GP
+    // round's) does not free and allocate again (about 1 ms of a C5 round
+    // when it did)
+    if (sizeof(uint64_t) * words > ctx->prog.cap)
+        CO_GROW(ctx->prog, sizeof(uint64_t) * (words + words / 4));
     CO_GROW(ctx->desc, sizeof(ExprDesc) * M);
     CO_GROW(ctx->X, sizeof(double) * nX);
     CO_GROW(ctx->Y, sizeof(double) * nY);
-    CO_GROW(ctx->C0, sizeof(double) * C);
-    CO_GROW(ctx->C, sizeof(double) * C);
+    const size_t Ch = (size_t)C + (size_t)C / 4;
+    if (sizeof(double) * C > ctx->C0.cap) CO_GROW(ctx->C0, sizeof(double) * Ch);
+    if (sizeof(double) * C > ctx->C.cap) CO_GROW(ctx->C, sizeof(double) * Ch);
     CO_GROW(ctx->status, sizeof(int32_t) * M);
     CO_GROW(ctx->li, sizeof(double) * M);
     CO_GROW(ctx->lf, sizeof(double) * M);
@@ -266,18 +273,37 @@ int grow_buffers(Ctx *ctx, const PopHeader *h, size_t words, bool in32, bool on_
     size_t stage = esz * nX;
     if (in32 && esz * nY > stage) stage = esz * nY;
     if (in32 && esz * C > stage) stage = esz * C;
-    CO_GROW(ctx->stage, stage);
+    if (stage > ctx->stage.cap) CO_GROW(ctx->stage, stage + stage / 4);
     return CO_OK;
 }
 
 // Queue the copies of the data (X, y) and c_init on stream s (fp32 host
 // inputs are widened on the device). With on_data only c_init goes over.
+// Host inputs up to this many bytes in all are first copied into page-locked
+// staging, so their copies to the device run as DMA without holding the host
+// (from pageable memory the runtime stages each copy itself, and the host
+// waits: C5, 1.1 MB of constants per round, 0.85 ms before the first range's
+// decode could start). Larger inputs (a target per expression) go directly.
+constexpr size_t kPinnedStageMax = 16u << 20;
+
 int upload_data(Ctx *ctx, const PopHeader *h, const void *c, const void *xs, const void *ym,
                 bool in32, bool on_data, bool shared_y, hipStream_t s) {
     const int M = h->M_prob, N = h->N, D = h->n_vars, C = h->total_c;
     const size_t nX = on_data ? 0 : (size_t)N * D;
     const size_t nY = on_data ? 0 : shared_y ? (size_t)N : (size_t)M * N;
     const size_t esz = in32 ? 4 : 8;
+    const auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t bX = esz * nX, bY = esz * nY, bC = ctx->dev_io ? 0 : esz * (size_t)C;
+    if (bX + bY + bC > 0 && up(bX) + up(bY) + up(bC) <= kPinnedStageMax) {
+        // the previous call's copies from the staging have finished before
+        // it is written again
+        CO_HIP(hipStreamSynchronize(s));
+        CO_GROW_HOST(ctx->h_stage, up(bX) + up(bY) + up(bC));
+        char *q = ctx->h_stage.data();
+        if (bX) { memcpy(q, xs, bX); xs = q; q += up(bX); }
+        if (bY) { memcpy(q, ym, bY); ym = q; q += up(bY); }
+        if (bC) { memcpy(q, c, bC); c = q; }
+    }
     // xs: row-major host array -> column-major fp64 on the device
     if (nX) {
         CO_HIP(hipMemcpyAsync(ctx->stage.p, xs, esz * nX, hipMemcpyHostToDevice, s));
@@ -798,14 +824,24 @@ int fit_pipelined(Ctx *ctx, const CoOptions &opt, const PopHeader *h, const int3
     pl.total_nodes = h->total_nodes;
     pl.total_c = h->total_c;
     FitRun fr;
+#ifdef CUSR_EXP_TIMING
+    const double u0 = now_ms();
+#endif
     rc = fr.begin(ctx, opt);
     if (rc != CO_OK) return rc;
     const hipStream_t cs = ctx->copy_stream;
+#ifdef CUSR_EXP_TIMING
+    const double u1 = now_ms();
+#endif
     rc = upload_data(ctx, h, c, xs, ym, in32, on_data, shared_y, cs);
     if (rc != CO_OK) {
         (void)hipStreamSynchronize(cs);
         return rc;
     }
+#ifdef CUSR_EXP_TIMING
+    fprintf(stderr, "[pipe] checks+grow %.2f begin %.2f upload %.2f ms\n", u0 - t0, u1 - u0,
+            now_ms() - u1);
+#endif
     ctx->ranges.assign(1, 0);
     int64_t wb = 0;
     for (int j = 0; j < nr; ++j) {
@@ -1341,6 +1377,7 @@ extern "C" void co_teardown(void *handle) {
         if (b->p) (void)hipFree(b->p);
     if (ctx->h_prog.p) (void)hipHostFree(ctx->h_prog.p);
     if (ctx->h_desc.p) (void)hipHostFree(ctx->h_desc.p);
+    if (ctx->h_stage.p) (void)hipHostFree(ctx->h_stage.p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     if (ctx->copy_stream) (void)hipStreamDestroy(ctx->copy_stream);
     for (int i = 0; i < kExtraStreams; ++i) {
