@@ -143,6 +143,7 @@ struct Ctx {
     HostBuf<uint64_t> h_prog;
     HostBuf<ExprDesc> h_desc;
     HostBuf<char> h_stage;   // page-locked copies of small host inputs (upload_data)
+    HostBuf<char> h_back;    // page-locked landing of small results (FitRun::finish)
     std::vector<double> h_c, h_li, h_lf, h_c0;   // co_optimize: fp64 results, c_init
     std::vector<float> h_li32, h_lf32;
 };
@@ -704,12 +705,40 @@ struct FitRun {
         CO_LAUNCH_HIP(hipEventRecord(ctx->ev_t1, s));
         // co_optimize_data_device: the outputs are device memory of the caller
         const hipMemcpyKind k = ctx->dev_io ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
-        if (c_out && C) CO_HIP(hipMemcpyAsync(c_out, ctx->C.p, 8 * (size_t)C, k, s));
-        if (status_out) CO_HIP(hipMemcpyAsync(status_out, ctx->status.p, 4 * (size_t)M, k, s));
-        if (li_out) CO_HIP(hipMemcpyAsync(li_out, ctx->li.p, 8 * (size_t)M, k, s));
-        if (lf_out) CO_HIP(hipMemcpyAsync(lf_out, ctx->lf.p, 8 * (size_t)M, k, s));
-        if (iters_out) CO_HIP(hipMemcpyAsync(iters_out, ctx->iters.p, 4 * (size_t)M, k, s));
-        CO_HIP(hipStreamSynchronize(s));
+        struct Out {
+            void *dst;
+            const void *src;
+            size_t bytes;
+        } outs[5] = {{c_out, ctx->C.p, c_out ? 8 * (size_t)C : 0},
+                     {status_out, ctx->status.p, status_out ? 4 * (size_t)M : 0},
+                     {li_out, ctx->li.p, li_out ? 8 * (size_t)M : 0},
+                     {lf_out, ctx->lf.p, lf_out ? 8 * (size_t)M : 0},
+                     {iters_out, ctx->iters.p, iters_out ? 4 * (size_t)M : 0}};
+        const auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+        size_t total = 0;
+        for (const Out &o : outs) total += up(o.bytes);
+        if (!ctx->dev_io && total > 0 && total <= kPinnedStageMax) {
+            // small results land in page-locked memory (DMA) and are copied
+            // out on the host, as small inputs go in (upload_data)
+            CO_GROW_HOST(ctx->h_back, total);
+            size_t off = 0;
+            for (const Out &o : outs) {
+                if (o.bytes)
+                    CO_HIP(hipMemcpyAsync(ctx->h_back.data() + off, o.src, o.bytes,
+                                          hipMemcpyDeviceToHost, s));
+                off += up(o.bytes);
+            }
+            CO_HIP(hipStreamSynchronize(s));
+            off = 0;
+            for (const Out &o : outs) {
+                if (o.bytes) memcpy(o.dst, ctx->h_back.data() + off, o.bytes);
+                off += up(o.bytes);
+            }
+        } else {
+            for (const Out &o : outs)
+                if (o.bytes) CO_HIP(hipMemcpyAsync(o.dst, o.src, o.bytes, k, s));
+            CO_HIP(hipStreamSynchronize(s));
+        }
         float ms = 0.0f;
         CO_HIP(hipEventElapsedTime(&ms, ctx->ev_t0, ctx->ev_t1));
         ctx->last_kernel_ms = ms;
@@ -1378,6 +1407,7 @@ extern "C" void co_teardown(void *handle) {
     if (ctx->h_prog.p) (void)hipHostFree(ctx->h_prog.p);
     if (ctx->h_desc.p) (void)hipHostFree(ctx->h_desc.p);
     if (ctx->h_stage.p) (void)hipHostFree(ctx->h_stage.p);
+    if (ctx->h_back.p) (void)hipHostFree(ctx->h_back.p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     if (ctx->copy_stream) (void)hipStreamDestroy(ctx->copy_stream);
     for (int i = 0; i < kExtraStreams; ++i) {
