@@ -114,6 +114,7 @@ struct FastWord {
 };
 struct FastFmt {
     typedef FastWord W;
+    static constexpr int kWords = 1;   // program words per instruction
     static __device__ __forceinline__ W load(ProgPtr p, int pc) {
         W r;
         r.w = p[pc];
@@ -143,6 +144,7 @@ struct FastFmt {
 };
 struct WideFmt {
     typedef Wide W;
+    static constexpr int kWords = 2;
     static __device__ __forceinline__ W load(ProgPtr p, int pc) {
         W w;
         w.a = p[2 * pc];
@@ -734,8 +736,11 @@ __device__ __forceinline__ void fetch(int kind, int idx, const R *acc, const Wav
 template <int K, typename R, int P, int JAC, typename F = FastFmt>
 __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<R, P> &w,
                                              const double *cs, int lane, R *acc, R *T) {
-    for (int pc = 0; pc < n; ++pc) {
-        const typename F::W ins = F::load(prog, pc);
+    // the word's address advances by one increment and the loop ends on it,
+    // instead of forming the address from a counter at every step
+    const ProgPtr end = prog + F::kWords * n;
+    for (ProgPtr q = prog; q != end; q += F::kWords) {
+        const typename F::W ins = F::load(q, 0);
         const int fid = F::fid(ins);
         const int ak = F::akind(ins), ai = F::aidx(ins);
         R a[P], b[P], o[P], d1[P], d2[P];
