@@ -293,6 +293,17 @@ def launch_bins(pop):
     return np.where(route != 0, co_inproc.CO_GENERAL_BIN, K)
 
 
+def dominant_bin(args, bins, bin_of):
+    """The bin whose launch alone the roofline measures: the longest beside the
+    others, or the one --roofline-bin names (refused when no expression is in it)."""
+    if args.roofline_bin is None:
+        return int(np.argmax(bins))
+    k = int(args.roofline_bin)
+    if not 0 <= k < len(bins) or not np.any(bin_of == k):
+        sys.exit(f"bench.py: --roofline-bin {k}: no expression of this workload is in that bin")
+    return k
+
+
 def kernel_name(cfg, pop, k, parts=0):
     """Kernel name (as rocprofv3 shows it, without the last template
     arguments) of bin k's fit with `parts` point partitions (0: the default
@@ -381,7 +392,7 @@ def run_resident(args, cfg, co, pop):
     kms = float(np.mean(fit_ms))
     bins = np.mean(np.asarray(bin_ms), axis=0)
     bin_of = launch_bins(pop)
-    kdom = int(np.argmax(bins))
+    kdom = dominant_bin(args, bins, bin_of)
 
     def fit_alone(sub):
         co.upload(sub)
@@ -437,7 +448,7 @@ def run_rounds(args, cfg, co, gen):
     value = fits / (sum(lat) / 1e3)
     pop, res, bins = last
     bin_of = launch_bins(pop)
-    kdom = int(np.argmax(bins))
+    kdom = dominant_bin(args, bins, bin_of)
 
     def fit_alone(sub):
         co.optimize_ex(sub, cfg.max_iter, ad_mode=cfg.ad_mode, precision=cfg.precision)
@@ -525,6 +536,10 @@ def main():
                     help="also run one copy kernel of known size (for rocprofv3 --pmc scaling)")
     ap.add_argument("--alone-reps", type=int, default=3,
                     help="launches of the dominant bin alone (the roofline's duration)")
+    ap.add_argument("--roofline-bin", type=int, default=None,
+                    help="the bin whose launch alone the roofline measures (default: the "
+                         "longest beside the others; counter runs fix it, since under the "
+                         "profiler the bins' concurrent times reorder)")
     ap.add_argument("--configs", default=None,
                     help="comma-separated configurations measured briefly after the main "
                          "one (default: C3,C4,C5 when --config is C2; '' for none)")

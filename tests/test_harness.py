@@ -155,3 +155,18 @@ def test_bench_host_description_and_launch_bins():
     gen = b == ci.CO_GENERAL_BIN
     assert gen.any() and (~gen).any()
     assert np.array_equal(b[~gen], K[~gen]) and np.all(K[gen] > ci.CO_FAST_MAX_K)
+
+
+def test_bench_roofline_bin_choice():
+    """The roofline's bin: the longest beside the others by default, the one
+    --roofline-bin names when an expression is in it, and a clear exit otherwise."""
+    import argparse
+    import bench
+    bins = np.array([0.0, 1.0, 3.0, 2.0])
+    bin_of = np.array([1, 2, 2, 3])
+    free = argparse.Namespace(roofline_bin=None)
+    assert bench.dominant_bin(free, bins, bin_of) == 2
+    assert bench.dominant_bin(argparse.Namespace(roofline_bin=3), bins, bin_of) == 3
+    for k in (0, 4, -1):
+        with pytest.raises(SystemExit, match="roofline-bin"):
+            bench.dominant_bin(argparse.Namespace(roofline_bin=k), bins, bin_of)
