@@ -101,15 +101,12 @@ typedef const __attribute__((address_space(4))) uint64_t *ProgPtr;
 
 // The two program formats of program.h, read by the same interpreter: one
 // 64-bit word per instruction for the fast kernels, two for the general one.
-// The word's halves ride beside it as opaque copies: the compiler then tests
-// a flag above bit 31 with one 32-bit bit test (on the 64-bit word it folds
-// the same test into a mask and a 64-bit compare), and the operator's arity
-// is tested twice, before the operand fetch and at the operator, each a bit
-// test and a branch of its own (one flag kept live between them became a
-// 64-bit lane mask, set and tested against exec at each use).
+// The word's high half rides beside it as an opaque copy: the compiler then
+// tests a flag above bit 31 with one 32-bit bit test (on the 64-bit word it
+// folds the same test into a mask and a 64-bit compare). The operator's arity
+// is tested once per step, and each arm fetches its own operands.
 struct FastWord {
     uint64_t w;
-    uint32_t l;   // low half, for the second arity test
     uint32_t h;   // w >> 32
 };
 struct FastFmt {
@@ -118,12 +115,10 @@ struct FastFmt {
     static __device__ __forceinline__ W load(ProgPtr p, int pc) {
         W r;
         r.w = p[pc];
-        r.l = (uint32_t)r.w;
         r.h = (uint32_t)(r.w >> 32);
-        __asm__("" : "+s"(r.l), "+s"(r.h));
+        __asm__("" : "+s"(r.h));
         return r;
     }
-    static __device__ __forceinline__ int binary_op(W w) { return (int)((w.l >> 6) & 1u); }
     static __device__ __forceinline__ int fid(W w) { return ins_fid(w.w); }
     static __device__ __forceinline__ int binary(W w) { return ins_binary(w.w); }
     static __device__ __forceinline__ int akind(W w) { return ins_akind(w.w); }
@@ -153,7 +148,6 @@ struct WideFmt {
     }
     static __device__ __forceinline__ int fid(W w) { return wins_fid(w.a); }
     static __device__ __forceinline__ int binary(W w) { return wins_binary(w.a); }
-    static __device__ __forceinline__ int binary_op(W w) { return wins_binary(w.a); }
     static __device__ __forceinline__ int akind(W w) { return wins_akind(w.a); }
     static __device__ __forceinline__ int aidx(W w) { return wins_aidx(w.a); }
     static __device__ __forceinline__ int bkind(W w) { return wins_bkind(w.a); }
@@ -745,11 +739,12 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
         const int ak = F::akind(ins), ai = F::aidx(ins);
         R a[P], b[P], o[P], d1[P], d2[P];
         uint64_t z1[P], z2[P];
-        // the right operand first: the accumulator is then dead once the left
-        // one is fetched, and the left operand can share its registers
-        if (F::binary(ins)) fetch<R, P>(F::bkind(ins), F::bidx(ins), acc, w, cs, lane, b);
-        fetch<R, P>(ak, ai, acc, w, cs, lane, a);
-        if (F::binary_op(ins)) {
+        // one arity test per step; a binary step fetches the right operand
+        // first: the accumulator is then dead once the left one is fetched,
+        // and the left operand can share its registers
+        if (F::binary(ins)) {
+            fetch<R, P>(F::bkind(ins), F::bidx(ins), acc, w, cs, lane, b);
+            fetch<R, P>(ak, ai, acc, w, cs, lane, a);
             // POW's log(l) only where its right partial is read: the tape, or a
             // scaled right range (the decoder sets scale_b exactly where
             // hi > mid and the partial is not unit)
@@ -761,6 +756,7 @@ __device__ __forceinline__ void forward_pass(ProgPtr prog, int n, const WaveLds<
                 if (F::tape_b(ins)) CUSR_FOR_P lds_at<R, P>(w.tape, t + ta, p, lane) = d2[p];
             }
         } else {
+            fetch<R, P>(ak, ai, acc, w, cs, lane, a);
             // d2 and z2 stay unset: the decoder never sets scale_b on a unary step
             unary_p<R, P, math_chunk<K, R, P, JAC>()>(fid, a, o, d1, z1);
             if constexpr (JAC == 2) {
